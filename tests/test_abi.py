@@ -1,0 +1,48 @@
+"""CPU checks of the C-ABI library: it loads, and exports exactly what include/*.h declares.
+
+No compute call is made here (this container has no GPU)."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+from vdn_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = []
+    for path in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(path).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\**\s*(vdn_[a-z0-9_]+)\s*\(", text, re.M)
+    return sorted(set(names))
+
+
+def test_header_declares_the_bound_signatures():
+    declared = declared_functions()
+    assert declared, "no declarations parsed from include/*.h"
+    assert sorted(_lib.exported_symbols()) == declared
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    if not os.path.exists(_lib.LIBRARY_PATH):
+        pytest.fail("libvdnmi.so is not built; run __graft_entry__.build()")
+    lib = _lib.load()
+    for name in declared_functions():
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
+    assert lib.vdn_abi_version() == 1
+    assert lib.vdn_last_error() is not None
+
+
+def test_invalid_arguments_are_rejected_without_a_device():
+    lib = _lib.load()
+    # Argument validation happens before any HIP call, so these run on a CPU-only host.
+    assert lib.vdn_mxfp8_quantize(None, 4, 0, 4, None, None, None, None) != 0
+    assert b"K > 0" in lib.vdn_last_error()
+    assert lib.vdn_mxfp8_gemm(None, None, 128, None, None, 128, 128, None, None, 1, 1, 1, 0,
+                              None, None) != 0
+    assert b"null pointer" in lib.vdn_last_error()

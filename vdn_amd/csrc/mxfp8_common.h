@@ -1,0 +1,46 @@
+// MXFP8 block-32 format helpers shared by the producer kernels and the GEMM.
+//
+// Format (reference src/models/ops/mxfp8_quant.py:15-74, mxfp8_kernels.py:15-27):
+//   * rows padded to RP = ceil(R/128)*128, K padded to KP = ceil(K/128)*128, padding is zero;
+//   * per row and per 32-element K block: one E8M0 scale byte and 32 E4M3FN codes;
+//   * scale bytes stored flat in the SWIZZLE_32_4_4 order, RP*KP/32 bytes.
+#pragma once
+
+#include "common.h"
+
+namespace vdn {
+
+// amax -> (E8M0 byte, 2^-e as fp32). Bit-level rule of the reference
+// (mxfp8_kernels.py:15-22, mxfp8_quant.py:65-70): e0 = biased_exp(amax) - 135,
+// bump by one when amax exceeds 1.75 * 2^(e0 + 8), clamp below at -127.
+__device__ __forceinline__ uint32_t e8m0_from_amax(float amax, float* inv_out) {
+  const int bits = __float_as_int(amax);
+  const int e0 = ((bits >> 23) & 255) - 135;
+  const float thr = __int_as_float(((e0 + 135) << 23) | 0x600000);
+  int e = e0 + (amax > thr ? 1 : 0);
+  e = e < -127 ? -127 : e;
+  *inv_out = __int_as_float((127 - e) << 23);
+  return static_cast<uint32_t>(e + 127);
+}
+
+// Byte offset of natural scale (row r, K-block c) in SWIZZLE_32_4_4 order
+// (mxfp8_kernels.py:25-27). `col_tiles` = KP / 128.
+__device__ __forceinline__ int64_t swizzled_scale_offset(int64_t r, int64_t c, int64_t col_tiles) {
+  const int64_t tile = (r >> 7) * col_tiles + (c >> 2);
+  return tile * 512 + (r & 31) * 16 + ((r & 127) >> 5) * 4 + (c & 3);
+}
+
+// Eight fp32 values (already multiplied by 2^-e) -> eight E4M3FN codes, RNE.
+__device__ __forceinline__ u32x2 e4m3x8(const float* v) {
+  int lo = 0, hi = 0;
+  lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], lo, false);
+  lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], lo, true);
+  hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4], v[5], hi, false);
+  hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6], v[7], hi, true);
+  u32x2 out;
+  out[0] = static_cast<uint32_t>(lo);
+  out[1] = static_cast<uint32_t>(hi);
+  return out;
+}
+
+}  // namespace vdn

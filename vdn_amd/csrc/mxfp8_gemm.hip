@@ -1,0 +1,279 @@
+// Block-scaled MXFP8 GEMM for gfx950:  C[m, n] = sum_k A[m, k] * W[n, k]  (both K-major),
+// E4M3FN codes with one E8M0 scale per 32 K values, fp32 accumulation, bf16 output.
+//
+// Replaces the reference's F.scaled_mm(BlockWise1x32, SWIZZLE_32_4_4) call in
+// MXFP8Linear.forward_quantized (src/models/ops/mxfp8_linear.py:61-93).
+//
+// Design:
+//   * one workgroup computes a BM x BN tile; its waves form a WGM x WGN grid and each
+//     wave owns a (BM/WGM) x (BN/WGN) sub-tile made of 16x16 outputs;
+//   * the inner product is v_mfma_scale_f32_16x16x128_f8f6f4. For 8-bit operands its K
+//     layout is split: lane l (group g = l / 16) holds row (l % 16), K [16g, 16g+16) in
+//     bytes 0-15 and K [64+16g, 64+16g+16) in bytes 16-31, and the E8M0 byte of lane l
+//     scales K-block g (K [32g, 32g+32)) of row l % 16 (measured on gfx950);
+//   * A and W tiles (128 K bytes per row) are streamed global -> LDS with
+//     global_load_lds_dwordx4 (no VGPR staging), double-buffered; each 16-byte chunk c of
+//     tile row r lives at chunk c ^ ((r >> 1) & 7) so the fragment reads of 16 consecutive
+//     rows touch 16 distinct 16-byte bank groups;
+//   * scale bytes are read straight from the caller's SWIZZLE_32_4_4 buffer: one dword
+//     holds a row's 4 K-blocks of one 128-K step, and each lane shifts its own block's
+//     byte into byte 0 (the instruction ignores OPSEL and always reads byte 0);
+//   * workgroup ids are remapped so consecutive tiles land on the same XCD (dispatch is
+//     round-robin over the 8 XCDs) and tiles are walked in GROUP_M-row groups, which keeps
+//     each XCD's L2 working set to a few A row-panels and W column-panels.
+#include "mxfp8_common.h"
+
+namespace vdn {
+namespace {
+
+constexpr int kBK = 128;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef const __attribute__((address_space(1))) void global_void_t;
+
+__device__ __forceinline__ void load_to_lds16(const void* src, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)lds_wave_base, 16, 0, 0);
+}
+
+// Offset of row r's scale dword for K step 0; K step ks adds 512 * ks.
+__device__ __forceinline__ uint32_t scale_row_offset(int64_t r, int64_t col_tiles) {
+  return static_cast<uint32_t>((r >> 7) * col_tiles * 512 + (r & 31) * 16 + ((r & 127) >> 5) * 4);
+}
+
+// `s_step` is wave-uniform (scale base + 512 * ks); the per-lane part is a 32-bit unsigned
+// offset, which lets the compiler use the SGPR-base + 32-bit VGPR-offset addressing form.
+__device__ __forceinline__ uint32_t scale_word(const uint8_t* __restrict__ s_step, uint32_t row_off) {
+  return *reinterpret_cast<const uint32_t*>(s_step + row_off);
+}
+
+enum Mode : int { kStore = 0, kAccumulate = 1 };
+
+template <int BM, int BN, int WGM, int WGN>
+__global__ void __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
+                  const uint8_t* __restrict__ W, const uint8_t* __restrict__ Ws, int64_t mp,
+                  int64_t np, int64_t kp, const uint16_t* __restrict__ bias,
+                  uint16_t* __restrict__ C, int64_t out_rows, int64_t n, int64_t ldc, int mode,
+                  uint32_t* __restrict__ nonfinite, int tiles_m, int tiles_n, int group_m) {
+  constexpr int kWaves = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int TM = WM / 16, TN = WN / 16;
+  constexpr int kASegs = BM / 8 / kWaves;  // 1 KB (8-row) segments per wave per K step
+  constexpr int kBSegs = BN / 8 / kWaves;
+  static_assert(kASegs * kWaves * 8 == BM && kBSegs * kWaves * 8 == BN, "tile/wave mismatch");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2][(BM + BN) * kBK];
+
+  // ---- tile selection: XCD-contiguous ids, then GROUP_M-row grouping ----
+  const int num_wg = tiles_m * tiles_n;
+  int pid = blockIdx.x;
+  {
+    const int xcd = pid & 7, local = pid >> 3;
+    const int per = num_wg >> 3, rem = num_wg & 7;
+    pid = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  }
+  const int in_group = group_m * tiles_n;
+  const int first_m = (pid / in_group) * group_m;
+  const int gm = min(tiles_m - first_m, group_m);
+  const int tm = first_m + (pid % in_group) % gm;
+  const int tn = (pid % in_group) / gm;
+  const int64_t m0 = static_cast<int64_t>(tm) * BM;
+  const int64_t n0 = static_cast<int64_t>(tn) * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int64_t col_tiles = kp >> 7;
+  const int nk = static_cast<int>(kp / kBK);
+
+  // ---- per-lane source offsets for the LDS-direct loads ----
+  // Segment g of a tile holds tile rows [8g, 8g+8); lane l writes 16 bytes at LDS offset
+  // 16 l of that segment, i.e. row 8g + l/8, physical chunk l%8, so it must fetch
+  // logical chunk (l%8) ^ ((row >> 1) & 7). Offsets are 32-bit and relative to the tile's
+  // first row (the host guarantees BM * kp < 2^31); rows past the padded end are clamped.
+  const uint8_t* a_tile = A + m0 * kp;
+  const uint8_t* w_tile = W + n0 * kp;
+  const int seg_row = lane >> 3;
+  // With an even wave count every segment a lane loads has the same (row >> 1) & 7.
+  static_assert(kWaves % 2 == 0, "chunk swizzle assumes an even wave count");
+  const uint32_t logical16 = ((lane & 7) ^ (((wave * 8 + seg_row) >> 1) & 7)) * 16;
+  const int a_last = static_cast<int>(min<int64_t>(BM, mp - m0)) - 1;
+  const int b_last = static_cast<int>(min<int64_t>(BN, np - n0)) - 1;
+  const uint32_t kpu = static_cast<uint32_t>(kp);
+  auto issue_loads = [&](int ks, int buf) {
+    const uint8_t* a_k = a_tile + static_cast<int64_t>(ks) * kBK;
+    const uint8_t* w_k = w_tile + static_cast<int64_t>(ks) * kBK;
+#pragma unroll
+    for (int i = 0; i < kASegs; ++i) {
+      const uint32_t row = min((i * kWaves + wave) * 8 + seg_row, a_last);
+      load_to_lds16(a_k + (row * kpu + logical16), &lds[buf][(i * kWaves + wave) * 1024]);
+    }
+#pragma unroll
+    for (int i = 0; i < kBSegs; ++i) {
+      const uint32_t row = min((i * kWaves + wave) * 8 + seg_row, b_last);
+      load_to_lds16(w_k + (row * kpu + logical16), &lds[buf][BM * kBK + (i * kWaves + wave) * 1024]);
+    }
+  };
+
+  // ---- scale offsets of this lane (32-bit: the host guarantees mp * kp / 32 < 2^31) ----
+  const int frag_row = lane & 15;
+  const int block_shift = 8 * (lane >> 4);
+  uint32_t a_soff[TM], b_soff[TN];
+#pragma unroll
+  for (int mt = 0; mt < TM; ++mt)
+    a_soff[mt] = scale_row_offset(min(m0 + wm * WM + mt * 16 + frag_row, mp - 1), col_tiles);
+#pragma unroll
+  for (int nt = 0; nt < TN; ++nt)
+    b_soff[nt] = scale_row_offset(min(n0 + wn * WN + nt * 16 + frag_row, np - 1), col_tiles);
+
+  uint32_t sa[TM], sb[TN];
+#pragma unroll
+  for (int mt = 0; mt < TM; ++mt) sa[mt] = scale_word(As, a_soff[mt]) >> block_shift;
+#pragma unroll
+  for (int nt = 0; nt < TN; ++nt) sb[nt] = scale_word(Ws, b_soff[nt]) >> block_shift;
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int mt = 0; mt < TM; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < TN; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  issue_loads(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  const int c_lo = lane >> 4;  // 16-byte chunks g and g + 4 of the 128-byte K step
+  for (int ks = 0; ks < nk; ++ks) {
+    const int buf = ks & 1;
+    const bool more = ks + 1 < nk;
+    // Scale words for the next step are issued before the tile prefetch and consumed only
+    // after the closing vmcnt(0): waiting on them earlier would also wait on the prefetch,
+    // since vector-memory counters retire in order.
+    uint32_t sa_next[TM], sb_next[TN];
+    if (more) {
+      const uint8_t* as_step = As + static_cast<int64_t>(ks + 1) * 512;
+      const uint8_t* ws_step = Ws + static_cast<int64_t>(ks + 1) * 512;
+#pragma unroll
+      for (int mt = 0; mt < TM; ++mt) sa_next[mt] = scale_word(as_step, a_soff[mt]);
+#pragma unroll
+      for (int nt = 0; nt < TN; ++nt) sb_next[nt] = scale_word(ws_step, b_soff[nt]);
+      issue_loads(ks + 1, buf ^ 1);
+    }
+    const uint8_t* abuf = lds[buf];
+    const uint8_t* bbuf = lds[buf] + BM * kBK;
+    i32x8 afrag[TM];
+#pragma unroll
+    for (int mt = 0; mt < TM; ++mt) {
+      const int row = wm * WM + mt * 16 + frag_row;
+      const int sw = (row >> 1) & 7;
+      const i32x4 lo = *reinterpret_cast<const i32x4*>(abuf + row * kBK + ((c_lo ^ sw) << 4));
+      const i32x4 hi = *reinterpret_cast<const i32x4*>(abuf + row * kBK + (((c_lo + 4) ^ sw) << 4));
+      afrag[mt] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+#pragma unroll
+    for (int nt = 0; nt < TN; ++nt) {
+      const int row = wn * WN + nt * 16 + frag_row;
+      const int sw = (row >> 1) & 7;
+      const i32x4 lo = *reinterpret_cast<const i32x4*>(bbuf + row * kBK + ((c_lo ^ sw) << 4));
+      const i32x4 hi = *reinterpret_cast<const i32x4*>(bbuf + row * kBK + (((c_lo + 4) ^ sw) << 4));
+      const i32x8 bfrag = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+      for (int mt = 0; mt < TM; ++mt) {
+        acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+            afrag[mt], bfrag, acc[mt][nt], 0, 0, 0, static_cast<int>(sa[mt]), 0,
+            static_cast<int>(sb[nt]));
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (more) {
+#pragma unroll
+      for (int mt = 0; mt < TM; ++mt) sa[mt] = sa_next[mt] >> block_shift;
+#pragma unroll
+      for (int nt = 0; nt < TN; ++nt) sb[nt] = sb_next[nt] >> block_shift;
+    }
+  }
+
+  // ---- epilogue: lane holds rows (lane/16)*4 + v of each 16x16 tile, column lane%16 ----
+  bool bad = false;
+#pragma unroll
+  for (int nt = 0; nt < TN; ++nt) {
+    const int64_t col = n0 + wn * WN + nt * 16 + frag_row;
+    if (col >= n) continue;
+    const float b = bias != nullptr ? bf16_bits_to_f32(bias[col]) : 0.f;
+#pragma unroll
+    for (int mt = 0; mt < TM; ++mt) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t row = m0 + wm * WM + mt * 16 + (lane >> 4) * 4 + v;
+        if (row >= out_rows) continue;
+        float y = round_bf16(acc[mt][nt][v]);
+        if (bias != nullptr) y = round_bf16(y + b);
+        uint16_t* dst = C + row * ldc + col;
+        if (mode == kAccumulate) y = round_bf16(bf16_bits_to_f32(*dst) + y);
+        bad = bad || !(fabsf(y) < INFINITY);
+        *dst = f32_to_bf16_bits(y);
+      }
+    }
+  }
+  if (nonfinite != nullptr && __ballot(bad) != 0 && lane == 0) atomicOr(nonfinite, 1u);
+}
+
+template <int BM, int BN, int WGM, int WGN>
+int launch_gemm(const uint8_t* a, const uint8_t* as, int64_t mp, const uint8_t* w,
+                const uint8_t* ws, int64_t np, int64_t kp, const uint16_t* bias, uint16_t* out,
+                int64_t out_rows, int64_t n, int64_t ldc, int mode, uint32_t* nonfinite,
+                hipStream_t stream) {
+  const int64_t tiles_m = (mp + BM - 1) / BM, tiles_n = (np + BN - 1) / BN;
+  if (tiles_m * tiles_n > (1ll << 31) - 1 || static_cast<int64_t>(BM) * kp >= (1ll << 31) ||
+      mp * kp / 32 >= (1ll << 31) || np * kp / 32 >= (1ll << 31))
+    return set_error(kUnsupported, "vdn_mxfp8_gemm: problem too large for 32-bit tile offsets");
+  const int group_m = 8;
+  hipLaunchKernelGGL((mxfp8_gemm_kernel<BM, BN, WGM, WGN>), dim3(tiles_m * tiles_n),
+                     dim3(WGM * WGN * 64), 0, stream, a, as, w, ws, mp, np, kp, bias, out,
+                     out_rows, n, ldc, mode, nonfinite, static_cast<int>(tiles_m),
+                     static_cast<int>(tiles_n), group_m);
+  return check_launch("vdn_mxfp8_gemm");
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+}  // namespace
+}  // namespace vdn
+
+using namespace vdn;
+
+// Reference: src/models/ops/mxfp8_linear.py:61-93 (MXFP8Linear.forward_quantized: scaled_mm
+// BlockWise1x32 + SWIZZLE_32_4_4, crop to [rows, N], + bias in bf16).
+// mode 0 stores, mode 1 adds into the existing bf16 output (out += y, one bf16 rounding per
+// op), as in `out[video] += to_out_linear(...)` (hybrid_attention.py:254). `nonfinite`
+// (nullable) receives 1 when any stored output is not finite (mxfp8_linear.py:91-92).
+VDN_API int vdn_mxfp8_gemm(const void* a, const void* a_scales, int64_t mp, const void* w,
+                           const void* w_scales, int64_t np, int64_t kp, const void* bias,
+                           void* out, int64_t out_rows, int64_t n, int64_t ldc, int mode,
+                           uint32_t* nonfinite, void* stream) {
+  const char* name = "vdn_mxfp8_gemm";
+  if (a == nullptr || a_scales == nullptr || w == nullptr || w_scales == nullptr || out == nullptr)
+    return set_error(kInvalidArgument, "%s: null pointer argument", name);
+  if (mp <= 0 || np <= 0 || kp <= 0 || mp % 128 || np % 128 || kp % 128)
+    return set_error(kInvalidArgument, "%s: padded M/N/K must be positive multiples of 128", name);
+  if (n <= 0 || n > np || out_rows < 0 || out_rows > mp || ldc < n)
+    return set_error(kInvalidArgument, "%s: invalid output geometry", name);
+  if (mode != kStore && mode != kAccumulate)
+    return set_error(kInvalidArgument, "%s: unknown mode %d", name, mode);
+  if (!aligned(a, 16) || !aligned(w, 16) || !aligned(a_scales, 4) || !aligned(w_scales, 4))
+    return set_error(kInvalidArgument, "%s: code buffers need 16-byte, scales 4-byte alignment",
+                     name);
+  if (out_rows == 0) return kOk;
+  auto st = static_cast<hipStream_t>(stream);
+  auto* ap = static_cast<const uint8_t*>(a);
+  auto* asp = static_cast<const uint8_t*>(a_scales);
+  auto* wp = static_cast<const uint8_t*>(w);
+  auto* wsp = static_cast<const uint8_t*>(w_scales);
+  auto* bp = static_cast<const uint16_t*>(bias);
+  auto* op = static_cast<uint16_t*>(out);
+  if (mp >= 1024 && np >= 1024)
+    return launch_gemm<256, 256, 2, 2>(ap, asp, mp, wp, wsp, np, kp, bp, op, out_rows, n, ldc,
+                                       mode, nonfinite, st);
+  return launch_gemm<128, 128, 2, 2>(ap, asp, mp, wp, wsp, np, kp, bp, op, out_rows, n, ldc, mode,
+                                     nonfinite, st);
+}

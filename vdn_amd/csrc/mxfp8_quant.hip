@@ -1,0 +1,348 @@
+// MXFP8 producer kernels for gfx950: block-32 E4M3FN codes + E8M0 scales in the
+// SWIZZLE_32_4_4 order, written straight from bf16 activations.
+//
+//   vdn_mxfp8_quantize          bf16 [R,K] -> codes [RP,KP] + scales       (mxfp8_kernels.py:31-58)
+//   vdn_mxfp8_act_quantize      act(bf16) rounded to bf16 -> codes+scales  (mxfp8_kernels.py:62-84;
+//                               GELU-tanh and SwiGLU activations)
+//   vdn_mxfp8_prenorm_quantize  RMSNorm * (1 + scale[i]) + shift[i] -> bf16 -> codes+scales
+//                               (mxfp8_kernels.py:87-110, 127-139)
+//
+// All three are HBM-bound. Work is split into 16-lane groups that own one row and
+// one 128-column chunk: each lane reads 8 contiguous bf16 (one 16-byte load), four
+// lanes form one 32-element block (amax by two xor-shuffles), and lane 0 of the group
+// stores the chunk's four scale bytes as one dword, because SWIZZLE_32_4_4 keeps the
+// four K-blocks of a row inside a 128-column chunk contiguous.
+#include "mxfp8_common.h"
+
+#include <math.h>
+
+namespace vdn {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kItemsPerGroup = 4;  // (row, chunk) items per 16-lane group
+
+enum Act : int { kActNone = 0, kActGeluTanh = 1, kActSwiGLU = 2 };
+
+__device__ __forceinline__ bool bf16_nonfinite(uint16_t h) { return (h & 0x7f80) == 0x7f80; }
+
+// Loads 8 bf16 values of one row starting at column c0 (masked to zero outside
+// [0,rows) x [0,k)). `vec` selects the 16-byte path (k % 8 == 0, aligned rows).
+template <bool kVec>
+__device__ __forceinline__ void load_row8(const uint16_t* __restrict__ x, int64_t r, int64_t c0,
+                                          int64_t rows, int64_t k, int64_t stride,
+                                          float* v, bool& bad) {
+  if (kVec) {
+    if (r < rows && c0 < k) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(x + r * stride + c0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint16_t lo = static_cast<uint16_t>(w[i] & 0xffff);
+        const uint16_t hi = static_cast<uint16_t>(w[i] >> 16);
+        bad = bad || bf16_nonfinite(lo) || bf16_nonfinite(hi);
+        v[2 * i] = bf16_bits_to_f32(lo);
+        v[2 * i + 1] = bf16_bits_to_f32(hi);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (r < rows && c0 + i < k) {
+        const uint16_t h = x[r * stride + c0 + i];
+        bad |= bf16_nonfinite(h);
+        v[i] = bf16_bits_to_f32(h);
+      } else {
+        v[i] = 0.f;
+      }
+    }
+  }
+}
+
+#pragma clang fp contract(off)
+__device__ __forceinline__ float gelu_tanh(float x) {
+  // torch's approximate="tanh" GELU, evaluated in fp32 and rounded once by the caller.
+  const float kBeta = 0.7978845608028654f;  // sqrt(2/pi)
+  const float kKappa = 0.044715f;
+  const float cube = x * x * x;
+  const float inner = kBeta * (x + kKappa * cube);
+  return 0.5f * x * (1.f + tanhf(inner));
+}
+
+__device__ __forceinline__ float silu_mul(float a, float g) {
+  const float sig = 1.f / (1.f + expf(-g));
+  return a * (g * sig);
+}
+#pragma clang fp contract(on)
+
+// Quantizes the 8 values a lane holds (one quarter of a 32-block), stores the 8 codes
+// and, from lane 0 of each 16-lane group, the chunk's 4 scale bytes.
+__device__ __forceinline__ void quantize_store8(const float* v, int lane16, int64_t r, int64_t chunk,
+                                                int64_t kp, uint8_t* __restrict__ q,
+                                                uint8_t* __restrict__ s) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 16));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 16));
+  float inv;
+  const uint32_t scale = e8m0_from_amax(amax, &inv);
+  float scaled[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) scaled[i] = v[i] * inv;
+  const u32x2 codes = e4m3x8(scaled);
+  *reinterpret_cast<u32x2*>(q + r * kp + chunk * 128 + lane16 * 8) = codes;
+  const uint32_t s1 = __shfl_down(scale, 4, 16);
+  const uint32_t s2 = __shfl_down(scale, 8, 16);
+  const uint32_t s3 = __shfl_down(scale, 12, 16);
+  if (lane16 == 0) {
+    const uint32_t word = scale | (s1 << 8) | (s2 << 16) | (s3 << 24);
+    *reinterpret_cast<uint32_t*>(s + swizzled_scale_offset(r, chunk * 4, kp >> 7)) = word;
+  }
+}
+
+template <int kAct, bool kVec>
+__global__ void __launch_bounds__(kThreads)
+mxfp8_quantize_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t k, int64_t stride,
+                      uint8_t* __restrict__ q, uint8_t* __restrict__ s, int64_t kp, int64_t items,
+                      uint32_t* __restrict__ nonfinite) {
+  const int lane16 = threadIdx.x & 15;
+  const int64_t ngroups = static_cast<int64_t>(gridDim.x) * (kThreads / 16);
+  const int64_t group = static_cast<int64_t>(blockIdx.x) * (kThreads / 16) + (threadIdx.x >> 4);
+  const int64_t chunks = kp >> 7;
+  bool bad = false;
+  float v[kItemsPerGroup][8];
+  // Issue every load of the group's items before any arithmetic.
+#pragma unroll
+  for (int j = 0; j < kItemsPerGroup; ++j) {
+    const int64_t item = group + j * ngroups;
+    const int64_t r = item < items ? item / chunks : rows;  // rows => zero fill
+    const int64_t c0 = (item % chunks) * 128 + lane16 * 8;
+    if (kAct == kActSwiGLU) {
+      float g[8];
+      load_row8<kVec>(x, r, c0, rows, k, stride, v[j], bad);
+      load_row8<kVec>(x + k, r, c0, rows, k, stride, g, bad);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[j][i] = round_bf16(silu_mul(v[j][i], g[i]));
+    } else {
+      load_row8<kVec>(x, r, c0, rows, k, stride, v[j], bad);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kItemsPerGroup; ++j) {
+    const int64_t item = group + j * ngroups;
+    if (item >= items) break;  // uniform across the 16-lane group
+    const int64_t r = item / chunks;
+    const int64_t chunk = item % chunks;
+    if (kAct == kActGeluTanh) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[j][i] = round_bf16(gelu_tanh(v[j][i]));
+    }
+    if (kAct != kActNone) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) bad |= !(fabsf(v[j][i]) < INFINITY);
+    }
+    quantize_store8(v[j], lane16, r, chunk, kp, q, s);
+  }
+  if (__ballot(bad) != 0 && (threadIdx.x & 63) == 0) atomicOr(nonfinite, 1u);
+}
+
+// One workgroup per padded row. The row stays in registers: slice j of thread t is
+// columns [8(t + 256 j), +8), so 4 consecutive lanes share a 32-block and 16 share a
+// 128-column chunk, exactly as in the plain quantizer.
+template <int kMaxSlices, bool kVec>
+__global__ void __launch_bounds__(kThreads)
+prenorm_quantize_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t k, int64_t stride,
+                        const void* __restrict__ weight, int weight_f32, float eps,
+                        const void* __restrict__ scale, int64_t scale_stride,
+                        const void* __restrict__ shift, int64_t shift_stride, int tables_f32,
+                        const int64_t* __restrict__ indices, uint16_t* __restrict__ y,
+                        uint8_t* __restrict__ q, uint8_t* __restrict__ s,
+                        uint8_t* __restrict__ finite, int64_t kp) {
+#pragma clang fp contract(off)
+  __shared__ float red_sum[kThreads / 64];
+  __shared__ int red_bad[kThreads / 64];
+  const int tid = threadIdx.x;
+  const int lane16 = tid & 15;
+  const int64_t r = blockIdx.x;
+  const bool in_row = r < rows;
+  const int64_t slices = kp >> 3;
+  const int64_t table_row = in_row ? indices[r] : 0;
+  float v[kMaxSlices][8];
+  bool bad = false;
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMaxSlices; ++j) {
+    const int64_t sl = tid + j * kThreads;
+    load_row8<kVec>(x, sl < slices ? r : rows, sl * 8, rows, k, stride, v[j], bad);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += v[j][i] * v[j][i];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+  if ((tid & 63) == 0) red_sum[tid >> 6] = ss;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) total += red_sum[w];
+  const float ms = total / static_cast<float>(k) + eps;
+  const float inv_rms = static_cast<float>(1.0 / sqrt(static_cast<double>(ms)));
+#pragma unroll
+  for (int j = 0; j < kMaxSlices; ++j) {
+    const int64_t sl = tid + j * kThreads;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t c = sl * 8 + i;
+      float value = 0.f;
+      if (in_row && c < k) {
+        const float w = weight_f32 ? static_cast<const float*>(weight)[c]
+                                   : bf16_bits_to_f32(static_cast<const uint16_t*>(weight)[c]);
+        float sc, sh;
+        if (tables_f32) {
+          sc = static_cast<const float*>(scale)[table_row * scale_stride + c];
+          sh = static_cast<const float*>(shift)[table_row * shift_stride + c];
+        } else {
+          sc = bf16_bits_to_f32(static_cast<const uint16_t*>(scale)[table_row * scale_stride + c]);
+          sh = bf16_bits_to_f32(static_cast<const uint16_t*>(shift)[table_row * shift_stride + c]);
+        }
+        const float t = (v[j][i] * inv_rms) * w;
+        const float u = 1.0f + sc;
+        value = round_bf16(t * u + sh);
+        bad |= !(fabsf(value) < INFINITY);
+      }
+      v[j][i] = value;
+    }
+    if (y != nullptr && in_row && sl < slices) {
+      if (kVec && sl * 8 < k) {
+        u32x4 packed;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) packed[i] = pack_bf16x2(v[j][2 * i], v[j][2 * i + 1]);
+        *reinterpret_cast<u32x4*>(y + r * k + sl * 8) = packed;
+      } else if (!kVec) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (sl * 8 + i < k) y[r * k + sl * 8 + i] = f32_to_bf16_bits(v[j][i]);
+      }
+    }
+    if (sl < slices) quantize_store8(v[j], lane16, r, sl >> 4, kp, q, s);
+  }
+  const int any_bad = __ballot(bad) != 0;
+  if ((tid & 63) == 0) red_bad[tid >> 6] = any_bad;
+  __syncthreads();
+  if (tid == 0) {
+    int b = 0;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) b |= red_bad[w];
+    finite[r] = b ? 0 : 1;
+  }
+}
+
+int64_t pad128(int64_t n) { return (n + 127) / 128 * 128; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+template <int kAct>
+int launch_quantize(const void* x, int64_t rows, int64_t k, int64_t stride, void* q, void* s,
+                    uint32_t* nonfinite, hipStream_t stream, const char* name) {
+  if (rows < 0 || k <= 0) return set_error(kInvalidArgument, "%s: rows must be >= 0 and K > 0", name);
+  if (stride < k * (kAct == kActSwiGLU ? 2 : 1))
+    return set_error(kInvalidArgument, "%s: row stride %lld smaller than row width", name,
+                     static_cast<long long>(stride));
+  if (x == nullptr || q == nullptr || s == nullptr || nonfinite == nullptr)
+    return set_error(kInvalidArgument, "%s: null pointer argument", name);
+  const int64_t rp = pad128(rows), kp = pad128(k);
+  if (rp == 0) return kOk;
+  const int64_t items = rp * (kp / 128);
+  const int64_t per_block = (kThreads / 16) * kItemsPerGroup;
+  const int64_t blocks = (items + per_block - 1) / per_block;
+  const bool vec = (k % 8 == 0) && (stride % 8 == 0) && aligned16(x) &&
+                   (kAct != kActSwiGLU || k % 8 == 0);
+  auto* xp = static_cast<const uint16_t*>(x);
+  auto* qp = static_cast<uint8_t*>(q);
+  auto* sp = static_cast<uint8_t*>(s);
+  if (vec) {
+    hipLaunchKernelGGL((mxfp8_quantize_kernel<kAct, true>), dim3(blocks), dim3(kThreads), 0, stream,
+                       xp, rows, k, stride, qp, sp, kp, items, nonfinite);
+  } else {
+    hipLaunchKernelGGL((mxfp8_quantize_kernel<kAct, false>), dim3(blocks), dim3(kThreads), 0, stream,
+                       xp, rows, k, stride, qp, sp, kp, items, nonfinite);
+  }
+  return check_launch(name);
+}
+
+}  // namespace
+}  // namespace vdn
+
+using namespace vdn;
+
+// Reference: src/models/ops/mxfp8_kernels.py:31-58 (_quantize / launch_quantize).
+VDN_API int vdn_mxfp8_quantize(const void* x, int64_t rows, int64_t k, int64_t row_stride,
+                               void* q, void* scales, uint32_t* nonfinite, void* stream) {
+  return launch_quantize<kActNone>(x, rows, k, row_stride, q, scales, nonfinite,
+                                   static_cast<hipStream_t>(stream), "vdn_mxfp8_quantize");
+}
+
+// Reference: src/models/ops/mxfp8_kernels.py:62-84, 113-124 (_swiglu_mx) and the block's
+// GELU-tanh FFN activation. act: 1 = GELU-tanh over [R,K]; 2 = SwiGLU a*silu(g) over [R,2K].
+VDN_API int vdn_mxfp8_act_quantize(const void* x, int64_t rows, int64_t k, int64_t row_stride,
+                                   int act, void* q, void* scales, uint32_t* nonfinite,
+                                   void* stream) {
+  auto st = static_cast<hipStream_t>(stream);
+  if (act == kActGeluTanh)
+    return launch_quantize<kActGeluTanh>(x, rows, k, row_stride, q, scales, nonfinite, st,
+                                         "vdn_mxfp8_act_quantize");
+  if (act == kActSwiGLU)
+    return launch_quantize<kActSwiGLU>(x, rows, k, row_stride, q, scales, nonfinite, st,
+                                       "vdn_mxfp8_act_quantize");
+  return set_error(kInvalidArgument, "vdn_mxfp8_act_quantize: unknown activation %d", act);
+}
+
+// Reference: src/models/ops/mxfp8_kernels.py:87-110, 127-139 (_prenorm_mx /
+// launch_prenorm_quantize). flags: bit0 weight is fp32, bit1 scale/shift tables are fp32.
+VDN_API int vdn_mxfp8_prenorm_quantize(const void* x, int64_t rows, int64_t k, int64_t row_stride,
+                                       const void* weight, float eps, const void* scale,
+                                       int64_t scale_stride, const void* shift,
+                                       int64_t shift_stride, const int64_t* indices, int flags,
+                                       void* y, void* q, void* scales, uint8_t* finite,
+                                       void* stream) {
+  const char* name = "vdn_mxfp8_prenorm_quantize";
+  if (rows < 0 || k <= 0) return set_error(kInvalidArgument, "%s: rows must be >= 0 and K > 0", name);
+  if (row_stride < k) return set_error(kInvalidArgument, "%s: row stride smaller than K", name);
+  if (x == nullptr || weight == nullptr || scale == nullptr || shift == nullptr ||
+      indices == nullptr || q == nullptr || scales == nullptr || finite == nullptr)
+    return set_error(kInvalidArgument, "%s: null pointer argument", name);
+  const int64_t rp = pad128(rows), kp = pad128(k);
+  if (rp == 0) return kOk;
+  const int64_t slices = kp / 8;
+  const bool vec = (k % 8 == 0) && (row_stride % 8 == 0) && aligned16(x) &&
+                   (y == nullptr || aligned16(y));
+  auto st = static_cast<hipStream_t>(stream);
+  auto* xp = static_cast<const uint16_t*>(x);
+  auto* yp = static_cast<uint16_t*>(y);
+  auto* qp = static_cast<uint8_t*>(q);
+  auto* sp = static_cast<uint8_t*>(scales);
+  const int wf = flags & 1, tf = (flags >> 1) & 1;
+#define VDN_PRENORM(MS)                                                                        \
+  if (vec)                                                                                     \
+    hipLaunchKernelGGL((prenorm_quantize_kernel<MS, true>), dim3(rp), dim3(kThreads), 0, st,  \
+                       xp, rows, k, row_stride, weight, wf, eps, scale, scale_stride, shift,   \
+                       shift_stride, tf, indices, yp, qp, sp, finite, kp);                     \
+  else                                                                                         \
+    hipLaunchKernelGGL((prenorm_quantize_kernel<MS, false>), dim3(rp), dim3(kThreads), 0, st, \
+                       xp, rows, k, row_stride, weight, wf, eps, scale, scale_stride, shift,   \
+                       shift_stride, tf, indices, yp, qp, sp, finite, kp);
+  if (slices <= kThreads * 1) {
+    VDN_PRENORM(1)
+  } else if (slices <= kThreads * 3) {
+    VDN_PRENORM(3)
+  } else if (slices <= kThreads * 8) {
+    VDN_PRENORM(8)
+  } else {
+    return set_error(kUnsupported, "%s: K=%lld exceeds the register-resident row limit 16384",
+                     name, static_cast<long long>(k));
+  }
+#undef VDN_PRENORM
+  return check_launch(name);
+}
