@@ -74,6 +74,107 @@ int vdn_mxfp8_gemm(const void* a, const void* a_scales, int64_t mp, const void* 
                    int64_t out_rows, int64_t n, int64_t ldc, int mode, uint32_t* nonfinite,
                    void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * VDA linear-attention branch (D = 128). A 4-D operand "(f, h, s, c)" is addressed as
+ * base + f*sf + h*sh + s*ss + c (element strides, channels contiguous); raw token-major
+ * projections [F*S, H, 128] with row stride R and head stride Hs map to sf = S*R, sh = Hs,
+ * ss = R.
+ * ------------------------------------------------------------------------------------- */
+
+/*
+ * tokens [n = frames*spatial, heads, 128] (row/head strides) -> out [frames, heads, spatial,
+ * 128]: SiLU, then L2 over the 128 channels when l2norm (clamp 1e-12 on the sum of squares).
+ * is_f32 selects fp32 in/out, else bf16.
+ * Replaces: paper_prepare (src/models/linear_attention/paper_stack.py:30-48) ->
+ * vdn_silu_l2norm (src/models/linear_attention/paper_sglang.py:251-283).
+ */
+int vdn_vda_prepare(const void* tokens, int64_t n, int heads, int64_t row_stride,
+                    int64_t head_stride, int frames, int spatial, int l2norm, int is_f32,
+                    void* out, void* stream);
+
+/*
+ * Joint statistics per (frame, head): A = (K^T diag(beta) K + transpose) / 2 (fp32-grade),
+ * B = bf16(bf16(v * bf16(beta))^T k) (fp32 storage), A, B: [frames, heads, 128, 128] fp32.
+ * k, v: bf16 operands; beta: bf16 (beta_f32 = 0) or fp32, addressed (f, h, s). activate = 1
+ * applies the paper_prepare activation in registers (k: SiLU + L2, v: SiLU) to raw
+ * projections.
+ * Replaces: paper_statistics / _joint_stats (src/models/linear_attention/paper_stack.py:51-110).
+ */
+int vdn_vda_statistics(const void* k, int64_t k_sf, int64_t k_sh, int64_t k_ss, const void* v,
+                       int64_t v_sf, int64_t v_sh, int64_t v_ss, const void* beta, int64_t b_sf,
+                       int64_t b_sh, int64_t b_ss, int beta_f32, int frames, int heads,
+                       int spatial, int activate, float* A, float* B, void* stream);
+
+/*
+ * T = diag(alpha) (I + A)^-1 and J = B (I + A)^-1 for `count` 128x128 fp32 matrices
+ * (I + A symmetric positive definite; no pivoting). alpha: [count, 128] or null (ones).
+ * Replaces: paper_delta_factors (src/models/linear_attention/paper_factor.py:133-186), the
+ * reference's pybind11 op delta_factors (src/models/ops/csrc/vdn_delta_factors.cpp:11-14).
+ */
+int vdn_vda_factors(const float* A, const float* B, const float* alpha, int64_t count, float* T,
+                    float* J, void* stream);
+
+/*
+ * Per chunk c (frames starts[c] .. ends[c]-1) and direction (0 forward, 1 reverse):
+ * CT = ordered product of the chunk's transitions, CI = the injection the chunk adds to a
+ * zero state. T, J: [frames, heads, 128, 128]; CT, CI: [2, chunks, heads, 128, 128].
+ * Replaces: _compose (src/models/linear_attention/paper_stack.py:162-181).
+ */
+int vdn_vda_compose(const float* T, const float* J, int heads, const int* starts, const int* ends,
+                    int chunks, float* CT, float* CI, void* stream);
+
+/*
+ * Both directional scans state <- state @ CT[c] + CI[c] over chunks, starting from seed
+ * (nullable: zero), writing bank [2, chunks, heads, 128, 128]. per_direction = 0 takes
+ * per-frame factors [chunks, heads, 128, 128] for both directions (one-frame chunks).
+ * Replaces: _scan_both / paper_boundary_scan (src/models/linear_attention/paper_stack.py:184-236).
+ */
+int vdn_vda_scan(const float* CT, const float* CI, const float* seed, int chunks, int heads,
+                 int per_direction, float* bank, void* stream);
+
+/*
+ * logp [frames + 1, heads, 128]: exclusive prefix sums of log(max(alpha, 1e-12)) over frames.
+ * Replaces: the log-prefix of paper_gather (src/models/linear_attention/paper_stack.py:256).
+ */
+int vdn_vda_log_prefix(const float* alpha, int frames, int heads, float* logp, void* stream);
+
+/*
+ * Boundary gather: out[f, h] = prefix[before[f], h] * exp(logp[f+1] - logp[bridge_before[f]])
+ * + suffix[after[f], h] * exp(logp[bridge_after[f]] - logp[f]) (per key channel; the exp
+ * factors only when bridge), with missing sides (has_* = 0) reading text (nullable: zero).
+ * prefix/suffix: [chunks, heads, 128, 128] fp32; index arrays int32 [frames];
+ * out: [frames, heads, 128, 128] bf16 (out_f32 = 0) or fp32.
+ * Replaces: paper_gather / _gather_state_kernel (src/models/linear_attention/paper_stack.py:239-263,
+ * paper_sglang.py:445-501).
+ */
+int vdn_vda_gather(const float* prefix, const float* suffix, const float* logp, const float* text,
+                   const int* before, const int* after, const int* has_before,
+                   const int* has_after, const int* bridge_before, const int* bridge_after,
+                   int frames, int heads, int bridge, int out_f32, void* out, void* stream);
+
+/*
+ * Fused readout: y = bf16(q' . state^T) per (frame, head), q' = bf16(L2(SiLU(q))) when
+ * activate_q, then out = bf16(y * (1/sqrt(mean(y^2) + eps)) * weight * gate).
+ * q, gate, out: bf16 addressed (f, h, s); state: bf16 [frames, heads, 128, 128] ([v][k]);
+ * weight: [128] bf16 or fp32 (weight_f32).
+ * Replaces: the readout matmul and vdn_linear_epilogue of paper_readout
+ * (src/models/linear_attention/paper_stack.py:317-318, paper_sglang.py:377-437).
+ */
+int vdn_vda_readout(const void* q, int64_t q_sf, int64_t q_sh, int64_t q_ss, int activate_q,
+                    const void* state, const void* weight, int weight_f32, float eps,
+                    const void* gate, int64_t g_sf, int64_t g_sh, int64_t g_ss, void* out,
+                    int64_t o_sf, int64_t o_sh, int64_t o_ss, int frames, int heads, int spatial,
+                    void* stream);
+
+/*
+ * RMSNorm(128) * weight * gate of a frame-major readout [frames, heads, spatial, 128] bf16.
+ * Replaces: vdn_linear_epilogue (src/models/linear_attention/paper_sglang.py:406-437).
+ */
+int vdn_vda_epilogue(const void* readout, const void* weight, int weight_f32, float eps,
+                     const void* gate, int64_t g_sf, int64_t g_sh, int64_t g_ss, void* out,
+                     int64_t o_sf, int64_t o_sh, int64_t o_ss, int frames, int heads, int spatial,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,224 @@
+"""GPU parity of the VDA kernels against the float64 oracle, at the reference test's
+tolerances (tests/test_paper_stack_vda_ops.py, test_paper_stack_vda_factor.py)."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import vda as ov
+from vdn_amd import vda as vv
+
+pytestmark = pytest.mark.gpu
+
+
+def close_rel(a, b, limit):
+    err = (a.double().cpu() - b.double().cpu()).norm() / b.double().cpu().norm().clamp_min(1e-20)
+    assert err.item() < limit, err.item()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("frames,spatial", [(1, 1), (3, 7), (17, 12)])
+@pytest.mark.parametrize("l2", [False, True])
+def test_prepare(device, dtype, frames, spatial, l2):
+    torch.manual_seed(711)
+    raw = torch.randn(frames * spatial, 2, 128, dtype=dtype)
+    out = vv.paper_prepare(raw.to(device), frames=frames, spatial=spatial, l2norm=l2)
+    ref = ov.prepare(raw, frames, spatial, l2)
+    assert out.is_contiguous() and out.shape == (frames, 2, spatial, 128)
+    if dtype == torch.bfloat16:
+        torch.testing.assert_close(out.cpu(), ref.to(dtype), atol=0., rtol=0.008)
+    else:
+        close_rel(out, ref, 5e-7)
+
+
+@pytest.mark.parametrize("beta_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("s", [1, 33, 129, 1008])
+def test_statistics(device, beta_dtype, s):
+    torch.manual_seed(s)
+    k = F.normalize(torch.randn(3, 2, s, 128), dim=-1).to(torch.bfloat16)
+    v = torch.randn_like(k)
+    beta = torch.rand(3, 2, s).to(beta_dtype)
+    a, b = vv.paper_statistics(k.to(device), v.to(device), beta.to(device))
+    ra, rb = ov.statistics(k, v, beta)
+    assert a.dtype == b.dtype == torch.float32
+    close_rel(a, ra, 5e-7)
+    close_rel(b, rb, 1e-4)
+    torch.testing.assert_close(a, a.transpose(-1, -2), atol=2e-6, rtol=1e-6)
+
+
+def test_statistics_correlated_keys_spd(device):
+    s = 1008
+    base = torch.randn(2, 3, 1, 128)
+    k = F.normalize(base + torch.randn(2, 3, s, 128) * .01, dim=-1).bfloat16()
+    v = torch.randn_like(k) * 10
+    beta = torch.rand(2, 3, s, dtype=torch.bfloat16)
+    a, b = vv.paper_statistics(k.to(device), v.to(device), beta.to(device))
+    ref = (k.double() * beta.double()[..., None]).transpose(-1, -2) @ k.double()
+    close_rel(a, ref, 5e-7)
+    assert torch.linalg.eigvalsh(a.double().cpu() + torch.eye(128, dtype=torch.float64)).min() > .999
+    t, inj = vv.paper_delta_factors(a, b)
+    inv = torch.linalg.inv(ref + torch.eye(128, dtype=torch.float64))
+    close_rel(t, inv, 3e-5)
+    close_rel(inj, b.double().cpu() @ inv, 3e-5)
+
+
+def test_statistics_from_projections_equals_prepare_then_statistics(device):
+    frames, spatial, h = 3, 50, 4
+    g = torch.Generator().manual_seed(4)
+    qkv = torch.randn(frames * spatial, 3 * h * 128, generator=g).to(torch.bfloat16).to(device)
+    k = qkv[:, h * 128:2 * h * 128].view(-1, h, 128)
+    v = qkv[:, 2 * h * 128:].view(-1, h, 128)
+    beta = torch.rand(frames * spatial, h, generator=g).to(torch.bfloat16).to(device)
+    a1, b1 = vv.statistics_from_projections(k, v, beta, frames, spatial)
+    kp = vv.paper_prepare(k, frames=frames, spatial=spatial, l2norm=True)
+    vp = vv.paper_prepare(v, frames=frames, spatial=spatial, l2norm=False)
+    bp = beta.view(frames, spatial, h).permute(0, 2, 1).contiguous()
+    a2, b2 = vv.paper_statistics(kp, vp, bp)
+    assert torch.equal(a1, a2) and torch.equal(b1, b2)
+
+
+def test_factors_fp64(device):
+    A, B, alpha = (t.float() for t in _stats(5, 3, seed=1))
+    T, J = vv.paper_delta_factors(A.to(device), B.to(device), alpha.to(device))
+    rT, rJ = ov.factors(A, B, alpha)
+    close_rel(T, rT, 1e-5)
+    close_rel(J, rJ, 3e-5)
+    T1, _ = vv.paper_delta_factors(A.to(device), B.to(device))
+    close_rel(T1, ov.factors(A, B)[0], 1e-5)
+    e = vv.paper_delta_factors(torch.empty(0, 128, 128, device=device),
+                               torch.empty(0, 128, 128, device=device))
+    assert e[0].shape == (0, 128, 128)
+
+
+def _stats(frames, heads, seed=0, s=9, decay=1.0):
+    g = torch.Generator().manual_seed(seed)
+    k = F.normalize(torch.randn(frames, heads, s, 128, generator=g), dim=-1)
+    A = (k.transpose(-1, -2) @ k).contiguous()
+    B = torch.randn(frames, heads, 128, 128, generator=g) * 0.1
+    alpha = (torch.rand(frames, heads, 128, generator=g) * 0.1 + 0.9) * decay
+    return A, B, alpha
+
+
+@pytest.mark.parametrize("frames,chunk", [(1, 1), (2, 8), (11, 4), (17, 8), (31, 1)])
+@pytest.mark.parametrize("text", [False, True])
+@pytest.mark.parametrize("decay", [1., 0.7, 0.001])
+def test_scan_and_gather_fp64(device, frames, chunk, text, decay):
+    h = 2
+    A, B, alpha = _stats(frames, h, seed=frames * 7 + chunk, decay=decay)
+    t, inj = vv.paper_delta_factors(A.to(device), B.to(device), alpha.to(device))
+    seed = torch.randn(h, 128, 128) * .3 if text else None
+    bounds = [(f // chunk * chunk - chunk, (f // chunk + 2) * chunk - 1) for f in range(frames)]
+    plan = vv.paper_boundary_plan(bounds, frames, device, chunk)
+    bank = vv.paper_boundary_scan(t, inj, plan, None if seed is None else seed.to(device))
+    prefix, suffix = ov.scan(t.cpu(), inj.cpu(), seed)
+    torch.testing.assert_close(bank[0].double().cpu(), prefix[torch.tensor(plan.cuts[1:]) - 1],
+                               atol=3e-6, rtol=3e-5)
+    torch.testing.assert_close(bank[1].double().cpu(), suffix[list(plan.cuts[:-1])],
+                               atol=3e-6, rtol=3e-5)
+    result = vv.paper_gather(bank, alpha.to(device), plan, None if seed is None else seed.to(device),
+                             torch.float32)
+    expected = ov.gather(prefix, suffix, alpha, bounds, seed)
+    torch.testing.assert_close(result.double().cpu(), expected, atol=4e-6, rtol=5e-5)
+    assert bank.shape == (2, plan.chunks, h, 128, 128)
+
+
+def test_gather_zero_decay_irregular_bounds_no_bridge(device):
+    frames, h = 9, 1
+    t = (torch.eye(128).expand(frames, h, 128, 128).contiguous() * .9)
+    inj = torch.randn_like(t)
+    alpha = torch.zeros(frames, h, 128)
+    bounds = [(max(0, f - f % 3), min(frames - 1, f + 2)) for f in range(frames)]
+    plan = vv.paper_boundary_plan(bounds, frames, device, 4)
+    seed = torch.randn_like(t[0])
+    bank = vv.paper_boundary_scan(t.to(device), inj.to(device), plan, seed.to(device))
+    prefix, suffix = ov.scan(t, inj, seed)
+    for bridge in (True, False):
+        out = vv.paper_gather(bank, alpha.to(device), plan, seed.to(device), torch.float32, bridge)
+        ref = ov.gather(prefix, suffix, alpha, bounds, seed, bridge)
+        torch.testing.assert_close(out.double().cpu(), ref, atol=5e-6, rtol=1e-5)
+
+
+def test_epilogue(device):
+    r = torch.randn(3, 2, 7, 128, dtype=torch.bfloat16)
+    w = torch.rand(128)
+    g = torch.rand(21, 2, 128, dtype=torch.bfloat16)
+    out = vv.vdn_linear_epilogue(r.to(device), w.to(device), g.to(device), 1e-6)
+    ref = ov.epilogue(r, w, g, 1e-6)
+    torch.testing.assert_close(out.cpu(), ref.to(out.dtype), atol=0.0078125, rtol=0.008)
+
+
+def _branch_inputs(frames, spatial, h, seed, text=False):
+    g = torch.Generator().manual_seed(seed)
+    raw = [torch.randn(frames * spatial, h, 128, generator=g).bfloat16() for _ in range(3)]
+    beta = torch.rand(frames * spatial, h, generator=g).bfloat16()
+    gate = torch.rand(frames * spatial, h, 128, generator=g).bfloat16()
+    alpha = torch.rand(frames, h, 128, generator=g) * 0.2 + 0.8
+    w = torch.rand(128, generator=g) + 0.5
+    tx = None
+    if text:
+        tx = (torch.randn(5, h, 128, generator=g).bfloat16(),
+              torch.randn(5, h, 128, generator=g).bfloat16(),
+              torch.rand(5, h, generator=g).bfloat16())
+    return raw, beta, gate, alpha, w, tx
+
+
+@pytest.mark.parametrize("text", [False, True])
+@pytest.mark.parametrize("frames,spatial,chunk,radius", [(11, 7, 4, 1), (9, 70, 8, 1),
+                                                         (5, 130, 8, 2)])
+def test_branch_against_fp64_oracle(device, text, frames, spatial, chunk, radius):
+    raw, beta, gate, alpha, w, tx = _branch_inputs(frames, spatial, 2, frames + spatial, text)
+    bounds = ov.window_bounds(frames, radius)
+    dev = lambda x: x.to(device)
+    out = vv.vda_forward(*map(dev, raw), dev(beta), dev(gate), dev(alpha), bounds, frames, spatial,
+                         dev(w), 1e-6, chunk_size=chunk,
+                         text=None if tx is None else tuple(map(dev, tx)))
+    ref, _ = ov.paper_branch(*raw, beta, gate, alpha, bounds, frames, spatial, w, 1e-6, text=tx)
+    assert out.dtype == torch.bfloat16 and out.shape == (frames * spatial, 2 * 128)
+    close_rel(out, ref, 0.004)
+
+
+def test_branch_on_fused_qkv_strides(device):
+    """Raw q/k/v as column slices of one fused projection output (the block's layout)."""
+    frames, spatial, h = 4, 40, 3
+    g = torch.Generator().manual_seed(8)
+    qkv = torch.randn(frames * spatial, 3 * h * 128, generator=g).bfloat16()
+    raw = [qkv[:, i * h * 128:(i + 1) * h * 128].view(-1, h, 128) for i in range(3)]
+    beta = torch.rand(frames * spatial, h, generator=g).bfloat16()
+    gate = torch.rand(frames * spatial, h, 128, generator=g).bfloat16()
+    alpha = torch.rand(frames, h, 128, generator=g) * 0.2 + 0.8
+    w = torch.ones(128)
+    bounds = ov.window_bounds(frames, 1)
+    qd = qkv.to(device)
+    rd = [qd[:, i * h * 128:(i + 1) * h * 128].view(-1, h, 128) for i in range(3)]
+    out = vv.vda_forward(*rd, beta.to(device), gate.to(device), alpha.to(device), bounds, frames,
+                         spatial, w.to(device), 1e-6)
+    ref, _ = ov.paper_branch(*raw, beta, gate, alpha, bounds, frames, spatial, w, 1e-6)
+    close_rel(out, ref, 0.004)
+
+
+def test_c3_full_shape_sampled_heads(device):
+    """C3: 30 frames x 3600 tokens, 40 heads, d 128, window +-1 frame. Heads are independent,
+    so parity is checked on 2 of the 40 heads against the float64 oracle."""
+    frames, spatial, h = 30, 3600, 40
+    g = torch.Generator().manual_seed(3)
+    n = frames * spatial
+    q = F.normalize(torch.randn(n, h, 128, generator=g), dim=-1).bfloat16()
+    k = F.normalize(torch.randn(n, h, 128, generator=g), dim=-1).bfloat16()
+    v = torch.randn(n, h, 128, generator=g).bfloat16()
+    beta = torch.sigmoid(torch.randn(n, h, generator=g)).bfloat16()
+    gate = torch.sigmoid(torch.randn(n, h, 128, generator=g)).bfloat16()
+    a = torch.empty(h).uniform_(1, 16, generator=g)
+    dt = torch.exp(torch.rand(h, 128, generator=g) * (torch.log(torch.tensor(0.1))
+                   - torch.log(torch.tensor(0.001))) + torch.log(torch.tensor(0.001)))
+    alpha = torch.exp(-a[:, None] * dt).expand(frames, h, 128).contiguous()
+    w = torch.ones(128)
+    bounds = ov.window_bounds(frames, 1)
+    out = vv.vda_forward(q.to(device), k.to(device), v.to(device), beta.to(device),
+                         gate.to(device), alpha.to(device), bounds, frames, spatial, w.to(device),
+                         1e-6)
+    assert bool(torch.isfinite(out).all())
+    heads = [0, 29]
+    sel = lambda x: x[:, heads].contiguous()
+    ref, _ = ov.paper_branch(sel(q), sel(k), sel(v), sel(beta), sel(gate), alpha[:, heads], bounds,
+                             frames, spatial, w, 1e-6)
+    got = out.view(n, h, 128)[:, heads].reshape(n, -1)
+    close_rel(got, ref, 0.004)

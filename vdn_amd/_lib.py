@@ -30,6 +30,19 @@ SIGNATURES = {
                                    _ptr, _i32, _ptr, _ptr, _ptr, _ptr, _ptr],
     "vdn_mxfp8_gemm": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64, _i64,
                        _i32, _ptr, _ptr],
+    "vdn_vda_prepare": [_ptr, _i64, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _ptr, _ptr],
+    "vdn_vda_statistics": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64,
+                           _i32, _i32, _i32, _i32, _i32, _ptr, _ptr, _ptr],
+    "vdn_vda_factors": [_ptr, _ptr, _ptr, _i64, _ptr, _ptr, _ptr],
+    "vdn_vda_compose": [_ptr, _ptr, _i32, _ptr, _ptr, _i32, _ptr, _ptr, _ptr],
+    "vdn_vda_scan": [_ptr, _ptr, _ptr, _i32, _i32, _i32, _ptr, _ptr],
+    "vdn_vda_log_prefix": [_ptr, _i32, _i32, _ptr, _ptr],
+    "vdn_vda_gather": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i32, _i32,
+                       _i32, _i32, _ptr, _ptr],
+    "vdn_vda_readout": [_ptr, _i64, _i64, _i64, _i32, _ptr, _ptr, _i32, _f32, _ptr, _i64, _i64,
+                        _i64, _ptr, _i64, _i64, _i64, _i32, _i32, _i32, _ptr],
+    "vdn_vda_epilogue": [_ptr, _ptr, _i32, _f32, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64,
+                         _i32, _i32, _i32, _ptr],
 }
 
 _LOCK = threading.Lock()

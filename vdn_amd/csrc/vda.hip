@@ -1,0 +1,909 @@
+// VDA frame-wise delta-rule linear attention ("vdn_solve", bridge = alpha) for gfx950.
+//
+// Per frame f and head h (S tokens, D = 128):
+//   k' = bf16(L2(SiLU(k))), v' = bf16(SiLU(v)), q' = bf16(L2(SiLU(q)))   (paper_prepare)
+//   A = 1/2 (Kᵀ diag(β) K + its transpose)  fp32-grade;  B = bf16(bf16(v'·β)ᵀ k')  (paper_statistics)
+//   T = diag(α) (I + A)⁻¹,  J = B (I + A)⁻¹                                (paper_delta_factors)
+//   forward/reverse affine scans over frames (or frame chunks)             (paper_boundary_scan)
+//   state = α-bridged sum of the states just outside each frame's window  (paper_gather)
+//   out = RMSNorm(bf16(q'·stateᵀ))·w·gate                                  (readout + vdn_linear_epilogue)
+// Reference: src/models/linear_attention/paper_stack.py, paper_sglang.py, paper_factor.py,
+// scan.py, delta_rule.py:45-60.
+//
+// MI355X design notes:
+//   * the statistics read raw token-major q/k/v straight from the QKV projection output (any
+//     row/head stride) and apply SiLU/L2 in registers, so no frame-major copy is written;
+//   * A needs fp32-grade accuracy (I + A is inverted). With bf16 k' and bf16 β the product
+//     p = β k' has at most 16 significant bits, so p = hi + lo with hi, lo bf16 is exact and
+//     A = Kᵀ·P_hi + Kᵀ·P_lo runs on bf16 MFMA with fp32 accumulation (3 terms for fp32 β);
+//   * token-contiguous MFMA operands come from token-major LDS tiles through
+//     ds_read_tr16_b64: within a 16-lane group, lane L reading 8 bytes at
+//     (row r0 + L/4, column c0 + 4 (L % 4)) delivers to lane l the 4 values
+//     M[r0 .. r0+3][c0 + l] (measured on gfx950);
+//   * the scans keep a 16-row block of the 128x128 fp32 state per workgroup (rows evolve
+//     independently) and use fp32 MFMA for state @ T.
+#include "common.h"
+
+#include <math.h>
+
+namespace vdn {
+namespace {
+
+constexpr int kD = 128;
+
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
+
+__device__ __forceinline__ bf16x4_t lds_read_tr(const uint16_t* lds_elem_ptr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+      (lds_bf16x4_t*)((__attribute__((address_space(3))) char*)(lds_elem_ptr)));
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// Sum over the 16 lanes of a 16-lane group (xor butterfly).
+__device__ __forceinline__ float sum16(float v) {
+  v += __shfl_xor(v, 1, 16);
+  v += __shfl_xor(v, 2, 16);
+  v += __shfl_xor(v, 4, 16);
+  v += __shfl_xor(v, 8, 16);
+  return v;
+}
+
+__device__ __forceinline__ void unpack8(const u32x4 w, float* v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffff));
+    v[2 * i + 1] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
+  }
+}
+
+__device__ __forceinline__ u32x4 pack8(const float* v) {
+  u32x4 w;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+  return w;
+}
+
+// SiLU (+ L2 over the 16-lane group's 128 channels) of 8 values, rounded to bf16.
+// paper_sglang.py:235-238: y = silu(x); y / sqrt(max(sum y^2, 1e-12)).
+__device__ __forceinline__ void activate8(float* v, bool l2) {
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[i] = silu(v[i]);
+    ss += v[i] * v[i];
+  }
+  if (l2) {
+    ss = sum16(ss);
+    const float inv = 1.0f / sqrtf(fmaxf(ss, 1e-12f));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] *= inv;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = round_bf16(v[i]);
+}
+
+// Strided 3-D view of a bf16 [frames, heads, tokens, channel] operand; channels contiguous.
+struct View {
+  const uint16_t* base;
+  int64_t sf, sh, ss;
+  __device__ __forceinline__ const uint16_t* at(int f, int h, int s) const {
+    return base + f * sf + h * sh + s * ss;
+  }
+};
+
+// ------------------------------------------------------------------- prepare ----
+// tokens [N, H, D] (row stride sn, head stride sh) -> frame-major out [F, H, S, D]
+template <bool kF32>
+__global__ void __launch_bounds__(256)
+vda_prepare_kernel(const void* __restrict__ x, int64_t n, int heads, int64_t sn, int64_t sh,
+                   int spatial, int l2, void* __restrict__ out) {
+  const int lane16 = threadIdx.x & 15;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  const int64_t items = n * heads;
+  if (item >= items) return;  // uniform per 16-lane group
+  const int64_t row = item / heads;
+  const int h = static_cast<int>(item % heads);
+  const int64_t f = row / spatial, s = row % spatial;
+  float v[8];
+  if (kF32) {
+    const float* src = static_cast<const float*>(x) + row * sn + h * sh + lane16 * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = src[i];
+  } else {
+    const uint16_t* src = static_cast<const uint16_t*>(x) + row * sn + h * sh + lane16 * 8;
+    unpack8(*reinterpret_cast<const u32x4*>(src), v);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[i] = silu(v[i]);
+    ss += v[i] * v[i];
+  }
+  if (l2) {
+    ss = sum16(ss);
+    const float inv = 1.0f / sqrtf(fmaxf(ss, 1e-12f));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] *= inv;
+  }
+  const int64_t dst = ((f * heads + h) * spatial + s) * kD + lane16 * 8;
+  if (kF32) {
+    float* o = static_cast<float*>(out) + dst;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = v[i];
+  } else {
+    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + dst) = pack8(v);
+  }
+}
+
+// ---------------------------------------------------------------- statistics ----
+constexpr int kTS = 32;          // tokens per step
+constexpr int kRow = 144;        // padded LDS row (bf16 elements): 288 bytes
+constexpr int kTile = kTS * kRow;
+
+// One workgroup per (frame, head); 4 waves, wave (wm, wn) owns the 64x64 quadrant
+// rows [64 wm, +64) x cols [64 wn, +64) of both A' = Kᵀ P and B' = Vbᵀ K.
+template <int kSplit>
+__global__ void __launch_bounds__(256)
+vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b_sf,
+                      int64_t b_sh, int64_t b_ss, int beta_f32, int spatial, int heads,
+                      int activate, float* __restrict__ A, float* __restrict__ B) {
+  constexpr int kTiles = 2 + kSplit;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2][kTiles][kTile];
+  const int fh = blockIdx.x;
+  const int f = fh / heads, h = fh % heads;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lane16 = tid & 15;
+  const int c8 = lane16 * 8;
+  const int steps = (spatial + kTS - 1) / kTS;
+
+  // loader: thread handles tokens (tid/16) and (tid/16 + 16) of the step, channels c8..c8+7
+  u32x4 kraw[2], vraw[2];
+  float braw[2];
+  auto load_step = [&](int step) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int s = step * kTS + (tid >> 4) + 16 * j;
+      if (s < spatial) {
+        kraw[j] = *reinterpret_cast<const u32x4*>(kv.at(f, h, s) + c8);
+        vraw[j] = *reinterpret_cast<const u32x4*>(vv.at(f, h, s) + c8);
+        const int64_t bo = f * b_sf + h * b_sh + s * b_ss;
+        braw[j] = beta_f32 ? static_cast<const float*>(beta)[bo]
+                           : bf16_bits_to_f32(static_cast<const uint16_t*>(beta)[bo]);
+      } else {
+        kraw[j] = u32x4{0, 0, 0, 0};
+        vraw[j] = u32x4{0, 0, 0, 0};
+        braw[j] = 0.f;
+      }
+    }
+  };
+  auto store_step = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int r = (tid >> 4) + 16 * j;
+      float kf[8], vf[8];
+      unpack8(kraw[j], kf);
+      unpack8(vraw[j], vf);
+      if (activate) {
+        activate8(kf, true);
+        activate8(vf, false);
+      }
+      const float b = braw[j];
+      const float b16 = round_bf16(b);
+      float p[3][8], vb[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float prod = b * kf[i];  // exact for bf16 beta
+        const float hi = round_bf16(prod);
+        const float rem = prod - hi;  // exact
+        p[0][i] = hi;
+        if (kSplit == 2) {
+          p[1][i] = rem;  // representable in bf16 for bf16 beta
+        } else {
+          const float mid = round_bf16(rem);
+          p[1][i] = mid;
+          p[2][i] = rem - mid;
+        }
+        vb[i] = round_bf16(vf[i] * b16);
+      }
+      uint16_t* row0 = &lds[buf][0][r * kRow + c8];
+      *reinterpret_cast<u32x4*>(row0) = pack8(kf);
+#pragma unroll
+      for (int t = 0; t < kSplit; ++t)
+        *reinterpret_cast<u32x4*>(&lds[buf][1 + t][r * kRow + c8]) = pack8(p[t]);
+      *reinterpret_cast<u32x4*>(&lds[buf][1 + kSplit][r * kRow + c8]) = pack8(vb);
+    }
+  };
+
+  f32x4 accA[4][4], accB[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      accA[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      accB[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+  // transpose-read fragment: lane (g = lane/16, l = lane%16) gets tokens 8g..8g+7 of channel
+  // c0 + l. Both MFMA operands use this same token assignment, so every token pairs with
+  // itself whatever order the instruction consumes its K slots in.
+  const int g = lane >> 4;
+  const int tr_row = 8 * g + (lane16 >> 2);
+  const int tr_col = 4 * (lane16 & 3);
+  auto frag = [&](const uint16_t* tile, int c0) {
+    const bf16x4_t lo = lds_read_tr(tile + tr_row * kRow + c0 + tr_col);
+    const bf16x4_t hi = lds_read_tr(tile + (tr_row + 4) * kRow + c0 + tr_col);
+    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  };
+
+  load_step(0);
+  store_step(0);
+  __syncthreads();
+  for (int step = 0; step < steps; ++step) {
+    const int buf = step & 1;
+    const bool more = step + 1 < steps;
+    if (more) load_step(step + 1);
+    const uint16_t* tk = lds[buf][0];
+    const uint16_t* tv = lds[buf][1 + kSplit];
+    bf16x8 kn[4];  // K fragments for this wave's column blocks (B' operand B)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) kn[nt] = frag(tk, wn * 64 + nt * 16);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const bf16x8 km = frag(tk, wm * 64 + mt * 16);
+      const bf16x8 vm = frag(tv, wm * 64 + mt * 16);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+#pragma unroll
+        for (int t = 0; t < kSplit; ++t) {
+          const bf16x8 pn = frag(lds[buf][1 + t], wn * 64 + nt * 16);
+          accA[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(km, pn, accA[mt][nt], 0, 0, 0);
+        }
+        accB[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vm, kn[nt], accB[mt][nt], 0, 0, 0);
+      }
+    }
+    if (more) store_step(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: A = (A' + A'ᵀ) / 2 through LDS; B rounded to bf16 ----
+  float* sA = reinterpret_cast<float*>(&lds[0][0][0]);  // [128][129] fp32 (66 KB, fits)
+  constexpr int kLd = 129;
+  const int row_base = (lane >> 4) * 4;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int i = wm * 64 + mt * 16 + row_base + v;
+        const int j = wn * 64 + nt * 16 + lane16;
+        sA[i * kLd + j] = accA[mt][nt][v];
+      }
+  __syncthreads();
+  float* An = A + static_cast<int64_t>(fh) * kD * kD;
+  for (int idx = tid; idx < kD * kD; idx += 256) {
+    const int i = idx >> 7, j = idx & 127;
+    An[idx] = (sA[i * kLd + j] + sA[j * kLd + i]) * 0.5f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int i = wm * 64 + mt * 16 + row_base + v;
+        const int j = wn * 64 + nt * 16 + lane16;
+        sA[i * kLd + j] = round_bf16(accB[mt][nt][v]);
+      }
+  __syncthreads();
+  float* Bn = B + static_cast<int64_t>(fh) * kD * kD;
+  for (int idx = tid; idx < kD * kD; idx += 256) Bn[idx] = sA[(idx >> 7) * kLd + (idx & 127)];
+}
+
+// ------------------------------------------------------------------- factors ----
+// One workgroup per matrix. Thread (ti, tj) = (tid / 16, tid % 16) keeps the 8x8 block
+// rows 8ti.., cols 8tj.. of M = I + A in registers; Gauss-Jordan without pivoting (I + A is
+// SPD, every pivot is >= 1), one pivot per step, pivot row/column broadcast through a
+// double-buffered LDS line so each step needs a single barrier.
+__global__ void __launch_bounds__(256, 2)
+vda_factors_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                   const float* __restrict__ alpha, float* __restrict__ T,
+                   float* __restrict__ J) {
+  __shared__ float prow[2][kD], pcol[2][kD];
+  __shared__ __attribute__((aligned(16))) float minv[kD * (kD + 4)];
+  constexpr int kLd = kD + 4;
+  const int64_t mat = static_cast<int64_t>(blockIdx.x) * kD * kD;
+  const int tid = threadIdx.x, ti = tid >> 4, tj = tid & 15;
+  const int i0 = ti * 8, j0 = tj * 8;
+  float m[8][8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(A + mat + (i0 + r) * kD + j0);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(A + mat + (i0 + r) * kD + j0 + 4);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      m[r][c] = a[c];
+      m[r][c + 4] = b[c];
+    }
+  }
+  if (ti == tj) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r) m[r][r] += 1.0f;
+  }
+#pragma unroll 1
+  for (int k = 0; k < kD; ++k) {
+    const int buf = k & 1, kb = k >> 3, kr = k & 7;
+    if (ti == kb) {
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+        if (r == kr) {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) prow[buf][j0 + c] = m[r][c];
+        }
+    }
+    if (tj == kb) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        if (c == kr) {
+#pragma unroll
+          for (int r = 0; r < 8; ++r) pcol[buf][i0 + r] = m[r][c];
+        }
+    }
+    __syncthreads();
+    const float rp = 1.0f / prow[buf][k];
+    float pr[8], pc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) pr[c] = prow[buf][j0 + c] * rp;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) pc[r] = pcol[buf][i0 + r];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const bool pivot_row = (i0 + r) == k;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const bool pivot_col = (j0 + c) == k;
+        const float upd = m[r][c] - pc[r] * pr[c];
+        const float col = -pc[r] * rp;
+        m[r][c] = pivot_row ? (pivot_col ? rp : pr[c]) : (pivot_col ? col : upd);
+      }
+    }
+  }
+  // T = diag(alpha) M^-1 (row i scaled by alpha[i]); M^-1 staged in LDS for J = B M^-1.
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const float a = alpha != nullptr ? alpha[static_cast<int64_t>(blockIdx.x) * kD + i0 + r] : 1.0f;
+    f32x4 lo, hi;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      lo[c] = a * m[r][c];
+      hi[c] = a * m[r][c + 4];
+    }
+    *reinterpret_cast<f32x4*>(T + mat + (i0 + r) * kD + j0) = lo;
+    *reinterpret_cast<f32x4*>(T + mat + (i0 + r) * kD + j0 + 4) = hi;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      lo[c] = m[r][c];
+      hi[c] = m[r][c + 4];
+    }
+    *reinterpret_cast<f32x4*>(&minv[(i0 + r) * kLd + j0]) = lo;
+    *reinterpret_cast<f32x4*>(&minv[(i0 + r) * kLd + j0 + 4]) = hi;
+  }
+  __syncthreads();
+  float acc[8][8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[r][c] = 0.f;
+  const float* Bn = B + mat + i0 * kD;
+#pragma unroll 1
+  for (int k = 0; k < kD; k += 4) {
+    f32x4 brow[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) brow[r] = *reinterpret_cast<const f32x4*>(Bn + r * kD + k);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(&minv[(k + kk) * kLd + j0]);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(&minv[(k + kk) * kLd + j0 + 4]);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const float bv = brow[r][kk];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          acc[r][c] = fmaf(bv, x0[c], acc[r][c]);
+          acc[r][c + 4] = fmaf(bv, x1[c], acc[r][c + 4]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    f32x4 lo, hi;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      lo[c] = acc[r][c];
+      hi[c] = acc[r][c + 4];
+    }
+    *reinterpret_cast<f32x4*>(J + mat + (i0 + r) * kD + j0) = lo;
+    *reinterpret_cast<f32x4*>(J + mat + (i0 + r) * kD + j0 + 4) = hi;
+  }
+}
+
+// --------------------------------------------------------- affine recurrence ----
+// state[16 x 128] <- state @ T + J over a sequence of frames. Workgroup = (row block of 16
+// state rows, head, direction[, chunk]); 4 waves, wave w owns output columns [32w, 32w+32).
+// state @ T runs on v_mfma_f32_16x16x4_f32: lane l feeds A = state[l%16][4k + l/16] and
+// B = T[4k + l/16][n0 + l%16]; the accumulator holds rows (l/16)*4 + v, column l%16.
+enum RecurMode : int { kScan = 0, kCompose = 1 };
+
+template <int kMode>
+__global__ void __launch_bounds__(256)
+vda_recur_kernel(const float* __restrict__ Tm, const float* __restrict__ Jm, int heads,
+                 const int* __restrict__ starts, const int* __restrict__ ends, int chunks,
+                 const float* __restrict__ seed, int per_direction, float* __restrict__ out0,
+                 float* __restrict__ out1) {
+  __shared__ __attribute__((aligned(16))) float sT[kD * kD];      // 64 KB
+  // state rows; compose keeps a second state (the accumulated injection b)
+  __shared__ __attribute__((aligned(16))) float sS[kMode == kCompose ? 2 : 1][16 * 132];
+  const int rb = blockIdx.x;  // 16-row block
+  const int dir = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r0 = rb * 16;
+  int h, c = 0;
+  if (kMode == kScan) {
+    h = blockIdx.y;
+  } else {
+    h = blockIdx.y % heads;
+    c = blockIdx.y / heads;
+  }
+  const int64_t mat = kD * kD;
+  // number of frames in the sequence and the frame index of step t
+  int n_steps, lo = 0, hi = 0;
+  if (kMode == kScan) {
+    n_steps = chunks;
+  } else {
+    lo = starts[c];
+    hi = ends[c];
+    n_steps = hi - lo;
+  }
+  auto frame_of = [&](int t) {
+    if (kMode == kScan) return dir == 0 ? t : chunks - 1 - t;
+    return dir == 0 ? lo + t : hi - 1 - t;
+  };
+  // input matrix of frame/chunk x for head h: per-direction composed maps [2, C, H] or
+  // per-frame factors [F, H] shared by both directions; scan outputs are always [2, C, H].
+  auto in_index = [&](int x) -> int64_t {
+    if (kMode == kScan && per_direction) return (static_cast<int64_t>(dir) * chunks + x) * heads + h;
+    return static_cast<int64_t>(x) * heads + h;
+  };
+  auto out_index = [&](int x) -> int64_t {
+    return (static_cast<int64_t>(dir) * chunks + x) * heads + h;
+  };
+  // initial state: scan -> seed or zero; compose -> m = I (sS[0]), b = 0 (sS[1])
+  for (int idx = tid; idx < 16 * kD; idx += 256) {
+    const int i = idx >> 7, j = idx & 127;
+    float s0;
+    if (kMode == kScan) {
+      s0 = seed != nullptr ? seed[(static_cast<int64_t>(h) * kD + r0 + i) * kD + j] : 0.f;
+    } else {
+      s0 = (r0 + i) == j ? 1.f : 0.f;
+      sS[kMode == kCompose ? 1 : 0][i * 132 + j] = 0.f;
+    }
+    sS[0][i * 132 + j] = s0;
+  }
+  const int n0 = wave * 32;
+  const int frow = lane & 15, fk = lane >> 4;
+  for (int t = 0; t < n_steps; ++t) {
+    const int x = frame_of(t);
+    const float* Tx = Tm + in_index(x) * mat;
+    const float* Jx = Jm + in_index(x) * mat;
+    __syncthreads();  // previous step finished reading sT / writing sS
+    for (int idx = tid * 4; idx < kD * kD; idx += 256 * 4)
+      *reinterpret_cast<f32x4*>(&sT[idx]) = *reinterpret_cast<const f32x4*>(Tx + idx);
+    __syncthreads();
+    f32x4 acc[2][2];  // [state m / b][n tile]
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) acc[a][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    constexpr int kStates = kMode == kCompose ? 2 : 1;
+#pragma unroll 8
+    for (int kk = 0; kk < kD / 4; ++kk) {
+      const int krow = 4 * kk + fk;
+      const float b0 = sT[krow * kD + n0 + frow];
+      const float b1 = sT[krow * kD + n0 + 16 + frow];
+#pragma unroll
+      for (int a = 0; a < kStates; ++a) {
+        const float av = sS[a][frow * 132 + krow];
+        acc[a][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b0, acc[a][0], 0, 0, 0);
+        acc[a][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b1, acc[a][1], 0, 0, 0);
+      }
+    }
+    __syncthreads();  // all waves done reading sS before it is overwritten
+    // the injection is added to the b state (compose) or the only state (scan)
+    const int inj = kMode == kCompose ? 1 : 0;
+#pragma unroll
+    for (int a = 0; a < kStates; ++a)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int i = (lane >> 4) * 4 + v;
+          const int j = n0 + nt * 16 + frow;
+          float y = acc[a][nt][v];
+          if (a == inj) y += Jx[(r0 + i) * kD + j];
+          sS[a][i * 132 + j] = y;
+          if (kMode == kScan) out0[out_index(x) * mat + (r0 + i) * kD + j] = y;
+        }
+  }
+  if (kMode == kCompose) {
+    __syncthreads();
+    const int64_t o = ((static_cast<int64_t>(dir) * chunks + c) * heads + h) * mat;
+    for (int idx = tid; idx < 16 * kD; idx += 256) {
+      const int i = idx >> 7, j = idx & 127;
+      out0[o + (r0 + i) * kD + j] = sS[0][i * 132 + j];
+      out1[o + (r0 + i) * kD + j] = sS[1][i * 132 + j];
+    }
+  }
+}
+
+// ----------------------------------------------------------------- log prefix ----
+// logp[n, h, j] = sum_{u < n} log(max(alpha[u, h, j], 1e-12)), summed in frame order.
+__global__ void vda_log_prefix_kernel(const float* __restrict__ alpha, int frames, int hd,
+                                      float* __restrict__ logp) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= hd) return;
+  float acc = 0.f;
+  logp[idx] = 0.f;
+  for (int n = 0; n < frames; ++n) {
+    acc += logf(fmaxf(alpha[static_cast<int64_t>(n) * hd + idx], 1e-12f));
+    logp[static_cast<int64_t>(n + 1) * hd + idx] = acc;
+  }
+}
+
+// -------------------------------------------------------------------- gather ----
+// out[f, h, i, j] = P[before f][h][i][j] * exp(lp[f+1] - lp[bb f])[j]
+//                 + R[after f][h][i][j]  * exp(lp[ba f] - lp[f])[j]
+// with out-of-range sides reading the text seed (or zero). paper_sglang.py:445-501.
+__global__ void __launch_bounds__(256)
+vda_gather_kernel(const float* __restrict__ prefix, const float* __restrict__ suffix,
+                  const float* __restrict__ logp, const float* __restrict__ text,
+                  const int* __restrict__ before, const int* __restrict__ after,
+                  const int* __restrict__ has_b, const int* __restrict__ has_a,
+                  const int* __restrict__ bridge_b, const int* __restrict__ bridge_a, int heads,
+                  int bridge, int out_f32, void* __restrict__ out) {
+  const int f = blockIdx.x, h = blockIdx.y;
+  const int64_t mat = kD * kD;
+  const int fb = before[f], fa = after[f];
+  const bool hb = has_b[f] != 0, ha = has_a[f] != 0;
+  const int64_t hd = static_cast<int64_t>(heads) * kD;
+  for (int idx = threadIdx.x + blockIdx.z * 256; idx < kD * kD; idx += 256 * gridDim.z) {
+    const int j = idx & 127;
+    float sb, sa;
+    const float ts = text != nullptr ? text[h * mat + idx] : 0.f;
+    sb = hb ? prefix[(static_cast<int64_t>(fb) * heads + h) * mat + idx] : ts;
+    sa = ha ? suffix[(static_cast<int64_t>(fa) * heads + h) * mat + idx] : ts;
+    if (bridge) {
+      const float lt1 = logp[(f + 1) * hd + h * kD + j];
+      const float lt = logp[f * hd + h * kD + j];
+      const float lbb = logp[bridge_b[f] * hd + h * kD + j];
+      const float lba = logp[bridge_a[f] * hd + h * kD + j];
+      sb = sb * expf(lt1 - lbb);
+      sa = sa * expf(lba - lt);
+    }
+    const float y = sb + sa;
+    const int64_t o = (static_cast<int64_t>(f) * heads + h) * mat + idx;
+    if (out_f32)
+      static_cast<float*>(out)[o] = y;
+    else
+      static_cast<uint16_t*>(out)[o] = f32_to_bf16_bits(y);
+  }
+}
+
+// ------------------------------------------------------------ readout + norm ----
+// RMSNorm(d)·w·gate of 8 channels held by one lane of a 16-lane token group
+// (paper_sglang.py:398-403): y * (1 / sqrt(mean(y^2) + eps)) * w * g, fp32, one rounding.
+__device__ __forceinline__ void norm_gate_store8(float* y, const float* w, const uint16_t* gsrc,
+                                                 uint16_t* dst, float eps) {
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss += y[i] * y[i];
+  ss = sum16(ss);
+  const float inv = 1.0f / sqrtf(ss / static_cast<float>(kD) + eps);
+  float gv[8];
+  unpack8(*reinterpret_cast<const u32x4*>(gsrc), gv);
+  float o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = y[i] * inv * w[i] * gv[i];
+  *reinterpret_cast<u32x4*>(dst) = pack8(o);
+}
+
+// Fused readout: per (frame, head, 64-token tile): q' = bf16(L2(SiLU(q_raw))) (optional),
+// y = bf16(q' · stateᵀ) on bf16 MFMA, then RMSNorm·w·gate into out[f*S + s, h*D + c].
+constexpr int kQT = 64;
+constexpr int kQRow = 136;  // padded bf16 row (272 bytes)
+
+__global__ void __launch_bounds__(256, 2)
+vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
+                   const void* __restrict__ weight, int weight_f32, float eps, View gv,
+                   uint16_t* __restrict__ out, int64_t o_sf, int64_t o_sh, int64_t o_ss,
+                   int spatial, int heads, int tiles) {
+  __shared__ __attribute__((aligned(16))) uint16_t sState[kD * kQRow];  // [v][k]
+  __shared__ __attribute__((aligned(16))) uint16_t sQ[kQT * kQRow];     // [token][k], then y
+  const int tile = blockIdx.x % tiles;
+  const int fh = blockIdx.x / tiles;
+  const int f = fh / heads, h = fh % heads;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lane16 = tid & 15;
+  const int s0 = tile * kQT;
+  const uint16_t* st = state + static_cast<int64_t>(fh) * kD * kD;
+  for (int idx = tid * 8; idx < kD * kD; idx += 256 * 8)
+    *reinterpret_cast<u32x4*>(&sState[(idx >> 7) * kQRow + (idx & 127)]) =
+        *reinterpret_cast<const u32x4*>(st + idx);
+  // q tile: 16 tokens per pass (one 16-lane group per token)
+#pragma unroll
+  for (int pass = 0; pass < kQT / 16; ++pass) {
+    const int r = pass * 16 + (tid >> 4);
+    const int s = s0 + r;
+    float v[8];
+    if (s < spatial) {
+      unpack8(*reinterpret_cast<const u32x4*>(qv.at(f, h, s) + lane16 * 8), v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = 0.f;
+    }
+    if (activate_q) activate8(v, true);
+    *reinterpret_cast<u32x4*>(&sQ[r * kQRow + lane16 * 8]) = pack8(v);
+  }
+  __syncthreads();
+  // wave w: tokens [16w, 16w+16) x all 128 outputs; K = 128 in 4 steps of 32
+  f32x4 acc[8];
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int g = lane >> 4;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int kc = ks * 32 + g * 8;
+    const bf16x8 a = *reinterpret_cast<const bf16x8*>(&sQ[(wave * 16 + lane16) * kQRow + kc]);
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(&sState[(nt * 16 + lane16) * kQRow + kc]);
+      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[nt], 0, 0, 0);
+    }
+  }
+  __syncthreads();  // every wave is done with sQ as the q tile
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      sQ[(wave * 16 + g * 4 + v) * kQRow + nt * 16 + lane16] = f32_to_bf16_bits(acc[nt][v]);
+  __syncthreads();
+  float w[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    w[i] = weight_f32 ? static_cast<const float*>(weight)[lane16 * 8 + i]
+                      : bf16_bits_to_f32(static_cast<const uint16_t*>(weight)[lane16 * 8 + i]);
+#pragma unroll
+  for (int pass = 0; pass < kQT / 16; ++pass) {
+    const int r = pass * 16 + (tid >> 4);
+    const int s = s0 + r;
+    if (s >= spatial) continue;  // uniform per 16-lane group
+    float y[8];
+    unpack8(*reinterpret_cast<const u32x4*>(&sQ[r * kQRow + lane16 * 8]), y);
+    norm_gate_store8(y, w, gv.at(f, h, s) + lane16 * 8,
+                     out + f * o_sf + h * o_sh + s * o_ss + lane16 * 8, eps);
+  }
+}
+
+// Epilogue alone (vdn_linear_epilogue): readout [F, H, S, D] bf16 -> out [F*S, H*D].
+__global__ void __launch_bounds__(256)
+vda_epilogue_kernel(const uint16_t* __restrict__ readout, const void* __restrict__ weight,
+                    int weight_f32, float eps, View gv, uint16_t* __restrict__ out,
+                    int64_t o_sf, int64_t o_sh, int64_t o_ss, int frames, int heads,
+                    int spatial) {
+  const int lane16 = threadIdx.x & 15;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  if (item >= static_cast<int64_t>(frames) * heads * spatial) return;
+  const int s = static_cast<int>(item % spatial);
+  const int fh = static_cast<int>(item / spatial);
+  const int f = fh / heads, h = fh % heads;
+  float y[8], w[8];
+  unpack8(*reinterpret_cast<const u32x4*>(readout + item * kD + lane16 * 8), y);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    w[i] = weight_f32 ? static_cast<const float*>(weight)[lane16 * 8 + i]
+                      : bf16_bits_to_f32(static_cast<const uint16_t*>(weight)[lane16 * 8 + i]);
+  norm_gate_store8(y, w, gv.at(f, h, s) + lane16 * 8,
+                   out + f * o_sf + h * o_sh + s * o_ss + lane16 * 8, eps);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+bool stride8(int64_t s) { return s % 8 == 0; }
+
+}  // namespace
+}  // namespace vdn
+
+using namespace vdn;
+
+// Reference: paper_stack.py:30-48 -> paper_sglang.py:211-283 (vdn_silu_l2norm, frame-major).
+VDN_API int vdn_vda_prepare(const void* tokens, int64_t n, int heads, int64_t row_stride,
+                            int64_t head_stride, int frames, int spatial, int l2norm, int is_f32,
+                            void* out, void* stream) {
+  const char* name = "vdn_vda_prepare";
+  if (tokens == nullptr || out == nullptr) return set_error(kInvalidArgument, "%s: null pointer", name);
+  if (n != static_cast<int64_t>(frames) * spatial || heads <= 0 || spatial <= 0)
+    return set_error(kInvalidArgument, "%s: tokens must be [frames*spatial, heads, 128]", name);
+  if (!is_f32 && (!aligned16(tokens) || !stride8(row_stride) || !stride8(head_stride)))
+    return set_error(kInvalidArgument, "%s: bf16 rows need 16-byte alignment", name);
+  if (n == 0) return kOk;
+  const int64_t items = n * heads;
+  auto st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>((items + 15) / 16));
+  if (is_f32)
+    hipLaunchKernelGGL(vda_prepare_kernel<true>, grid, dim3(256), 0, st, tokens, n, heads,
+                       row_stride, head_stride, spatial, l2norm, out);
+  else
+    hipLaunchKernelGGL(vda_prepare_kernel<false>, grid, dim3(256), 0, st, tokens, n, heads,
+                       row_stride, head_stride, spatial, l2norm, out);
+  return check_launch(name);
+}
+
+// Reference: paper_stack.py:51-110 (_joint_stats / paper_statistics; BF16 path), fed either
+// prepared [F,H,S,D] operands (activate = 0) or raw token-major projections with the
+// paper_prepare activation applied in registers (activate = 1).
+// Strides are in elements: operand (f, h, s, c) at base + f*sf + h*sh + s*ss + c.
+VDN_API int vdn_vda_statistics(const void* k, int64_t k_sf, int64_t k_sh, int64_t k_ss,
+                               const void* v, int64_t v_sf, int64_t v_sh, int64_t v_ss,
+                               const void* beta, int64_t b_sf, int64_t b_sh, int64_t b_ss,
+                               int beta_f32, int frames, int heads, int spatial, int activate,
+                               float* A, float* B, void* stream) {
+  const char* name = "vdn_vda_statistics";
+  if (k == nullptr || v == nullptr || beta == nullptr || A == nullptr || B == nullptr)
+    return set_error(kInvalidArgument, "%s: null pointer", name);
+  if (frames <= 0 || heads <= 0 || spatial <= 0)
+    return set_error(kInvalidArgument, "%s: positive frames/heads/spatial required", name);
+  if (!aligned16(k) || !aligned16(v) || !stride8(k_sf) || !stride8(k_sh) || !stride8(k_ss) ||
+      !stride8(v_sf) || !stride8(v_sh) || !stride8(v_ss))
+    return set_error(kInvalidArgument, "%s: k/v rows need 16-byte alignment", name);
+  auto st = static_cast<hipStream_t>(stream);
+  const View kv{static_cast<const uint16_t*>(k), k_sf, k_sh, k_ss};
+  const View vv{static_cast<const uint16_t*>(v), v_sf, v_sh, v_ss};
+  const dim3 grid(frames * heads);
+  if (beta_f32)
+    hipLaunchKernelGGL(vda_statistics_kernel<3>, grid, dim3(256), 0, st, kv, vv, beta, b_sf, b_sh,
+                       b_ss, 1, spatial, heads, activate, A, B);
+  else
+    hipLaunchKernelGGL(vda_statistics_kernel<2>, grid, dim3(256), 0, st, kv, vv, beta, b_sf, b_sh,
+                       b_ss, 0, spatial, heads, activate, A, B);
+  return check_launch(name);
+}
+
+// Reference: paper_factor.py:133-186 -> vdn_delta_factors (T = diag(alpha) (I+A)^-1,
+// J = B (I+A)^-1, fp32, no pivoting). alpha may be null (all ones).
+VDN_API int vdn_vda_factors(const float* A, const float* B, const float* alpha, int64_t count,
+                            float* T, float* J, void* stream) {
+  const char* name = "vdn_vda_factors";
+  if (A == nullptr || B == nullptr || T == nullptr || J == nullptr)
+    return set_error(kInvalidArgument, "%s: null pointer", name);
+  if (count < 0 || count > (1ll << 31) - 1) return set_error(kInvalidArgument, "%s: bad count", name);
+  if (!aligned16(A) || !aligned16(B) || !aligned16(T) || !aligned16(J))
+    return set_error(kInvalidArgument, "%s: matrices need 16-byte alignment", name);
+  if (count == 0) return kOk;
+  hipLaunchKernelGGL(vda_factors_kernel, dim3(static_cast<unsigned>(count)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), A, B, alpha, T, J);
+  return check_launch(name);
+}
+
+// Reference: paper_stack.py:162-181 (_compose): per chunk c and direction, CT = ordered
+// product of the chunk's transitions, CI = the chunk's accumulated injection.
+// T, J: [F, H, 128, 128]; starts/ends: int32 [chunks]; CT, CI: [2, chunks, H, 128, 128].
+VDN_API int vdn_vda_compose(const float* T, const float* J, int heads, const int* starts,
+                            const int* ends, int chunks, float* CT, float* CI, void* stream) {
+  const char* name = "vdn_vda_compose";
+  if (T == nullptr || J == nullptr || starts == nullptr || ends == nullptr || CT == nullptr ||
+      CI == nullptr)
+    return set_error(kInvalidArgument, "%s: null pointer", name);
+  if (heads <= 0 || chunks <= 0) return set_error(kInvalidArgument, "%s: bad geometry", name);
+  hipLaunchKernelGGL(vda_recur_kernel<kCompose>, dim3(kD / 16, heads * chunks, 2), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), T, J, heads, starts, ends, chunks,
+                     nullptr, 0, CT, CI);
+  return check_launch(name);
+}
+
+// Reference: paper_stack.py:184-199 (_scan_both): both directional scans over chunks.
+// per_direction = 1: CT, CI are [2, chunks, H, 128, 128] (composed maps); per_direction = 0:
+// CT, CI are per-frame factors [chunks, H, 128, 128] used by both directions (one-frame
+// chunks). bank: [2, chunks, H, 128, 128] fp32; seed (nullable): [H, 128, 128].
+VDN_API int vdn_vda_scan(const float* CT, const float* CI, const float* seed, int chunks,
+                         int heads, int per_direction, float* bank, void* stream) {
+  const char* name = "vdn_vda_scan";
+  if (CT == nullptr || CI == nullptr || bank == nullptr)
+    return set_error(kInvalidArgument, "%s: null pointer", name);
+  if (heads <= 0 || chunks <= 0) return set_error(kInvalidArgument, "%s: bad geometry", name);
+  hipLaunchKernelGGL(vda_recur_kernel<kScan>, dim3(kD / 16, heads, 2), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), CT, CI, heads, nullptr, nullptr, chunks,
+                     seed, per_direction, bank, nullptr);
+  return check_launch(name);
+}
+
+// Exclusive log-prefix of alpha over frames (paper_stack.py:256): logp [F+1, H, 128].
+VDN_API int vdn_vda_log_prefix(const float* alpha, int frames, int heads, float* logp,
+                               void* stream) {
+  if (alpha == nullptr || logp == nullptr)
+    return set_error(kInvalidArgument, "vdn_vda_log_prefix: null pointer");
+  const int hd = heads * kD;
+  hipLaunchKernelGGL(vda_log_prefix_kernel, dim3((hd + 255) / 256), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), alpha, frames, hd, logp);
+  return check_launch("vdn_vda_log_prefix");
+}
+
+// Reference: paper_stack.py:239-263 -> paper_sglang.py:445-501 (_gather_state_kernel) with
+// compact bank indices. prefix/suffix: [chunks, H, 128, 128] views of bank[0]/bank[1];
+// index arrays int32 [frames]; text (nullable) [H, 128, 128]; out [F, H, 128, 128].
+VDN_API int vdn_vda_gather(const float* prefix, const float* suffix, const float* logp,
+                           const float* text, const int* before, const int* after,
+                           const int* has_before, const int* has_after, const int* bridge_before,
+                           const int* bridge_after, int frames, int heads, int bridge,
+                           int out_f32, void* out, void* stream) {
+  const char* name = "vdn_vda_gather";
+  if (prefix == nullptr || suffix == nullptr || (bridge && logp == nullptr) || before == nullptr ||
+      after == nullptr || has_before == nullptr || has_after == nullptr || out == nullptr ||
+      (bridge && (bridge_before == nullptr || bridge_after == nullptr)))
+    return set_error(kInvalidArgument, "%s: null pointer", name);
+  if (frames <= 0 || heads <= 0) return set_error(kInvalidArgument, "%s: bad geometry", name);
+  hipLaunchKernelGGL(vda_gather_kernel, dim3(frames, heads, 8), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), prefix, suffix, logp, text, before, after,
+                     has_before, has_after, bridge_before, bridge_after, heads, bridge, out_f32,
+                     out);
+  return check_launch(name);
+}
+
+// Fused readout (paper_stack.py:317 torch.matmul + paper_sglang.py:377-437 epilogue), with
+// the q activation of paper_prepare applied in registers when activate_q = 1.
+// q: (f, h, s, c) at q + f*q_sf + h*q_sh + s*q_ss + c; gate likewise; out likewise.
+// state: bf16 [F, H, 128, 128] ([v][k]); weight [128] bf16 or fp32.
+VDN_API int vdn_vda_readout(const void* q, int64_t q_sf, int64_t q_sh, int64_t q_ss,
+                            int activate_q, const void* state, const void* weight, int weight_f32,
+                            float eps, const void* gate, int64_t g_sf, int64_t g_sh, int64_t g_ss,
+                            void* out, int64_t o_sf, int64_t o_sh, int64_t o_ss, int frames,
+                            int heads, int spatial, void* stream) {
+  const char* name = "vdn_vda_readout";
+  if (q == nullptr || state == nullptr || weight == nullptr || gate == nullptr || out == nullptr)
+    return set_error(kInvalidArgument, "%s: null pointer", name);
+  if (frames <= 0 || heads <= 0 || spatial <= 0)
+    return set_error(kInvalidArgument, "%s: bad geometry", name);
+  if (!aligned16(q) || !aligned16(gate) || !aligned16(out) || !aligned16(state) ||
+      !stride8(q_sf) || !stride8(q_sh) || !stride8(q_ss) || !stride8(g_sf) || !stride8(g_sh) ||
+      !stride8(g_ss) || !stride8(o_sf) || !stride8(o_sh) || !stride8(o_ss))
+    return set_error(kInvalidArgument, "%s: operands need 16-byte aligned rows", name);
+  const int tiles = (spatial + kQT - 1) / kQT;
+  const View qv{static_cast<const uint16_t*>(q), q_sf, q_sh, q_ss};
+  const View gv{static_cast<const uint16_t*>(gate), g_sf, g_sh, g_ss};
+  hipLaunchKernelGGL(vda_readout_kernel, dim3(frames * heads * tiles), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), qv, activate_q,
+                     static_cast<const uint16_t*>(state), weight, weight_f32, eps, gv,
+                     static_cast<uint16_t*>(out), o_sf, o_sh, o_ss, spatial, heads, tiles);
+  return check_launch(name);
+}
+
+// Reference: paper_sglang.py:377-437 (_linear_epilogue_kernel / vdn_linear_epilogue):
+// readout [F, H, S, 128] bf16 contiguous -> RMSNorm(d)·w·gate -> out.
+VDN_API int vdn_vda_epilogue(const void* readout, const void* weight, int weight_f32, float eps,
+                             const void* gate, int64_t g_sf, int64_t g_sh, int64_t g_ss,
+                             void* out, int64_t o_sf, int64_t o_sh, int64_t o_ss, int frames,
+                             int heads, int spatial, void* stream) {
+  const char* name = "vdn_vda_epilogue";
+  if (readout == nullptr || weight == nullptr || gate == nullptr || out == nullptr)
+    return set_error(kInvalidArgument, "%s: null pointer", name);
+  if (frames <= 0 || heads <= 0 || spatial <= 0)
+    return set_error(kInvalidArgument, "%s: bad geometry", name);
+  const int64_t items = static_cast<int64_t>(frames) * heads * spatial;
+  const View gv{static_cast<const uint16_t*>(gate), g_sf, g_sh, g_ss};
+  hipLaunchKernelGGL(vda_epilogue_kernel, dim3(static_cast<unsigned>((items + 15) / 16)),
+                     dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(readout), weight, weight_f32, eps, gv,
+                     static_cast<uint16_t*>(out), o_sf, o_sh, o_ss, frames, heads, spatial);
+  return check_launch(name);
+}

@@ -1,0 +1,420 @@
+"""VDA (frame-wise delta-rule linear attention) operators with the reference's signatures.
+
+Mirrors src/models/linear_attention/paper_stack.py (paper_prepare, paper_statistics,
+BoundaryPlan / paper_boundary_plan, paper_boundary_scan, paper_gather, paper_readout),
+paper_factor.py (paper_delta_factors) and paper_sglang.py (vdn_linear_epilogue). Every
+device step runs in libvdnmi.so; there is no eager or Triton fallback.
+
+Two fused entry points have no single reference counterpart but compute exactly what the
+reference chain computes, without the intermediate frame-major copies:
+  statistics_from_projections  paper_prepare(k), paper_prepare(v) + paper_statistics
+  linear_readout               paper_prepare(q) + q @ stateᵀ + vdn_linear_epilogue
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from functools import lru_cache
+
+import torch
+
+from . import _lib
+
+HEAD_DIM = 128
+
+
+def _cuda(t, name, dtype=None):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda or (dtype is not None and t.dtype != dtype):
+        raise ValueError(f"{name} must be CUDA {dtype or 'floating point'}")
+    if t.requires_grad:
+        raise ValueError(f"{name}: paper stack is inference only")
+
+
+def _stream(t):
+    return _lib.stream(t.device)
+
+
+# -------------------------------------------------------------------- prepare ----
+
+def paper_prepare(tokens, *, frames, spatial, l2norm, conv=None, proj=None, frame_size=None):
+    """Raw [F*S, H, D] -> contiguous [F, H, S, D]: SiLU (+ L2 over D) (paper_stack.py:30-48)."""
+    _cuda(tokens, "tokens")
+    if tokens.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("paper_prepare supports BF16/FP32")
+    if tokens.ndim != 3 or tokens.shape[0] != frames * spatial or min(frames, spatial) < 1:
+        raise ValueError("tokens must be [frames*spatial, heads, dim] with positive sizes")
+    if conv is not None and proj in getattr(conv, "projs", ()):
+        raise NotImplementedError("short convolution is not part of this build's hot path")
+    n, h, d = tokens.shape
+    if d != HEAD_DIM:
+        raise ValueError("head_dim 128 required")
+    if tokens.stride(-1) != 1:
+        tokens = tokens.contiguous()
+    out = torch.empty((frames, h, spatial, d), dtype=tokens.dtype, device=tokens.device)
+    _lib.call("vdn_vda_prepare", tokens.data_ptr(), n, h, tokens.stride(0), tokens.stride(1),
+              frames, spatial, int(bool(l2norm)), int(tokens.dtype == torch.float32),
+              out.data_ptr(), _stream(tokens))
+    return out
+
+
+# ----------------------------------------------------------------- statistics ----
+
+def _stats_call(k, k_strides, v, v_strides, beta, b_strides, frames, heads, spatial, activate,
+                a=None, b=None):
+    if a is None:
+        a = torch.empty((frames, heads, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=k.device)
+        b = torch.empty_like(a)
+    _lib.call("vdn_vda_statistics", k.data_ptr(), *k_strides, v.data_ptr(), *v_strides,
+              beta.data_ptr(), *b_strides, int(beta.dtype == torch.float32), frames, heads,
+              spatial, activate, a.data_ptr(), b.data_ptr(), _stream(k))
+    return a, b
+
+
+def paper_statistics(key, value, beta):
+    """Joint A/B statistics of prepared [F,H,S,D] K/V and [F,H,S] beta (paper_stack.py:86-110).
+
+    A = (Kᵀ diag(β) K + transpose)/2 in fp32-grade arithmetic; B = bf16(bf16(v·β)ᵀ k) for
+    bf16 K/V. Both returned as fp32 [F,H,D,D].
+    """
+    for name, t in (("key", key), ("value", value), ("beta", beta)):
+        _cuda(t, name)
+    if (key.ndim != 4 or value.shape != key.shape or beta.shape != key.shape[:-1]
+            or value.dtype != key.dtype or key.dtype not in (torch.bfloat16, torch.float32)
+            or beta.dtype not in (torch.bfloat16, torch.float32)
+            or any(t.device != key.device or not t.is_contiguous() for t in (value, beta, key))):
+        raise ValueError("joint statistics require contiguous compatible F,H,S,D inputs")
+    f, h, s, d = key.shape
+    if min(f, h, s) < 1 or d not in (16, 32, 64, 128):
+        raise ValueError("positive F,H,S and D in 16,32,64,128 required")
+    if d != HEAD_DIM or key.dtype != torch.bfloat16:
+        raise NotImplementedError("the gfx950 statistics kernel takes bf16 K/V with D = 128")
+    ks = (h * s * d, s * d, d)
+    bs = (h * s, s, 1)
+    return _stats_call(key, ks, value, ks, beta, bs, f, h, s, 0)
+
+
+def statistics_from_projections(k_raw, v_raw, beta, frames, spatial, a=None, b=None):
+    """A/B statistics straight from raw token-major projections.
+
+    k_raw, v_raw: [F*S, H, D] bf16 views (any row/head stride, unit channel stride), the
+    pre-activation K/V of the shared QKV projection; beta: [F*S, H]. Equivalent to
+    paper_statistics(paper_prepare(k, l2norm=True), paper_prepare(v, l2norm=False), beta
+    reshaped to [F,H,S]); `a`/`b` may be preallocated [F,H,D,D] fp32 outputs.
+    """
+    for name, t in (("k_raw", k_raw), ("v_raw", v_raw), ("beta", beta)):
+        _cuda(t, name)
+    n, h, d = k_raw.shape
+    if (v_raw.shape != k_raw.shape or d != HEAD_DIM or n != frames * spatial
+            or beta.shape != (n, h) or k_raw.dtype != torch.bfloat16 or v_raw.dtype != torch.bfloat16
+            or k_raw.stride(-1) != 1 or v_raw.stride(-1) != 1):
+        raise ValueError("expected bf16 [frames*spatial, H, 128] projections and [F*S, H] beta")
+    ks = (spatial * k_raw.stride(0), k_raw.stride(1), k_raw.stride(0))
+    vs = (spatial * v_raw.stride(0), v_raw.stride(1), v_raw.stride(0))
+    bs = (spatial * beta.stride(0), beta.stride(1), beta.stride(0))
+    return _stats_call(k_raw, ks, v_raw, vs, beta, bs, frames, h, spatial, 1, a, b)
+
+
+# -------------------------------------------------------------------- factors ----
+
+def _check_factor_tensor(t, name):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.dtype != torch.float32:
+        raise TypeError(f"{name} must have dtype float32, got {t.dtype}")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a CUDA tensor")
+    if t.layout != torch.strided or not t.is_contiguous():
+        raise ValueError(f"{name} must have contiguous strided storage")
+    if t.requires_grad:
+        raise ValueError(f"{name} requires_grad is unsupported by this inference-only kernel")
+
+
+def _aligned(t):
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def paper_delta_factors(A, B, alpha=None):
+    """(diag(alpha) @ inv(I + A), B @ inv(I + A)) for [..., 128, 128] fp32 (paper_factor.py:133-186)."""
+    _check_factor_tensor(A, "A")
+    _check_factor_tensor(B, "B")
+    if A.ndim < 2 or A.shape[-2:] != (HEAD_DIM, HEAD_DIM):
+        raise ValueError("A must have shape [..., 128, 128]")
+    if B.shape != A.shape:
+        raise ValueError("B shape must exactly equal A shape")
+    if B.device != A.device:
+        raise ValueError("A and B must be on the same CUDA device")
+    if alpha is not None:
+        _check_factor_tensor(alpha, "alpha")
+        if alpha.shape != A.shape[:-1]:
+            raise ValueError("alpha must have exact shape [..., 128] matching A")
+        if alpha.device != A.device:
+            raise ValueError("alpha must be on the same CUDA device as A")
+    transition, injection = torch.empty_like(A), torch.empty_like(B)
+    if A.numel() == 0:
+        return transition, injection
+    n = A.numel() // (HEAD_DIM * HEAD_DIM)
+    A, B = _aligned(A), _aligned(B)
+    al = None if alpha is None else _aligned(alpha)
+    _lib.call("vdn_vda_factors", A.data_ptr(), B.data_ptr(), _lib.ptr(al), n,
+              transition.data_ptr(), injection.data_ptr(), _stream(A))
+    return transition, injection
+
+
+# ------------------------------------------------------------- boundary plan ----
+
+@dataclass(frozen=True)
+class BoundaryPlan:
+    frames: int
+    cuts: tuple
+    starts: torch.Tensor
+    ends: torch.Tensor
+    before: torch.Tensor
+    after: torch.Tensor
+    has_before: torch.Tensor
+    has_after: torch.Tensor
+    bridge_before: torch.Tensor
+    bridge_after: torch.Tensor
+
+    @property
+    def chunks(self):
+        return len(self.cuts) - 1
+
+
+@lru_cache(maxsize=64)
+def _boundary_plan(bounds, frames, chunk_size, device):
+    """Compact boundary plan (paper_stack.py:131-154): chunk cut points are every window edge
+    plus splits every `chunk_size` frames between edges; each frame reads the prefix bank of
+    the chunk ending at its window start and the suffix bank of the chunk starting after it."""
+    if frames < 1 or len(bounds) != frames or chunk_size < 1:
+        raise ValueError("positive frames/chunk_size and one bound per frame required")
+    edges = {0, frames}
+    for f, (lo, hi) in enumerate(bounds):
+        if not lo <= f <= hi:
+            raise ValueError("each inclusive window must contain its query frame")
+        edges.add(max(0, lo))
+        edges.add(min(frames, hi + 1))
+    ordered = sorted(edges)
+    cuts = set(ordered)
+    for a, b in zip(ordered[:-1], ordered[1:]):
+        cuts.update(range(a + chunk_size, b, chunk_size))
+    cuts = tuple(sorted(cuts))
+    index = {x: i for i, x in enumerate(cuts)}
+    last_chunk = len(cuts) - 2
+
+    def i32(values):
+        return torch.tensor(values, dtype=torch.int32, device=device)
+
+    return BoundaryPlan(
+        frames, cuts, i32(cuts[:-1]), i32(cuts[1:]),
+        i32([max(0, index[max(0, lo)] - 1) for lo, _ in bounds]),
+        i32([min(last_chunk, index[min(frames, hi + 1)]) for _, hi in bounds]),
+        i32([int(lo > 0) for lo, _ in bounds]),
+        i32([int(hi + 1 < frames) for _, hi in bounds]),
+        i32([max(0, lo) for lo, _ in bounds]),
+        i32([min(frames, hi + 1) for _, hi in bounds]))
+
+
+def paper_boundary_plan(bounds, frames, device, chunk_size=8):
+    return _boundary_plan(tuple(tuple(int(x) for x in b) for b in bounds), int(frames),
+                          int(chunk_size), str(device))
+
+
+# ----------------------------------------------------------------------- scan ----
+
+def paper_boundary_scan(transitions, injections, plan, text_state=None):
+    """Chunk composition, then both directional scans: bank [2, C, H, D, D] fp32
+    (paper_stack.py:202-236). bank[0, c] is the forward state after chunk c; bank[1, c] the
+    reverse state after chunk c (i.e. covering frames cuts[c]..F-1)."""
+    _cuda(transitions, "transitions", torch.float32)
+    _cuda(injections, "injections", torch.float32)
+    if (transitions.ndim != 4 or transitions.shape != injections.shape
+            or transitions.device != injections.device
+            or not transitions.is_contiguous() or not injections.is_contiguous()):
+        raise ValueError("matching contiguous FP32 [F,H,D,D] factors required")
+    f, h, d, dk = transitions.shape
+    if f != plan.frames or d != dk or d not in (16, 32, 64, 128) or h < 1:
+        raise ValueError("factor geometry incompatible with boundary plan")
+    if d != HEAD_DIM:
+        raise NotImplementedError("the gfx950 scan kernel takes D = 128")
+    if plan.starts.device != transitions.device:
+        raise ValueError("plan and factors must share a device")
+    if text_state is not None:
+        _cuda(text_state, "text_state", torch.float32)
+        if text_state.shape != (h, d, d) or text_state.device != transitions.device:
+            raise ValueError("text_state must be head-local H,D,D")
+        text_state = text_state.contiguous()
+    shape = (2, plan.chunks, h, d, d)
+    bank = transitions.new_empty(shape)
+    stream = _stream(transitions)
+    if plan.chunks == f:
+        # every chunk is one frame: both directions scan the frame factors themselves
+        _lib.call("vdn_vda_scan", transitions.data_ptr(), injections.data_ptr(),
+                  _lib.ptr(text_state), plan.chunks, h, 0, bank.data_ptr(), stream)
+        return bank
+    ct = transitions.new_empty(shape)
+    ci = transitions.new_empty(shape)
+    _lib.call("vdn_vda_compose", transitions.data_ptr(), injections.data_ptr(), h,
+              plan.starts.data_ptr(), plan.ends.data_ptr(), plan.chunks, ct.data_ptr(),
+              ci.data_ptr(), stream)
+    _lib.call("vdn_vda_scan", ct.data_ptr(), ci.data_ptr(), _lib.ptr(text_state), plan.chunks,
+              h, 1, bank.data_ptr(), stream)
+    return bank
+
+
+# --------------------------------------------------------------------- gather ----
+
+def paper_gather(bank, alpha, plan, text_state=None, out_dtype=torch.bfloat16, bridge=True):
+    """Alpha-bridged boundary gather [F, H, D, D] (paper_stack.py:239-263)."""
+    _cuda(bank, "bank", torch.float32)
+    _cuda(alpha, "alpha", torch.float32)
+    if bank.ndim != 5 or bank.shape[:2] != (2, plan.chunks):
+        raise ValueError("bank must be [2,chunks,H,D,D]")
+    _, _, h, d, dk = bank.shape
+    if (d != dk or alpha.shape != (plan.frames, h, d) or not bank.is_contiguous()
+            or alpha.device != bank.device or plan.starts.device != bank.device
+            or out_dtype not in (torch.bfloat16, torch.float32)):
+        raise ValueError("gather geometry/device/dtype mismatch")
+    if d != HEAD_DIM:
+        raise NotImplementedError("the gfx950 gather kernel takes D = 128")
+    if text_state is not None:
+        _cuda(text_state, "text_state", torch.float32)
+        if text_state.shape != (h, d, d) or text_state.device != bank.device:
+            raise ValueError("text_state geometry/device mismatch")
+        text_state = text_state.contiguous()
+    alpha = alpha.contiguous()
+    stream = _stream(bank)
+    logp = None
+    if bridge:
+        logp = torch.empty((plan.frames + 1, h, d), dtype=torch.float32, device=bank.device)
+        _lib.call("vdn_vda_log_prefix", alpha.data_ptr(), plan.frames, h, logp.data_ptr(), stream)
+    out = torch.empty((plan.frames, h, d, d), device=bank.device, dtype=out_dtype)
+    _lib.call("vdn_vda_gather", bank[0].data_ptr(), bank[1].data_ptr(), _lib.ptr(logp),
+              _lib.ptr(text_state), plan.before.data_ptr(), plan.after.data_ptr(),
+              plan.has_before.data_ptr(), plan.has_after.data_ptr(),
+              plan.bridge_before.data_ptr(), plan.bridge_after.data_ptr(), plan.frames, h,
+              int(bool(bridge)), int(out_dtype == torch.float32), out.data_ptr(), stream)
+    return out
+
+
+# ------------------------------------------------------------ readout / norm ----
+
+def _weight_flag(w):
+    if w.dtype not in (torch.bfloat16, torch.float32) or w.shape != (HEAD_DIM,):
+        raise ValueError("norm weight must be [128] bf16 or fp32")
+    return int(w.dtype == torch.float32)
+
+
+def vdn_linear_epilogue(readout, norm_weight, gate, eps):
+    """readout [F,H,S,D] bf16, gate [F*S,H,D] -> RMSNorm(d)·w·gate as [F*S, H*D] bf16
+    (paper_sglang.py:406-437)."""
+    _cuda(readout, "readout", torch.bfloat16)
+    f, h, s, d = readout.shape
+    if d != HEAD_DIM:
+        raise ValueError("head_dim 128 required")
+    readout = readout.contiguous()
+    gate = gate.reshape(f * s, h, d).to(readout.dtype)
+    if gate.stride(-1) != 1:
+        gate = gate.contiguous()
+    w = norm_weight.to(device=readout.device).contiguous()
+    out = torch.empty((f * s, h * d), dtype=readout.dtype, device=readout.device)
+    gs = (s * gate.stride(0), gate.stride(1), gate.stride(0))
+    os_ = (s * out.stride(0), d, out.stride(0))
+    _lib.call("vdn_vda_epilogue", readout.data_ptr(), w.data_ptr(), _weight_flag(w), float(eps),
+              gate.data_ptr(), *gs, out.data_ptr(), *os_, f, h, s, _stream(readout))
+    return out
+
+
+def linear_readout(q, state, norm_weight, gate, eps, frames, spatial, *, activate_q=True,
+                   out=None):
+    """Fused q activation + readout + epilogue.
+
+    q: raw [F*S, H, D] bf16 (any row/head stride; prepared q with activate_q=False);
+    state: [F, H, D, D] bf16 from paper_gather; gate [F*S, H, D] bf16.
+    Returns (or writes into `out`) [F*S, H*D] bf16 = RMSNorm(bf16(q'·stateᵀ))·w·gate.
+    """
+    _cuda(q, "q", torch.bfloat16)
+    _cuda(state, "state", torch.bfloat16)
+    _cuda(gate, "gate", torch.bfloat16)
+    n, h, d = q.shape
+    if (d != HEAD_DIM or n != frames * spatial or state.shape != (frames, h, d, d)
+            or gate.shape != (n, h, d) or q.stride(-1) != 1 or gate.stride(-1) != 1):
+        raise ValueError("readout geometry mismatch")
+    state = state.contiguous()
+    w = norm_weight.to(device=q.device).contiguous()
+    if out is None:
+        out = torch.empty((n, h * d), dtype=torch.bfloat16, device=q.device)
+    elif out.shape != (n, h * d) or out.stride(-1) != 1 or out.dtype != torch.bfloat16:
+        raise ValueError("out must be bf16 [F*S, H*D]")
+    qs = (spatial * q.stride(0), q.stride(1), q.stride(0))
+    gs = (spatial * gate.stride(0), gate.stride(1), gate.stride(0))
+    os_ = (spatial * out.stride(0), d, out.stride(0))
+    _lib.call("vdn_vda_readout", q.data_ptr(), *qs, int(bool(activate_q)), state.data_ptr(),
+              w.data_ptr(), _weight_flag(w), float(eps), gate.data_ptr(), *gs, out.data_ptr(),
+              *os_, frames, h, spatial, _stream(q))
+    return out
+
+
+# ---------------------------------------------------------------- orchestration ----
+
+def vda_forward(q_raw, k_raw, v_raw, beta, gate, alpha, bounds, num_frames, tokens_per_frame,
+                norm_weight, eps, *, chunk_size=8, bridge=True, text=None, out=None):
+    """The paper VDA branch body on raw projections (paper_stack.py:266-318).
+
+    q_raw/k_raw/v_raw: [F*S, H, 128] bf16 raw projections; beta [F*S, H]; gate [F*S, H, 128];
+    alpha [F, H, 128] fp32. `text` = (tk_raw, tv_raw, text_beta) adds the prompt's virtual
+    frame (its factors share the batch; half its injection seeds both scans).
+    """
+    f, s = num_frames, tokens_per_frame
+    h = q_raw.shape[1]
+    device = q_raw.device
+    extra = 1 if text is not None else 0
+    a = torch.empty((f + extra, h, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=device)
+    b = torch.empty_like(a)
+    statistics_from_projections(k_raw, v_raw, beta, f, s, a[extra:], b[extra:])
+    if text is not None:
+        tk, tv, tb = text
+        statistics_from_projections(tk, tv, tb, 1, tk.shape[0], a[:1], b[:1])
+        factor_alpha = torch.cat((torch.ones_like(alpha[:1]), alpha))
+    else:
+        factor_alpha = alpha
+    transitions, injections = paper_delta_factors(a, b, factor_alpha.contiguous())
+    del a, b
+    seed = None
+    if text is not None:
+        seed = injections[0] * 0.5
+        transitions, injections = transitions[1:], injections[1:]
+    plan = paper_boundary_plan(bounds, f, device, chunk_size)
+    bank = paper_boundary_scan(transitions, injections, plan, seed)
+    del transitions, injections
+    state = paper_gather(bank, alpha, plan, seed, torch.bfloat16, bridge)
+    del bank
+    return linear_readout(q_raw, state, norm_weight, gate, eps, f, s, out=out)
+
+
+def paper_readout(branch, xv, num_frames, tokens_per_frame, bounds, qkv_raw, frame_size=None,
+                  text_x=None, text_qkv_raw=None, heads=None, beta=None, gate=None,
+                  frame_mean=None, text_beta=None):
+    """Branch body with the reference signature (paper_stack.py:266-318). `branch` supplies
+    beta_proj, alpha, output_gate, norm, bridge and paper_vda_chunk_size."""
+    if getattr(branch, "short_conv", None) is not None:
+        raise NotImplementedError("short convolution is not part of this build's hot path")
+    q, k, v = qkv_raw
+    h = q.shape[1]
+    if beta is None:
+        beta = torch.sigmoid(branch.beta_proj(xv))
+    if frame_mean is None:
+        frame_mean = xv.view(num_frames, tokens_per_frame, -1).mean(1, dtype=torch.float32)
+    alpha = branch.alpha(frame_mean, heads=heads).float().contiguous()
+    text = None
+    if text_x is not None or text_beta is not None:
+        if text_qkv_raw is None or text_qkv_raw[1].shape[0] < 1:
+            raise ValueError("prompt inputs require nonempty text QKV")
+        if text_beta is None:
+            text_beta = torch.sigmoid(branch.beta_proj(text_x))
+        text = (text_qkv_raw[1], text_qkv_raw[2], text_beta.reshape(-1, h))
+    if gate is None:
+        gate = branch.output_gate(xv)
+    return vda_forward(q, k, v, beta.reshape(-1, h), gate.reshape(-1, h, HEAD_DIM), alpha, bounds,
+                       num_frames, tokens_per_frame, branch.norm.weight, branch.norm.eps,
+                       chunk_size=branch.paper_vda_chunk_size, bridge=branch.bridge == "alpha",
+                       text=text)
