@@ -175,6 +175,43 @@ int vdn_vda_epilogue(const void* readout, const void* weight, int weight_f32, fl
                      int64_t o_sf, int64_t o_sh, int64_t o_ss, int frames, int heads, int spatial,
                      void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Frame-window softmax branch.
+ * ------------------------------------------------------------------------------------- */
+
+/*
+ * QK RMSNorm + rotate-half RoPE: n = bf16((x * rsqrt(mean(x^2) + eps)) * w); for channel
+ * i < rot: out = bf16(bf16(n_i * c_i) + bf16(r_i * s_i)) with r_i = -n_{i+rot/2} (i < rot/2)
+ * or n_{i-rot/2}; channels >= rot pass n. q, k: bf16 [tokens, heads, head_dim] with element
+ * strides (token, head, channel); weights [head_dim] with stride (flags bit0 / bit1: fp32
+ * q / k weight, else bf16); cos, sin (nullable together): [tokens, rot] with strides, fp32
+ * when flags bit2 else bf16 (values rounded to bf16 before use). qo, ko: contiguous bf16.
+ * Replaces: paper_qk_rmsnorm_rope (src/models/softmax_attention/paper_qk_rope.py:145-211).
+ */
+int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64_t q_sd, const void* k,
+                        int64_t k_st, int64_t k_sh, int64_t k_sd, const void* q_w, int64_t q_ws,
+                        const void* k_w, int64_t k_ws, float eps, const void* cos_t, int64_t c_st,
+                        int64_t c_sd, const void* sin_t, int64_t s_st, int64_t s_sd, int rot,
+                        int flags, int64_t tokens, int heads, int head_dim, void* qo, void* ko,
+                        void* stream);
+
+/*
+ * Exact softmax attention of query blocks over key intervals (head_dim 128, bf16):
+ * blocks int32 [nblocks, 3] = (first query, end of its query range, group), <= 128 queries
+ * each; grp_kv int32 [groups, 8, 2] key intervals [a, b); grp_n int32 [groups].
+ * q, k, v addressed by (token, head) strides with unit channel stride. gate (nullable): bf16
+ * per (token, head) scalar applied as out = bf16(bf16(o) * gate). out: bf16 (token, head)
+ * strides; lse (nullable): fp32 natural-log sum-exp of the scaled scores.
+ * Replaces: paper_window_attention (src/models/softmax_attention/paper_window.py:182-243)
+ * and apply_softmax_gate (src/models/softmax_attention/kernels.py:51-67).
+ */
+int vdn_window_attention(const void* q, int64_t q_st, int64_t q_sh, const void* k, int64_t k_st,
+                         int64_t k_sh, const void* v, int64_t v_st, int64_t v_sh,
+                         const int* blocks, int nblocks, const int* grp_kv, const int* grp_n,
+                         int heads, float scale, const void* gate, int64_t g_st, int64_t g_sh,
+                         void* out, int64_t o_st, int64_t o_sh, float* lse, int64_t l_st,
+                         int64_t l_sh, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,209 @@
+"""GPU parity of the window attention and QK norm/RoPE kernels against the oracle, at the
+reference tests' tolerances (tests/test_paper_stack_attention_window.py:121-212,
+tests/test_paper_stack_attention_rope.py:466-525)."""
+import pytest
+import torch
+
+from oracle import window as ow
+from vdn_amd import window as vw
+
+pytestmark = pytest.mark.gpu
+
+LAYOUTS = [(0, 0), (3, 0), (0, 4), (3, 4)]
+GEOMETRY = [(1, 0, 0), (2, 5, 1), (7, 3, 0), (7, 3, 1), (7, 0, 1), (7, 5, 1), (7, 0, 99)]
+
+
+@pytest.mark.parametrize("before,after", LAYOUTS)
+@pytest.mark.parametrize("frames,chunk,radius", GEOMETRY)
+@pytest.mark.parametrize("anchor", ["none", "rows", "columns", "both"])
+@torch.no_grad()
+def test_dense_fp32_oracle(device, before, after, frames, chunk, radius, anchor):
+    torch.manual_seed(819)
+    layout = vw.SequenceLayout(before + frames * 3 + after, before, frames, 3)
+    bounds = vw.window_bounds(frames, radius, chunk)
+    backing = torch.randn(layout.seq_len + 5, 3, 14, 128, device=device, dtype=torch.bfloat16)
+    q, k, v = [backing[:, i, 3:10] for i in range(3)]
+    old = backing.clone()
+    plan = vw.prepare_paper_window_plan(layout, bounds, anchor, device=device, max_query_rows=5,
+                                        max_gather_rows=2 * layout.seq_len)
+    out, lse = vw.paper_window_attention(q, k, v, plan, enabled=True, return_lse=True)
+    s = layout.seq_len
+    mask = ow.dense_mask(s, before, frames, 3, bounds, anchor)
+    expected, el = ow.attention_dense(q[:s].cpu(), k[:s].cpu(), v[:s].cpu(), mask, 128 ** -.5)
+    got = out[:s].float().cpu()
+    torch.testing.assert_close(got, expected, atol=.009, rtol=.015)
+    assert ((got - expected).norm() / expected.norm()) < .004
+    torch.testing.assert_close(lse[:s].cpu(), el, atol=3e-5, rtol=3e-6)
+    assert out[s:].count_nonzero() == 0
+    assert torch.isneginf(lse[s:]).all()
+    assert torch.equal(backing, old)
+    assert out.is_contiguous() and out.data_ptr() != backing.data_ptr()
+
+
+@torch.no_grad()
+def test_constant_values_anchor_union_mass(device):
+    layout = vw.SequenceLayout(45, 2, 13, 3)
+    bounds = vw.window_bounds(13, 1, 3)
+    q = torch.zeros(45, 7, 128, device=device, dtype=torch.bfloat16)
+    v = torch.arange(45, device=device, dtype=torch.float32)[:, None, None].expand_as(q).to(q.dtype)
+    p = vw.prepare_paper_window_plan(layout, bounds, "columns", device=device, max_gather_rows=70)
+    out, lse = vw.paper_window_attention(q, q, v, p, enabled=True, return_lse=True)
+    mask = ow.dense_mask(45, 2, 13, 3, bounds, "columns")
+    expected = (mask.float() @ torch.arange(45).float()) / mask.sum(-1)
+    torch.testing.assert_close(out[:, 0, 0].cpu(), expected.bfloat16(), rtol=0, atol=0)
+    torch.testing.assert_close(lse[:, 0].cpu(), mask.sum(-1).float().log(), rtol=1e-6, atol=1e-6)
+
+
+@torch.no_grad()
+def test_global_only_and_custom_stream(device):
+    layout = vw.SequenceLayout(13, 7, 0, 1)
+    plan = vw.prepare_paper_window_plan(layout, [], device=device, max_gather_rows=1, max_query_rows=4)
+    q, k, v = [torch.randn(15, 7, 128, device=device, dtype=torch.bfloat16) for _ in range(3)]
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        out = vw.paper_window_attention(q, k, v, plan, enabled=True)
+    torch.cuda.current_stream().wait_stream(stream)
+    expected, _ = ow.attention_dense(q[:13].cpu(), k[:13].cpu(), v[:13].cpu(),
+                                     torch.ones(13, 13, dtype=torch.bool), 128 ** -.5)
+    torch.testing.assert_close(out[:13].float().cpu(), expected, rtol=.015, atol=.009)
+    assert out[13:].count_nonzero() == 0
+
+
+@torch.no_grad()
+def test_reject_bad_runtime_contract(device):
+    p = vw.prepare_paper_window_plan(vw.SequenceLayout(7, 1, 2, 3), [(0, 1)] * 2, device=device)
+    q = torch.randn(7, 7, 128, device=device, dtype=torch.bfloat16)
+    for args in ((q[:6],) * 3, (q, q, q[:6]), (q.float(),) * 3, (q[..., ::2],) * 3):
+        with pytest.raises(ValueError):
+            vw.paper_window_attention(*args, p, enabled=True)
+    with pytest.raises(ValueError, match="finite"):
+        vw.paper_window_attention(q, q, q, p, scale=float("nan"), enabled=True)
+    cp = vw.prepare_paper_window_plan(p.layout, p.bounds)
+    with pytest.raises(ValueError, match="same CUDA"):
+        vw.paper_window_attention(q, q, q, cp, enabled=True)
+
+
+@torch.no_grad()
+def test_fused_gate_equals_separate_gate(device):
+    torch.manual_seed(3)
+    layout = vw.SequenceLayout(4 * 300, 0, 4, 300)
+    bounds = vw.window_bounds(4, 1)
+    q, k, v = [torch.randn(1200, 5, 128, device=device, dtype=torch.bfloat16) for _ in range(3)]
+    gate = torch.rand(1200, 5, 1, device=device, dtype=torch.bfloat16)
+    plan = vw.prepare_paper_window_plan(layout, bounds, device=device)
+    plain = vw.paper_window_attention(q, k, v, plan, enabled=True)
+    fused = vw.paper_window_attention(q, k, v, plan, enabled=True, gate=gate)
+    assert torch.equal(fused.reshape(1200, -1), vw.apply_softmax_gate(plain, gate))
+
+
+@torch.no_grad()
+def test_c4_full_shape_sampled(device):
+    """C4: 108,000 tokens (30 frames x 3600), 40 heads, d 128, +-1-frame window. Sampled
+    queries (every frame edge and interior, several heads) against the fp32 oracle."""
+    frames, spatial, h = 30, 3600, 40
+    n = frames * spatial
+    g = torch.Generator().manual_seed(4)
+    q, k, v = [(torch.randn(n, h, 128, generator=g) / 128 ** .5).to(torch.bfloat16) for _ in range(3)]
+    layout = vw.SequenceLayout(n, 0, frames, spatial)
+    bounds = vw.window_bounds(frames, 1)
+    plan = vw.prepare_paper_window_plan(layout, bounds, device=device)
+    out, lse = vw.paper_window_attention(q.to(device), k.to(device), v.to(device), plan,
+                                         enabled=True, return_lse=True)
+    out, lse = out.cpu(), lse.cpu()
+    for f in (0, 1, 14, 29):
+        lo, hi = max(0, f - 1), min(frames - 1, f + 1)
+        keys = slice(lo * spatial, (hi + 1) * spatial)
+        rows = torch.cat([torch.arange(f * spatial, f * spatial + 130),
+                          torch.arange((f + 1) * spatial - 20, (f + 1) * spatial)])
+        for hh in (0, 17, 39):
+            qs = q[rows, hh].float()
+            scores = qs @ k[keys, hh].float().T * 128 ** -.5
+            ref = scores.softmax(-1) @ v[keys, hh].float()
+            torch.testing.assert_close(out[rows, hh].float(), ref, atol=.009, rtol=.015)
+            torch.testing.assert_close(lse[rows, hh], scores.logsumexp(-1), atol=3e-5, rtol=3e-6)
+
+
+# ------------------------------------------------------------------------------ RoPE ----
+
+def rope_inputs(d=128, r=96, layout="qkv", t=13):
+    g = torch.Generator().manual_seed(194)
+    h = 7
+    if layout == "qkv":
+        storage = torch.randn(t, 3 * h * d, generator=g).bfloat16()
+        q = storage[:, :h * d].view(t, h, d)
+        k = storage[:, h * d:2 * h * d].view(t, h, d)
+    else:
+        storage = torch.randn(t, 3, h * 2, d * 2, generator=g).bfloat16()
+        q, k = storage[:, 0, ::2, ::2], storage[:, 1, ::2, ::2]
+    qw = (torch.rand(d * 2, generator=g) + 0.5).bfloat16()[::2]
+    kw = (torch.rand(d * 2, generator=g) + 0.5).bfloat16()[::2]
+    angles = torch.randn(t, r * 2, generator=g)
+    return storage, q, k, qw, kw, angles.cos()[:, ::2], angles.sin()[:, ::2]
+
+
+@pytest.mark.parametrize("layout", ["qkv", "inner"])
+@pytest.mark.parametrize("r", [None, 96, 128])
+@torch.no_grad()
+def test_rope_independent_oracle_strided_inputs(device, layout, r):
+    storage, q, k, qw, kw, c, s = rope_inputs(r=r or 96, layout=layout, t=33)
+    backing = storage.to(device)
+    qg = backing.as_strided(q.shape, q.stride(), q.storage_offset())
+    kg = backing.as_strided(k.shape, k.stride(), k.storage_offset())
+    qwd, kwd = qw.to(device), kw.to(device)
+    cg, sg = (None, None) if r is None else (c.to(device), s.to(device))
+    before = backing.clone()
+    outputs = vw.paper_qk_rmsnorm_rope(qg, kg, qwd, kwd, 1e-5, cg, sg, enabled=True)
+    for output, raw, weight in zip(outputs, (q, k), (qw, kw)):
+        expected = ow.qk_rope(raw, weight, 1e-5, None if r is None else c, None if r is None else s)
+        err = (output.float().cpu() - expected.float()).norm() / expected.float().norm()
+        assert err.item() < 2e-3
+        torch.testing.assert_close(output.cpu(), expected, rtol=0.02, atol=.032)
+        assert output.is_contiguous() and output.shape == (33, 7, 128)
+    assert torch.equal(backing, before)
+    assert outputs[0].data_ptr() != outputs[1].data_ptr()
+
+
+@torch.no_grad()
+def test_rope_bf16_intermediate_round_trap(device):
+    g = torch.Generator().manual_seed(715)
+    x = torch.ones(3, 7, 128, dtype=torch.bfloat16)
+    w = (torch.rand(128, generator=g) * 1.7 + .1).bfloat16()
+    angles = torch.randn(3, 96, generator=g)
+    c, s = angles.cos(), angles.sin()
+    expected = ow.qk_rope(x, w, .25, c, s)
+    assert torch.count_nonzero(expected != ow.qk_rope(x, w, .25, c, s, round_norm=False)) > 100
+    xd = x.to(device)
+    out, _ = vw.paper_qk_rmsnorm_rope(xd, xd, w.to(device), w.to(device), .25, c.to(device),
+                                      s.to(device), enabled=True)
+    torch.testing.assert_close(out.cpu(), expected, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("d,r", [(64, 32), (256, 192)])
+@torch.no_grad()
+def test_rope_other_widths_fp32_weights_strided_tables(device, d, r):
+    _, q, k, qw, kw, c, s = rope_inputs(d=d, r=r)
+    q, k = q.to(device), k.to(device)
+    wb = torch.empty(2, d * 2, device=device)
+    wb[0, ::2], wb[1, ::2] = qw.float().to(device), kw.float().to(device)
+    qwf, kwf = wb[0, ::2], wb[1, ::2]
+    cb, sb = torch.empty(13, r * 2, device=device), torch.empty(13, r * 2, device=device)
+    cb[:, ::2], sb[:, ::2] = c.to(device), s.to(device)
+    out, _ = vw.paper_qk_rmsnorm_rope(q, k, qwf, kwf, cos=cb[:, ::2], sin=sb[:, ::2], enabled=True)
+    torch.testing.assert_close(out.cpu(), ow.qk_rope(q.cpu(), qw.float(), 1e-6, c, s), atol=.032, rtol=.02)
+    qo, ko = vw.paper_qk_rmsnorm_rope(q[:0], k[:0], qwf, kwf, enabled=True)
+    assert qo.shape == ko.shape == (0, 7, d)
+
+
+@torch.no_grad()
+def test_rope_3d_tables_c4_geometry(device):
+    """3D RoPE (t,h,w) over 44/42/42 dims, theta 1e4, on a 2x45x80 slab of the C4 grid."""
+    cos, sin = vw.rope_tables_3d(2, 45, 80, device=device)
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(7200, 4, 128, generator=g).bfloat16()
+    w = torch.ones(128, dtype=torch.bfloat16)
+    out, _ = vw.paper_qk_rmsnorm_rope(q.to(device), q.to(device), w.to(device), w.to(device),
+                                      1e-6, cos, sin, enabled=True)
+    expected = ow.qk_rope(q, w, 1e-6, cos.cpu(), sin.cpu())
+    torch.testing.assert_close(out.cpu(), expected, atol=.032, rtol=.02)
+    assert ((out.cpu().float() - expected.float()).norm() / expected.float().norm()) < 2e-3

@@ -43,6 +43,12 @@ SIGNATURES = {
                         _i64, _ptr, _i64, _i64, _i64, _i32, _i32, _i32, _ptr],
     "vdn_vda_epilogue": [_ptr, _ptr, _i32, _f32, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64,
                          _i32, _i32, _i32, _ptr],
+    "vdn_qk_rmsnorm_rope": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _ptr,
+                            _i64, _f32, _ptr, _i64, _i64, _ptr, _i64, _i64, _i32, _i32, _i64,
+                            _i32, _i32, _ptr, _ptr, _ptr],
+    "vdn_window_attention": [_ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i32,
+                             _ptr, _ptr, _i32, _f32, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr,
+                             _i64, _i64, _ptr],
 }
 
 _LOCK = threading.Lock()

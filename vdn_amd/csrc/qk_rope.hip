@@ -1,0 +1,141 @@
+// QK RMSNorm + rotate-half RoPE for gfx950 (bf16 activations).
+//
+// Per (token, head) row x of D channels (reference src/models/softmax_attention/
+// paper_qk_rope.py:105-140, eager semantics :82-95):
+//   n   = bf16((x * rsqrt(sum(x^2) / D + eps)) * w)            (fp32, one rounding)
+//   for channel i < R: out = bf16(bf16(n_i * c_i) + bf16(r_i * s_i)),
+//       r_i = -n_{i+R/2} (i < R/2), n_{i-R/2} (R/2 <= i < R); c, s = table values in bf16
+//   channels i >= R pass n through.
+// A row is held by D/8 lanes (8 channels each); the rotate partner is exchanged through a
+// per-row LDS line, which keeps arbitrary even R <= D exact.
+#include "common.h"
+
+#include <math.h>
+
+namespace vdn {
+namespace {
+
+struct RopeArgs {
+  const uint16_t* x;
+  int64_t st, sh, sd;  // token, head, channel strides (elements)
+  const void* w;
+  int64_t ws;
+  int w_f32;
+  uint16_t* out;  // contiguous [T, H, D]
+};
+
+template <int kD>
+__global__ void __launch_bounds__(256)
+qk_rope_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float eps,
+               const void* __restrict__ cos_t, const void* __restrict__ sin_t, int64_t c_st,
+               int64_t c_sd, int64_t s_st, int64_t s_sd, int table_f32, int rot) {
+#pragma clang fp contract(off)
+  constexpr int kLanes = kD / 8;
+  constexpr int kRowsPerBlock = 256 / kLanes;
+  __shared__ float line[kRowsPerBlock][kD + 1];
+  const int sub = threadIdx.x % kLanes;
+  const int slot = threadIdx.x / kLanes;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + slot;
+  const int which = blockIdx.y;  // 0: q, 1: k
+  const RopeArgs& a = which == 0 ? q : k;
+  const bool live = row < tokens * heads;
+  const int64_t t = live ? row / heads : 0;
+  const int h = live ? static_cast<int>(row % heads) : 0;
+  float v[8];
+  const uint16_t* src = a.x + t * a.st + h * a.sh + static_cast<int64_t>(sub) * 8 * a.sd;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = live ? bf16_bits_to_f32(src[i * a.sd]) : 0.f;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+#pragma unroll
+  for (int off = 1; off < kLanes; off <<= 1) ss += __shfl_xor(ss, off, kLanes);
+  const float inv = 1.0f / sqrtf(ss / static_cast<float>(kD) + eps);
+  float n[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = sub * 8 + i;
+    const float w = a.w_f32 ? static_cast<const float*>(a.w)[c * a.ws]
+                            : bf16_bits_to_f32(static_cast<const uint16_t*>(a.w)[c * a.ws]);
+    n[i] = round_bf16((v[i] * inv) * w);
+    line[slot][c] = n[i];
+  }
+  __syncthreads();
+  float o[8];
+  const int half = rot / 2;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = sub * 8 + i;
+    if (c < rot) {
+      const float other = c < half ? -line[slot][c + half] : line[slot][c - half];
+      float cv, sv;
+      if (table_f32) {
+        cv = round_bf16(static_cast<const float*>(cos_t)[t * c_st + c * c_sd]);
+        sv = round_bf16(static_cast<const float*>(sin_t)[t * s_st + c * s_sd]);
+      } else {
+        cv = bf16_bits_to_f32(static_cast<const uint16_t*>(cos_t)[t * c_st + c * c_sd]);
+        sv = bf16_bits_to_f32(static_cast<const uint16_t*>(sin_t)[t * s_st + c * s_sd]);
+      }
+      o[i] = round_bf16(round_bf16(n[i] * cv) + round_bf16(other * sv));
+    } else {
+      o[i] = n[i];
+    }
+  }
+  if (live) {
+    uint16_t* dst = a.out + row * kD + sub * 8;
+    u32x4 packed;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) packed[i] = pack_bf16x2(o[2 * i], o[2 * i + 1]);
+    *reinterpret_cast<u32x4*>(dst) = packed;
+  }
+}
+
+}  // namespace
+}  // namespace vdn
+
+using namespace vdn;
+
+// Reference: paper_qk_rmsnorm_rope (src/models/softmax_attention/paper_qk_rope.py:145-211).
+// q, k: bf16 [tokens, heads, D] with arbitrary element strides; weights [D] (stride w_s,
+// bf16 or fp32 per flags bit0 for q / bit1 for k); cos/sin (nullable: norm only): [tokens, R]
+// with strides, fp32 when flags bit2 else bf16; qo, ko: contiguous bf16 [tokens, heads, D].
+VDN_API int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64_t q_sd,
+                                const void* k, int64_t k_st, int64_t k_sh, int64_t k_sd,
+                                const void* q_w, int64_t q_ws, const void* k_w, int64_t k_ws,
+                                float eps, const void* cos_t, int64_t c_st, int64_t c_sd,
+                                const void* sin_t, int64_t s_st, int64_t s_sd, int rot,
+                                int flags, int64_t tokens, int heads, int head_dim, void* qo,
+                                void* ko, void* stream) {
+  const char* name = "vdn_qk_rmsnorm_rope";
+  if (q == nullptr || k == nullptr || q_w == nullptr || k_w == nullptr || qo == nullptr ||
+      ko == nullptr)
+    return set_error(kInvalidArgument, "%s: null pointer", name);
+  if (heads <= 0 || tokens < 0 || (head_dim != 64 && head_dim != 128 && head_dim != 256))
+    return set_error(kInvalidArgument, "%s: heads > 0 and D in {64, 128, 256} required", name);
+  if ((cos_t == nullptr) != (sin_t == nullptr) || rot < 0 || rot > head_dim || rot % 2 ||
+      (cos_t != nullptr && rot == 0))
+    return set_error(kInvalidArgument, "%s: invalid rotary width %d", name, rot);
+  if (tokens == 0) return kOk;
+  const RopeArgs qa{static_cast<const uint16_t*>(q), q_st, q_sh, q_sd, q_w, q_ws, flags & 1,
+                    static_cast<uint16_t*>(qo)};
+  const RopeArgs ka{static_cast<const uint16_t*>(k), k_st, k_sh, k_sd, k_w, k_ws, (flags >> 1) & 1,
+                    static_cast<uint16_t*>(ko)};
+  const int64_t rows = tokens * heads;
+  auto st = static_cast<hipStream_t>(stream);
+  const int r = cos_t == nullptr ? 0 : rot;
+  const int tf = (flags >> 2) & 1;
+#define VDN_ROPE(D)                                                                             \
+  hipLaunchKernelGGL(qk_rope_kernel<D>, dim3(static_cast<unsigned>((rows + 256 / (D / 8) - 1) /  \
+                                                                    (256 / (D / 8))), 2),       \
+                     dim3(256), 0, st, qa, ka, tokens, heads, eps, cos_t, sin_t, c_st, c_sd,    \
+                     s_st, s_sd, tf, r);
+  if (head_dim == 64) {
+    VDN_ROPE(64)
+  } else if (head_dim == 128) {
+    VDN_ROPE(128)
+  } else {
+    VDN_ROPE(256)
+  }
+#undef VDN_ROPE
+  return check_launch(name);
+}

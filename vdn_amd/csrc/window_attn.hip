@@ -1,0 +1,295 @@
+// Frame-window softmax attention for gfx950 (bf16, head_dim 128), flash style.
+//
+// Replaces the packed varlen passes of paper_window_attention
+// (src/models/softmax_attention/paper_window.py:182-243) and the softmax gate
+// (softmax_attention/kernels.py:51-67). Each query block attends to a short list of key
+// intervals (the frame window, global rows, anchor frames), so no K/V gather copies exist.
+//
+// Per workgroup: 128 queries of one head (4 waves x 32), key tiles of 64.
+//   Sᵀ[key][q] = K · Qᵀ   on v_mfma_f32_32x32x16_bf16 (A = K rows, B = Q rows; Q fragments for
+//                         all 128 channels stay in registers for the whole kernel);
+//   online softmax in the exp2 domain, fp32 running max / sum per query;
+//   Oᵀ[d][q] += Vᵀ · Pᵀ   where Pᵀ is the Sᵀ accumulator itself: the 32x32 accumulator puts
+//                         keys 8(v/4) + 4g + v%4 of query l%32 in lane l (g = l/32), which is
+//                         exactly the B-operand K layout of the 16-key MFMA (slots 0-3 = keys
+//                         4g.., 4-7 = keys 8+4g..; measured), so P never leaves registers;
+//                         Vᵀ fragments come from the token-major V tile via ds_read_tr16_b64.
+// K/V tiles stream global -> LDS with global_load_lds_dwordx4, double-buffered; 16-byte
+// chunk c of tile row r is stored at c ^ (r & 15) (K: row reads) or c ^ 2 (r & 7) (V: the
+// 4-row transpose reads), which keeps both read patterns free of bank conflicts.
+#include "common.h"
+
+#include <math.h>
+
+namespace vdn {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kBM = 128;
+constexpr int kBN = 64;
+constexpr int kMaxIntervals = 8;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef const __attribute__((address_space(1))) void global_void_t;
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
+
+__device__ __forceinline__ void load_to_lds16(const void* src, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)lds_wave_base, 16, 0, 0);
+}
+
+__device__ __forceinline__ bf16x4_t lds_read_tr(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+      (lds_bf16x4_t*)((__attribute__((address_space(3))) char*)(p)));
+}
+
+__device__ __forceinline__ int swz_k(int row) { return row & 15; }
+__device__ __forceinline__ int swz_v(int row) { return 2 * (row & 7); }
+
+struct Layout {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh;  // token / head strides (elements)
+};
+
+__global__ void __launch_bounds__(256)
+window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restrict__ grp_kv,
+                   const int* __restrict__ grp_n, int nblocks, int heads, float scale_log2,
+                   const uint16_t* __restrict__ gate, int64_t g_st, int64_t g_sh,
+                   uint16_t* __restrict__ out, int64_t o_st, int64_t o_sh,
+                   float* __restrict__ lse, int64_t l_st, int64_t l_sh) {
+  __shared__ __attribute__((aligned(1024))) uint16_t sK[2][kBN * kD];
+  __shared__ __attribute__((aligned(1024))) uint16_t sV[2][kBN * kD];
+
+  // ---- work item: (head, query block); consecutive ids of a head land on one XCD ----
+  const int total = nblocks * heads;
+  int pid = blockIdx.x;
+  {
+    const int xcd = pid & 7, local = pid >> 3;
+    const int per = total >> 3, rem = total & 7;
+    pid = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  }
+  const int h = pid / nblocks;
+  const int blk = pid % nblocks;
+  const int q0 = blocks[3 * blk], q1 = blocks[3 * blk + 1], grp = blocks[3 * blk + 2];
+  const int nint = grp_n[grp];
+  const int* kv = grp_kv + grp * kMaxIntervals * 2;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5, col = lane & 31;
+
+  // ---- Q fragments: query q0 + 32 wave + col, channels 16 ks + 8 g .. +8 ----
+  const int my_q = q0 + wave * 32 + col;
+  const bool q_live = my_q < q1;
+  bf16x8 qf[8];
+  {
+    const uint16_t* src = in.q + static_cast<int64_t>(q_live ? my_q : q0) * in.q_st + h * in.q_sh;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(src + 16 * ks + 8 * g);
+      qf[ks] = __builtin_bit_cast(bf16x8, w);
+    }
+  }
+
+  // ---- tile schedule over the key intervals ----
+  int ntiles = 0;
+  for (int i = 0; i < nint; ++i) ntiles += (kv[2 * i + 1] - kv[2 * i] + kBN - 1) / kBN;
+  auto tile_range = [&](int t, int& a, int& b) {
+    int i = 0;
+    for (; i < nint; ++i) {
+      const int n = (kv[2 * i + 1] - kv[2 * i] + kBN - 1) / kBN;
+      if (t < n) break;
+      t -= n;
+    }
+    a = kv[2 * i] + t * kBN;
+    b = min(a + kBN, kv[2 * i + 1]);
+  };
+  // lane's share of a tile load: 4 x 1 KB segments (4 rows each) per tensor per wave
+  const int seg_row = lane >> 4, phys = lane & 15;
+  auto issue_tile = [&](int t, int buf) {
+    int a, b;
+    tile_range(t, a, b);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int seg = j * 4 + wave;
+      const int row = seg * 4 + seg_row;
+      const int key = min(a + row, b - 1);
+      const uint16_t* ksrc = in.k + static_cast<int64_t>(key) * in.k_st + h * in.k_sh;
+      const uint16_t* vsrc = in.v + static_cast<int64_t>(key) * in.v_st + h * in.v_sh;
+      load_to_lds16(ksrc + 8 * (phys ^ swz_k(row)), &sK[buf][seg * 4 * kD]);
+      load_to_lds16(vsrc + 8 * (phys ^ swz_v(row)), &sV[buf][seg * 4 * kD]);
+    }
+  };
+
+  f32x16 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
+  float m = -INFINITY, l = 0.f;
+
+  if (ntiles > 0) issue_tile(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  // transpose-read coordinates (16-lane group G = lane/16)
+  const int G = lane >> 4, L = lane & 15;
+  const int tr_row = 4 * (G >> 1) + (L >> 2);
+  const int tr_col = 16 * (G & 1) + 4 * (L & 3);
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) issue_tile(t + 1, buf ^ 1);
+    int a, b;
+    tile_range(t, a, b);
+    const uint16_t* tk = sK[buf];
+    const uint16_t* tv = sV[buf];
+
+    // ---- Sᵀ = K Qᵀ for the tile's 64 keys (two 32-key accumulators) ----
+    f32x16 s[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) s[kt][v] = 0.f;
+      const int row = kt * 32 + col;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const int chunk = (2 * ks + g) ^ swz_k(row);
+        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(tk + row * kD + chunk * 8);
+        s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[ks], s[kt], 0, 0, 0);
+      }
+    }
+    // ---- online softmax (exp2 domain) ----
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = a + kt * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+        const float x = key < b ? s[kt][v] * scale_log2 : -INFINITY;
+        s[kt][v] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m, mx);
+    const float corr = __builtin_amdgcn_exp2f(m - m_new);
+    float rs = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float p = __builtin_amdgcn_exp2f(s[kt][v] - m_new);
+        s[kt][v] = p;
+        rs += p;
+      }
+    rs += __shfl_xor(rs, 32);
+    l = l * corr + rs;
+    m = m_new;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[db][v] *= corr;
+
+    // ---- Oᵀ += Vᵀ Pᵀ, 16 keys per MFMA ----
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      bf16x8 pb;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pb[j] = static_cast<__bf16>(s[c >> 1][(c & 1) * 8 + j]);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        bf16x4_t lo, hi;
+        {
+          const int row = 16 * c + tr_row;
+          const int e = 32 * db + tr_col;
+          const int chunk = (e >> 3) ^ swz_v(row);
+          lo = lds_read_tr(tv + row * kD + chunk * 8 + (e & 7));
+        }
+        {
+          const int row = 16 * c + 8 + tr_row;
+          const int e = 32 * db + tr_col;
+          const int chunk = (e >> 3) ^ swz_v(row);
+          hi = lds_read_tr(tv + row * kD + chunk * 8 + (e & 7));
+        }
+        const bf16x8 va{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, o[db], 0, 0, 0);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+
+  // ---- epilogue: O / l, optional gate, through LDS to coalesced rows ----
+  const float inv_l = l > 0.f ? 1.0f / l : 0.f;
+  uint16_t* sO = sK[0];  // [128 queries][128 channels] bf16 = 32 KB (spans sK[0..1])
+  const int qr = wave * 32 + col;
+  float gv = 1.f;
+  if (gate != nullptr && q_live) gv = bf16_bits_to_f32(gate[static_cast<int64_t>(my_q) * g_st + h * g_sh]);
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int d = 32 * db + (v >> 2) * 8 + g * 4 + (v & 3);
+      float y = round_bf16(o[db][v] * inv_l);
+      if (gate != nullptr) y = y * gv;
+      sO[qr * kD + d] = f32_to_bf16_bits(y);
+    }
+  if (lse != nullptr && q_live && g == 0)
+    lse[static_cast<int64_t>(my_q) * l_st + h * l_sh] = (m + log2f(l)) * kLn2;
+  __syncthreads();
+  // 16 lanes write one query row (256 bytes)
+  for (int r = tid >> 4; r < kBM; r += 16) {
+    const int q = q0 + r;
+    if (q >= q1) continue;
+    const int c8 = (tid & 15) * 8;
+    *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(q) * o_st + h * o_sh + c8) =
+        *reinterpret_cast<const u32x4*>(&sO[r * kD + c8]);
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+}  // namespace vdn
+
+using namespace vdn;
+
+// Reference: paper_window_attention (src/models/softmax_attention/paper_window.py:182-243),
+// window_softmax_reference (window.py:56-111), apply_softmax_gate (kernels.py:51-67).
+// q, k, v: bf16 [rows, heads, 128] (token / head strides, unit channel stride);
+// blocks: int32 [nblocks, 3] = (first query, end of its query group, group index), each
+// block at most 128 queries; grp_kv: int32 [groups, 8, 2] key intervals [a, b); grp_n:
+// int32 [groups] interval counts. gate (nullable): bf16 per (token, head) scalar multiplied
+// into the bf16 output. out: bf16 rows of 128 channels; lse (nullable): fp32 natural-log
+// sum of exp of the scaled scores.
+VDN_API int vdn_window_attention(const void* q, int64_t q_st, int64_t q_sh, const void* k,
+                                 int64_t k_st, int64_t k_sh, const void* v, int64_t v_st,
+                                 int64_t v_sh, const int* blocks, int nblocks, const int* grp_kv,
+                                 const int* grp_n, int heads, float scale, const void* gate,
+                                 int64_t g_st, int64_t g_sh, void* out, int64_t o_st,
+                                 int64_t o_sh, float* lse, int64_t l_st, int64_t l_sh,
+                                 void* stream) {
+  const char* name = "vdn_window_attention";
+  if (q == nullptr || k == nullptr || v == nullptr || blocks == nullptr || grp_kv == nullptr ||
+      grp_n == nullptr || out == nullptr)
+    return set_error(kInvalidArgument, "%s: null pointer", name);
+  if (heads <= 0 || nblocks < 0) return set_error(kInvalidArgument, "%s: bad geometry", name);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || q_st % 8 ||
+      q_sh % 8 || k_st % 8 || k_sh % 8 || v_st % 8 || v_sh % 8 || o_st % 8 || o_sh % 8)
+    return set_error(kInvalidArgument, "%s: rows need 16-byte alignment", name);
+  if (!(scale > 0.f) || !isfinite(scale)) return set_error(kInvalidArgument, "%s: bad scale", name);
+  if (nblocks == 0) return kOk;
+  const Layout in{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                  static_cast<const uint16_t*>(v), q_st, q_sh, k_st, k_sh, v_st, v_sh};
+  const int64_t total = static_cast<int64_t>(nblocks) * heads;
+  if (total > (1ll << 31) - 1) return set_error(kUnsupported, "%s: too many blocks", name);
+  hipLaunchKernelGGL(window_attn_kernel, dim3(static_cast<unsigned>(total)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), in, blocks, grp_kv, grp_n, nblocks, heads,
+                     scale * kLog2e, static_cast<const uint16_t*>(gate), g_st, g_sh,
+                     static_cast<uint16_t*>(out), o_st, o_sh, lse, l_st, l_sh);
+  return check_launch(name);
+}

@@ -1,0 +1,412 @@
+"""Frame-window softmax attention and QK RMSNorm + RoPE with the reference's signatures.
+
+Mirrors src/models/sequence_layout.py (SequenceLayout), softmax_attention/window.py
+(window_bounds), paper_window.py (prepare_paper_window_plan, paper_window_attention),
+paper_qk_rope.py (paper_qk_rmsnorm_rope) and kernels.py (apply_softmax_gate). Device work
+runs in libvdnmi.so. The plan keeps the reference's groups, passes and budget errors; the
+gfx950 kernel consumes an interval form of the same visible sets (query blocks of <= 128
+rows, each with <= 8 contiguous key intervals), so it never gathers K/V.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from itertools import accumulate
+from numbers import Real
+
+import torch
+
+from . import _lib
+
+BLOCK_M = 128
+MAX_INTERVALS = 8
+
+
+@dataclass(frozen=True)
+class SequenceLayout:
+    """Packed-row geometry (sequence_layout.py:10-116)."""
+    seq_len: int
+    video_start: int
+    num_frames: int
+    tokens_per_frame: int
+    frame_height: int = 0
+    frame_width: int = 0
+    text_start: int = 0
+    text_len: int = 0
+
+    @property
+    def video_end(self):
+        return self.video_start + self.num_frames * self.tokens_per_frame
+
+    @property
+    def text_range(self):
+        if not self.text_len:
+            raise ValueError("this layout carries no text rows")
+        return self.text_start, self.text_start + self.text_len
+
+    @property
+    def frame_size(self):
+        if not (self.frame_height and self.frame_width):
+            raise ValueError("this layout carries no spatial grid")
+        if self.frame_height * self.frame_width != self.tokens_per_frame:
+            raise ValueError("grid does not match tokens/frame")
+        return self.frame_height, self.frame_width
+
+    def global_index(self, device):
+        idx = torch.arange(self.seq_len, device=device)
+        return torch.cat([idx[:self.video_start], idx[self.video_end:]])
+
+
+def window_bounds(num_frames, radius, chunk=0):
+    """Per-frame inclusive window [lo, hi], unclamped (window.py:26-52)."""
+    if chunk <= 0:
+        return [(t - radius, t + radius) for t in range(num_frames)]
+    return [(((t // chunk) - radius) * chunk, ((t // chunk) + radius + 1) * chunk - 1)
+            for t in range(num_frames)]
+
+
+# --------------------------------------------------------------------------- plan ----
+
+def _union(ranges):
+    out = []
+    for a, b in sorted(ranges):
+        if a >= b:
+            continue
+        if out and out[-1][1] >= a:
+            out[-1] = (out[-1][0], max(b, out[-1][1]))
+        else:
+            out.append((a, b))
+    return tuple(out)
+
+
+def _count(ranges):
+    return sum(b - a for a, b in ranges)
+
+
+def _split(ranges, budget):
+    current, size = [], 0
+    for a, b in ranges:
+        while a < b:
+            end = min(b, a + budget - size)
+            current.append((a, end))
+            size += end - a
+            a = end
+            if size == budget:
+                yield tuple(current)
+                current, size = [], 0
+    if current:
+        yield tuple(current)
+
+
+@dataclass(frozen=True)
+class VisibleGroup:
+    query_ranges: tuple
+    key_ranges: tuple
+
+
+@dataclass(frozen=True)
+class PackedPass:
+    groups: tuple
+    query_rows: torch.Tensor
+    key_rows: torch.Tensor | None
+    cu_q: torch.Tensor
+    cu_k: torch.Tensor
+    max_q: int
+    max_k: int
+    dense: bool
+
+
+@dataclass(frozen=True)
+class DevicePlan:
+    """Interval form for the gfx950 kernel: blocks int32 [nb, 3] (q0, range end, group),
+    intervals int32 [ng, 8, 2], counts int32 [ng]."""
+    blocks: torch.Tensor
+    intervals: torch.Tensor
+    counts: torch.Tensor
+    nblocks: int
+
+
+@dataclass(frozen=True)
+class PaperWindowPlan:
+    layout: SequenceLayout
+    bounds: tuple
+    anchor_frames: str
+    max_gather_rows: int
+    max_query_rows: int
+    device: torch.device
+    passes: tuple
+    device_plan: DevicePlan = field(default=None, compare=False)
+
+    @property
+    def peak_gather_rows(self):
+        return max((p.key_rows.numel() for p in self.passes if not p.dense), default=0)
+
+
+def _device_plan(groups_with_keys, device):
+    blocks, intervals, counts = [], [], []
+    for gi, (query_ranges, key_ranges) in enumerate(groups_with_keys):
+        if len(key_ranges) > MAX_INTERVALS:
+            raise ValueError(f"a visible set needs {len(key_ranges)} key intervals; the kernel "
+                             f"takes at most {MAX_INTERVALS}")
+        pad = list(key_ranges) + [(0, 0)] * (MAX_INTERVALS - len(key_ranges))
+        intervals.append([list(r) for r in pad])
+        counts.append(len(key_ranges))
+        for a, b in query_ranges:
+            for q0 in range(a, b, BLOCK_M):
+                blocks.append([q0, b, gi])
+    bt = torch.tensor(blocks if blocks else [[0, 0, 0]], dtype=torch.int32)
+    it = torch.tensor(intervals if intervals else [[[0, 0]] * MAX_INTERVALS], dtype=torch.int32)
+    ct = torch.tensor(counts if counts else [0], dtype=torch.int32)
+    return DevicePlan(bt.to(device), it.to(device), ct.to(device), len(blocks))
+
+
+def prepare_paper_window_plan(layout: SequenceLayout, bounds, anchor_frames="none", *,
+                              device="cpu", max_gather_rows=65_536, max_query_rows=8_192):
+    """Plan of visible sets per query group (paper_window.py:86-168), with the same
+    validation, grouping, pass budgets and errors; adds the kernel's interval form."""
+    if not isinstance(layout, SequenceLayout):
+        raise TypeError("layout must be SequenceLayout")
+    s, vs, f, tpf = layout.seq_len, layout.video_start, layout.num_frames, layout.tokens_per_frame
+    if (any(type(x) is not int for x in (s, vs, f, tpf)) or s <= 0 or f < 0 or tpf <= 0 or vs < 0
+            or vs + f * tpf > s):
+        raise ValueError("invalid used-row/video geometry")
+    if anchor_frames not in ("none", "rows", "columns", "both"):
+        raise ValueError("anchor_frames must be none, rows, columns, or both")
+    if any(type(x) is not int or x <= 0 for x in (max_gather_rows, max_query_rows)):
+        raise ValueError("row budgets must be positive integers")
+    bounds = tuple(tuple(b) for b in bounds)
+    if len(bounds) != f or any(len(b) != 2 or any(type(x) is not int for x in b) or b[0] > b[1]
+                               for b in bounds):
+        raise ValueError("one ordered integer bound pair required per video frame")
+    device = torch.device(device)
+    if device.type == "cuda" and device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    ve = vs + f * tpf
+    globals_ = _union(((0, vs), (ve, s)))
+    anchors = {0, f - 1} if f else set()
+    row_anchors = anchors if anchor_frames in ("rows", "both") else set()
+    col_anchors = anchors if anchor_frames in ("columns", "both") else set()
+    dense_ranges, groups = list(globals_), []
+    for frame in range(f):
+        qr = (vs + frame * tpf, vs + (frame + 1) * tpf)
+        lo, hi = bounds[frame]
+        kr = _union(list(globals_) + [(vs + max(0, lo) * tpf, vs + min(f, hi + 1) * tpf)]
+                    + [(vs + a * tpf, vs + (a + 1) * tpf) for a in col_anchors])
+        if frame in row_anchors or kr == ((0, s),):
+            dense_ranges.append(qr)
+        else:
+            if not kr:
+                raise ValueError(f"video frame {frame} has no visible keys")
+            if _count(kr) > max_gather_rows:
+                raise ValueError(f"visible set requires {_count(kr)} gather rows, "
+                                 f"budget={max_gather_rows}; increase max_gather_rows")
+            if groups and groups[-1].key_ranges == kr and groups[-1].query_ranges[-1][1] == qr[0]:
+                groups[-1] = VisibleGroup(_union(groups[-1].query_ranges + (qr,)), kr)
+            else:
+                groups.append(VisibleGroup((qr,), kr))
+
+    def indices(ranges):
+        return torch.cat([torch.arange(a, b, dtype=torch.long) for a, b in ranges]).to(device)
+
+    def make_pass(gs, dense=False):
+        qlens = [_count(g.query_ranges) for g in gs]
+        klens = [_count(g.key_ranges) for g in gs]
+
+        def cumulative(lengths):
+            return torch.tensor([0] + list(accumulate(lengths)), dtype=torch.int32, device=device)
+        return PackedPass(tuple(gs), indices(tuple(r for g in gs for r in g.query_ranges)),
+                          None if dense else indices(tuple(r for g in gs for r in g.key_ranges)),
+                          cumulative(qlens), cumulative(klens), max(qlens), max(klens), dense)
+
+    dense_union = _union(dense_ranges)
+    passes = [make_pass([VisibleGroup(qr, ((0, s),))], True)
+              for qr in _split(dense_union, max_query_rows)]
+    current, nq, nk = [], 0, 0
+    for group in groups:
+        for qr in _split(group.query_ranges, max_query_rows):
+            small = VisibleGroup(qr, group.key_ranges)
+            qlen, klen = _count(qr), _count(small.key_ranges)
+            if current and (nq + qlen > max_query_rows or nk + klen > max_gather_rows):
+                passes.append(make_pass(current))
+                current, nq, nk = [], 0, 0
+            current.append(small)
+            nq, nk = nq + qlen, nk + klen
+    if current:
+        passes.append(make_pass(current))
+    if sum(p.query_rows.numel() for p in passes) != s:
+        raise AssertionError("internal plan coverage mismatch")
+    kernel_groups = ([(dense_union, ((0, s),))] if dense_union else []) + \
+        [(g.query_ranges, g.key_ranges) for g in groups]
+    return PaperWindowPlan(layout, bounds, anchor_frames, max_gather_rows, max_query_rows, device,
+                           tuple(passes), _device_plan(kernel_groups, device))
+
+
+# ---------------------------------------------------------------------- attention ----
+
+def paper_window_attention(query, key, value, plan: PaperWindowPlan, scale=None, *,
+                           enabled=False, return_lse=False, nvtx=True, gate=None):
+    """[used+padding, H, D] -> fresh output of the same shape; padding rows are zero
+    (paper_window.py:182-243). LSE (fp32 [rows, H], natural log) is -inf on padding.
+    `gate` ([rows, H] or [rows, H, 1]) fuses apply_softmax_gate: out = bf16(bf16(o) * gate)."""
+    if not enabled:
+        raise RuntimeError("paper window attention is disabled; retain the existing caller path "
+                           "or explicitly enable")
+    if torch.is_grad_enabled():
+        raise RuntimeError("paper window attention is inference-only; use no_grad/inference_mode")
+    if not isinstance(plan, PaperWindowPlan):
+        raise TypeError("plan must be prepared with prepare_paper_window_plan")
+    if any(x.ndim != 3 or x.shape != query.shape or x.dtype != query.dtype
+           or x.device != query.device for x in (query, key, value)):
+        raise ValueError("Q/K/V must have identical [rows,H,D], dtype and device")
+    if query.shape[0] < plan.layout.seq_len or query.shape[1] <= 0 or query.shape[2] not in (64, 128, 256):
+        raise ValueError("invalid Q/K/V geometry or insufficient used rows")
+    if query.dtype not in (torch.bfloat16, torch.float16) or any(x.stride(-1) != 1 for x in (query, key, value)):
+        raise ValueError("native varlen requires BF16/FP16 and unit innermost stride")
+    if not query.is_cuda or query.device != plan.device:
+        raise ValueError("Q/K/V and prepared plan must be on the same CUDA device")
+    if query.shape[2] != 128 or query.dtype != torch.bfloat16:
+        raise NotImplementedError("the gfx950 window kernel takes bf16 with head_dim 128")
+    scale = query.shape[-1] ** -0.5 if scale is None else float(scale)
+    if not math.isfinite(scale):
+        raise ValueError("scale must be finite")
+    rows, h, d = query.shape
+    out = torch.empty((rows, h, d), dtype=query.dtype, device=query.device)
+    lse = torch.empty((rows, h), dtype=torch.float32, device=query.device) if return_lse else None
+    used = plan.layout.seq_len
+    if rows > used:
+        out[used:].zero_()
+        if lse is not None:
+            lse[used:].fill_(-float("inf"))
+    if gate is not None:
+        if gate.shape[0] < used or gate.numel() != gate.shape[0] * h:
+            raise ValueError("gate must be [rows, H] or [rows, H, 1] covering the used rows")
+        gate = gate.reshape(gate.shape[0], h)
+        if gate.dtype != torch.bfloat16:
+            gate = gate.to(torch.bfloat16)
+    dp = plan.device_plan
+    _lib.call("vdn_window_attention", query.data_ptr(), query.stride(0), query.stride(1),
+              key.data_ptr(), key.stride(0), key.stride(1), value.data_ptr(), value.stride(0),
+              value.stride(1), dp.blocks.data_ptr(), dp.nblocks, dp.intervals.data_ptr(),
+              dp.counts.data_ptr(), h, scale, _lib.ptr(gate),
+              0 if gate is None else gate.stride(0), 0 if gate is None else gate.stride(1),
+              out.data_ptr(), out.stride(0), out.stride(1), _lib.ptr(lse),
+              0 if lse is None else lse.stride(0), 0 if lse is None else lse.stride(1),
+              _lib.stream(query.device))
+    return (out, lse) if return_lse else out
+
+
+def apply_softmax_gate(softmax_out, gate, inference=False):
+    """out * gate (bf16) flattened to [T, H*D] (softmax_attention/kernels.py:62-67); the fused
+    form is paper_window_attention(..., gate=gate)."""
+    return (softmax_out * gate.to(softmax_out.dtype)).reshape(softmax_out.shape[0], -1)
+
+
+# ---------------------------------------------------------------- QK norm + RoPE ----
+
+_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
+
+def _validate_rope(q, k, q_weight, k_weight, eps, cos, sin, enabled, nvtx):
+    if not isinstance(enabled, bool) or not isinstance(nvtx, bool):
+        raise TypeError("enabled and nvtx must be bool")
+    if torch.is_grad_enabled():
+        raise RuntimeError("paper_qk_rmsnorm_rope is inference-only; use torch.no_grad()")
+    if isinstance(eps, bool) or not isinstance(eps, Real):
+        raise TypeError("eps must be a finite positive real scalar")
+    if not math.isfinite(eps) or eps <= 0:
+        raise ValueError("eps must be finite and positive")
+    for name, value in (("q", q), ("k", k), ("q_weight", q_weight), ("k_weight", k_weight)):
+        if not isinstance(value, torch.Tensor):
+            raise TypeError(f"{name} must be a tensor")
+        if value.layout != torch.strided:
+            raise ValueError(f"{name} must have strided layout")
+    if q.ndim != 3 or k.shape != q.shape:
+        raise ValueError("q and k must have identical [T, H, D] shapes")
+    t, h, d = q.shape
+    if h <= 0 or d not in (64, 128, 256):
+        raise ValueError("H must be positive and D must be 64, 128, or 256")
+    if q.dtype not in _DTYPES or k.dtype != q.dtype:
+        raise TypeError("q and k must share a BF16, FP16, or FP32 dtype")
+    if q.device.type not in ("cpu", "cuda") or k.device != q.device:
+        raise ValueError("q and k must share a CPU or CUDA device")
+    for name, weight in (("q_weight", q_weight), ("k_weight", k_weight)):
+        if weight.shape != (d,):
+            raise ValueError(f"{name} must have shape [D], shared by every head")
+        if weight.device != q.device:
+            raise ValueError(f"{name} must be on the q/k device")
+        if weight.dtype not in (q.dtype, torch.float32):
+            raise TypeError(f"{name} must have the activation dtype or FP32")
+    if (cos is None) != (sin is None):
+        raise ValueError("cos and sin must both be supplied or both be None")
+    if cos is not None:
+        for name, table in (("cos", cos), ("sin", sin)):
+            if not isinstance(table, torch.Tensor):
+                raise TypeError(f"{name} must be a tensor")
+            if table.layout != torch.strided or table.ndim != 2:
+                raise ValueError(f"{name} must have strided shape [T, R]")
+            if table.device != q.device:
+                raise ValueError(f"{name} must be on the q/k device")
+            if table.dtype not in _DTYPES:
+                raise TypeError(f"{name} must be BF16, FP16, or FP32")
+        if cos.shape != sin.shape or cos.shape[0] != t:
+            raise ValueError("cos and sin must have identical [T, R] shapes")
+        r = cos.shape[1]
+        if r <= 0 or r > d or r % 2:
+            raise ValueError("rotary width R must be positive, even, and at most D")
+
+
+def paper_qk_rmsnorm_rope(q, k, q_weight, k_weight, eps=1e-6, cos=None, sin=None, *,
+                          enabled=False, nvtx=True):
+    """New contiguous normalized/rotated Q and K (paper_qk_rope.py:145-211).
+
+    enabled=False is refused here: the disabled path of the reference is its eager CPU/CUDA
+    implementation, which this build does not ship (the oracle holds it). enabled=True runs
+    the gfx950 kernel for bf16 activations.
+    """
+    _validate_rope(q, k, q_weight, k_weight, eps, cos, sin, enabled, nvtx)
+    if not enabled:
+        raise RuntimeError("paper_qk_rmsnorm_rope: only the enabled (device) path is built")
+    if not q.is_cuda:
+        raise ValueError("enabled=True requires a HIP device")
+    if q.dtype != torch.bfloat16:
+        raise NotImplementedError("the gfx950 QK norm/RoPE kernel takes bf16 activations")
+    qo = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    ko = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    if q.shape[0] == 0:
+        return qo, ko
+    tables = cos is not None
+    if tables:
+        if cos.dtype == torch.float16:
+            cos, sin = cos.float(), sin.float()
+        if sin.dtype != cos.dtype:
+            sin = sin.to(cos.dtype)
+    flags = (int(q_weight.dtype == torch.float32) | (int(k_weight.dtype == torch.float32) << 1)
+             | (int(tables and cos.dtype == torch.float32) << 2))
+    t, h, d = q.shape
+    _lib.call("vdn_qk_rmsnorm_rope", q.data_ptr(), *q.stride(), k.data_ptr(), *k.stride(),
+              q_weight.data_ptr(), q_weight.stride(0), k_weight.data_ptr(), k_weight.stride(0),
+              float(eps), _lib.ptr(cos) if tables else None, cos.stride(0) if tables else 0,
+              cos.stride(1) if tables else 0, _lib.ptr(sin) if tables else None,
+              sin.stride(0) if tables else 0, sin.stride(1) if tables else 0,
+              cos.shape[1] if tables else 0, flags, t, h, d, qo.data_ptr(), ko.data_ptr(),
+              _lib.stream(q.device))
+    return qo, ko
+
+
+def rope_tables_3d(frames, height, width, *, dims=(44, 42, 42), theta=10000.0, device="cpu",
+                   dtype=torch.float32):
+    """Full-width rotate-half cos/sin tables [F*H*W, sum(dims)] for 3D positions (t, h, w).
+
+    Pair i of the rotate-half layout pairs channel i with i + R/2 (R = sum(dims)); the R/2
+    pairs are split over the axes as dims/2 each (22 t, 21 h, 21 w for 44/42/42), each axis
+    using frequencies theta^(-2j/dim_axis). Column i and i + R/2 carry the same angle.
+    """
+    pos = torch.stack(torch.meshgrid(torch.arange(frames), torch.arange(height),
+                                     torch.arange(width), indexing="ij"), -1).reshape(-1, 3)
+    angles = []
+    for axis, dim in enumerate(dims):
+        inv = theta ** (-torch.arange(0, dim, 2, dtype=torch.float64) / dim)
+        angles.append(pos[:, axis:axis + 1].double() * inv[None, :])
+    half = torch.cat(angles, dim=1)
+    full = torch.cat((half, half), dim=1)
+    return full.cos().to(device=device, dtype=dtype), full.sin().to(device=device, dtype=dtype)
