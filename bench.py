@@ -1,0 +1,248 @@
+"""Hybrid DiT block forward at the 108k-token clip shape on one MI355X.
+
+Workload: one block (hidden 5120, 40 heads x 128, FFN 13824 GELU-tanh, rank-64 LoRA merged into
+QKV, AdaLN from a timestep embedding, frame-window softmax (+-1 frame) with 3D RoPE, VDA linear
+attention, cross-attention to 512 context rows, gated residuals) over 30 latent frames of
+45 x 80 = 108,000 tokens, bf16 activations, MXFP8 projections. Random-init weights N(0, 0.02),
+hidden/temb/context N(0, 1), all resident in HBM before timing.
+
+Prints one JSON line: value = ms per block forward (lower is better), the MXFP8 GEMM roofline
+(algorithmic FLOP / measured launch time, HIP events on the launch stream), the VDA passes'
+algorithmic GB/s, a per-entry-point breakdown, and the CPU fp32 path timed on a bounded sample.
+
+  python bench.py [--steps K] [--warmup W] [--frames F] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+METRIC = "ms per hybrid DiT block fwd @108k tok; MXFP8 TFLOP/s & VDA GB/s vs peak"
+PEAK_MXFP8_TFLOPS = 5000.0   # dense MXFP8 / FP8 MFMA, MI355X
+PEAK_BF16_TFLOPS = 2500.0    # dense bf16 MFMA, MI355X
+PEAK_HBM_GBS = 8000.0        # HBM3E, MI355X
+HEIGHT, WIDTH = 45, 80
+D = 128
+
+VDA_ENTRIES = ("vdn_vda_statistics", "vdn_vda_factors", "vdn_vda_compose", "vdn_vda_scan",
+               "vdn_vda_log_prefix", "vdn_vda_gather", "vdn_vda_readout")
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def padded(n):
+    return -(-n // 128) * 128
+
+
+def work(name, a, plans):
+    """Algorithmic (flop, bytes) of one launch from its C-ABI arguments."""
+    if name == "vdn_mxfp8_gemm":
+        kp, rows, n = a[6], a[14], a[15]
+        ops = [a[7], a[8], a[10], a[12]]  # bias, addend, residual, gate
+        extra = rows * n * 2 * sum(1 for p in ops[1:3] if p is not None)
+        return 2.0 * rows * n * kp, rows * kp + n * kp + (rows + n) * kp / 32 + rows * n * 2 + extra
+    if name == "vdn_mxfp8_quantize":
+        rows, k = a[1], a[2]
+        return 0.0, rows * k * 2 + padded(rows) * padded(k) * (1 + 1 / 32)
+    if name == "vdn_mxfp8_act_quantize":
+        rows, k, act = a[1], a[2], a[4]
+        inner = 2 * k if act == 2 else k
+        return 0.0, rows * inner * 2 + padded(rows) * padded(k) * (1 + 1 / 32)
+    if name == "vdn_mxfp8_prenorm_quantize":
+        rows, k, y = a[1], a[2], a[12]
+        return 0.0, (rows * k * 2 * (2 if y is not None else 1) + rows * 8 + padded(rows)
+                     + padded(rows) * padded(k) * (1 + 1 / 32))
+    if name == "vdn_qk_rmsnorm_rope":
+        flags, tokens, heads, hd, rot = a[20], a[21], a[22], a[23], a[19]
+        operands = 1 if flags & 8 else 2
+        tables = 0 if a[13] is None else 2 * tokens * rot * (4 if flags & 4 else 2)
+        return 0.0, operands * tokens * heads * hd * 4 + tables
+    if name == "vdn_window_attention":
+        heads = a[13]
+        pairs = plans.get(a[11], 0)
+        return 4.0 * D * heads * pairs, 0.0
+    if name == "vdn_vda_statistics":
+        f, h, s, beta_f32 = a[13], a[14], a[15], a[12]
+        return (4.0 * f * h * s * D * D, 2 * f * s * h * D * 2 + f * s * h * (4 if beta_f32 else 2)
+                + 2 * f * h * D * D * 4)
+    if name == "vdn_vda_factors":
+        count = a[3]
+        return 0.0, 4 * count * D * D * 4 + (count * D * 4 if a[2] is not None else 0)
+    if name == "vdn_vda_compose":
+        heads, chunks = a[2], a[5]
+        return 0.0, 4 * chunks * heads * D * D * 4
+    if name == "vdn_vda_scan":
+        chunks, heads = a[3], a[4]
+        return 0.0, 4 * chunks * heads * D * D * 4
+    if name == "vdn_vda_log_prefix":
+        f, h = a[1], a[2]
+        return 0.0, 2 * f * h * D * 4
+    if name == "vdn_vda_gather":
+        f, h, out_f32 = a[10], a[11], a[13]
+        return 0.0, 2 * f * h * D * D * 4 + f * h * D * D * (4 if out_f32 else 2)
+    if name == "vdn_vda_readout":
+        f, h, s = a[17], a[18], a[19]
+        return 2.0 * f * s * h * D * D, 3 * f * s * h * D * 2 + f * h * D * D * 2
+    return 0.0, 0.0
+
+
+def visible_pairs(frames, spatial, radius):
+    """Query-key pairs per head of the +-radius frame window."""
+    total = 0
+    for f in range(frames):
+        lo, hi = max(0, f - radius), min(frames - 1, f + radius)
+        total += spatial * spatial * (hi - lo + 1)
+    return total
+
+
+def cpu_baseline(cfg, weights, hidden, temb, ctx, cos, sin, frames_total, sample_frames):
+    """The fp32 CPU block (the oracle's eager path) on the first `sample_frames` frames,
+    extrapolated linearly in frames to the full clip."""
+    import torch
+    from oracle import block as ob
+    spatial = HEIGHT * WIDTH
+    t = sample_frames * spatial
+    w = {k: v.cpu() for k, v in weights.tensors.items()}
+    args = (w, cfg, hidden[:t].cpu(), temb.cpu(), ctx.cpu(), sample_frames, HEIGHT, WIDTH,
+            cos[:t].cpu(), sin[:t].cpu())
+    start = time.perf_counter()
+    with torch.no_grad():
+        ob.eager_block_fp32(*args)
+    elapsed = time.perf_counter() - start
+    return dict(value=round(elapsed * 1e3 * frames_total / sample_frames, 1), unit="ms",
+                cores=torch.get_num_threads(), kind="port",
+                sample=(f"fp32 eager block (torch CPU, nn.Linear-equivalent bf16->fp32 weights, "
+                        f"per-frame SDPA, eager VDA) on the first {sample_frames} frames "
+                        f"({t} tokens): {elapsed:.1f} s, scaled x{frames_total / sample_frames:g} "
+                        f"to {frames_total} frames"))
+
+
+def main():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=5)
+    p.add_argument("--warmup", type=int, default=2)
+    p.add_argument("--frames", type=int, default=30)
+    p.add_argument("--cpu-sample-frames", type=int, default=3)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    args = p.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the block runs whole on a single MI355X "
+              "(no sharding in this build); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from vdn_amd import _lib
+    from vdn_amd import window as vw
+    from vdn_amd.block import (BlockConfig, BlockWeights, HybridDiTBlock, cross_attention_plan,
+                               make_inputs)
+    if not torch.cuda.is_available():
+        raise RuntimeError("bench.py needs a HIP device")
+    _lib.load()
+    cfg = BlockConfig()
+    frames = args.frames
+    spatial = HEIGHT * WIDTH
+    tokens = frames * spatial
+    log(f"building block weights (hidden {cfg.hidden}, ffn {cfg.ffn}) and inputs "
+        f"({frames} x {HEIGHT}x{WIDTH} = {tokens} tokens)")
+    weights = BlockWeights.random(cfg, seed=0, device="cuda")
+    block = HybridDiTBlock(cfg, weights)
+    hidden, temb, ctx, layout, (cos, sin) = make_inputs(cfg, frames, HEIGHT, WIDTH, seed=1,
+                                                       device="cuda")
+    plan = vw.prepare_paper_window_plan(layout, vw.window_bounds(frames, cfg.radius),
+                                        device="cuda")
+    cplan = cross_attention_plan(tokens, ctx.shape[0], "cuda")
+    plans = {plan.device_plan.intervals.data_ptr(): visible_pairs(frames, spatial, cfg.radius),
+             cplan.intervals.data_ptr(): tokens * ctx.shape[0]}
+
+    def step():
+        return block(hidden, temb, ctx, layout, (cos, sin), plan, cplan)
+
+    for i in range(args.warmup):
+        step()
+        torch.cuda.synchronize()
+        log(f"warmup {i + 1}/{args.warmup} done")
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    names = set(_lib.SIGNATURES)
+    with _lib.LaunchTimer(names) as timer:
+        torch.cuda.synchronize()
+        start.record()
+        for i in range(args.steps):
+            step()
+        end.record()
+        torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    log(f"timed {args.steps} steps: {ms:.2f} ms per block")
+
+    per = {}
+    for name, a, t in timer.durations():
+        flop, nbytes = work(name, a, plans)
+        e = per.setdefault(name, [0, 0.0, 0.0, 0.0])
+        e[0] += 1
+        e[1] += t
+        e[2] += flop
+        e[3] += nbytes
+    breakdown = {}
+    for name, (count, t, flop, nbytes) in sorted(per.items(), key=lambda kv: -kv[1][1]):
+        row = dict(ms_per_step=round(t / args.steps, 3), launches_per_step=count // args.steps,
+                   avg_launch_ms=round(t / count, 4))
+        if flop and name in ("vdn_mxfp8_gemm", "vdn_window_attention"):
+            row["tflops"] = round(flop / (t * 1e-3) / 1e12, 1)
+        if nbytes and name not in ("vdn_mxfp8_gemm", "vdn_window_attention"):
+            row["gbs"] = round(nbytes / (t * 1e-3) / 1e9, 1)
+        breakdown[name] = row
+    g = per["vdn_mxfp8_gemm"]
+    gemm_tflops = g[2] / (g[1] * 1e-3) / 1e12
+    vda_t = sum(per[n][1] for n in VDA_ENTRIES if n in per)
+    vda_bytes = sum(per[n][3] for n in VDA_ENTRIES if n in per)
+    vda_gbs = vda_bytes / (vda_t * 1e-3) / 1e9
+    w = per["vdn_window_attention"]
+    traffic = None
+    traffic_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                                "gemm_block_108k_traffic.json")
+    if os.path.exists(traffic_path):
+        traffic = json.load(open(traffic_path)).get("bytes_per_launch")
+
+    result = {
+        "metric": METRIC, "value": round(ms, 3), "unit": "ms", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "mxfp8-e4m3 GEMMs, bf16 attention/activations, fp32 VDA state",
+        "data": "synthetic: random-init weights N(0,0.02), hidden/temb/context N(0,1)",
+        "config": {"workload": (f"hybrid DiT block forward, {frames} frames x {HEIGHT}x{WIDTH} = "
+                                f"{tokens} tokens, hidden {cfg.hidden}, {cfg.heads}x{cfg.head_dim} "
+                                f"heads, FFN {cfg.ffn} GELU-tanh, {ctx.shape[0]} context rows, "
+                                f"LoRA r{cfg.lora_rank} merged, +-{cfg.radius} frame window"),
+                   "tokens": tokens, "hidden": cfg.hidden, "heads": cfg.heads,
+                   "head_dim": cfg.head_dim, "ffn": cfg.ffn, "context": ctx.shape[0],
+                   "parallelism": "single GPU"},
+        "roofline": {"kernel": "vdn_mxfp8_gemm (all 9 block projections)", "bound": "mfma",
+                     "achieved": round(gemm_tflops, 1), "peak": PEAK_MXFP8_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_MXFP8_TFLOPS, 4),
+                     "traffic": traffic,
+                     "avg_launch_ms": round(g[1] / g[0], 4),
+                     "flop_per_launch": g[2] / g[0]},
+        "mxfp8_tflops": round(gemm_tflops, 1),
+        "vda_gbs": round(vda_gbs, 1), "vda_hbm_frac": round(vda_gbs / PEAK_HBM_GBS, 4),
+        "vda_ms": round(vda_t / args.steps, 3),
+        "window_attention_tflops": round(w[2] / (w[1] * 1e-3) / 1e12, 1),
+        "window_attention_bf16_frac": round(w[2] / (w[1] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "breakdown": breakdown,
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        sample = min(args.cpu_sample_frames, frames)
+        log(f"timing the CPU fp32 path on {sample} frames")
+        result["cpu_baseline"] = cpu_baseline(cfg, weights, hidden, temb, ctx, cos, sin, frames,
+                                              sample)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -62,17 +62,22 @@ int vdn_mxfp8_prenorm_quantize(const void* x, int64_t rows, int64_t k, int64_t r
                                uint8_t* finite, void* stream);
 
 /*
- * Block-scaled GEMM: out[r, c] = bf16(sum_k dq(a)[r, k] * dq(w)[c, k]) (+ bf16 bias[c]),
- * r < out_rows <= mp, c < n <= np, out row stride ldc. a: codes [mp, kp] + scales,
- * w: codes [np, kp] + scales (mp, np, kp multiples of 128). mode 0 stores, mode 1 adds
- * into out (out = bf16(out + y)). *nonfinite (nullable) becomes 1 on a nonfinite output.
+ * Block-scaled GEMM: y[r, c] = bf16(sum_k dq(a)[r, k] * dq(w)[c, k]), r < out_rows <= mp,
+ * c < n <= np. a: codes [mp, kp] + scales, w: codes [np, kp] + scales (mp, np, kp multiples
+ * of 128). Epilogue, each step rounded to bf16 (all operands bf16, nullable):
+ *   y = y + bias[c];  y = addend[r, c] + y;  y = residual[r, c] + gate[c] * y
+ * (gate requires residual; gate null means 1), stored to out (row stride ldc; out may alias
+ * addend or residual). *nonfinite (nullable) becomes 1 on a nonfinite output.
  * Replaces: F.scaled_mm(BlockWise1x32, SWIZZLE_32_4_4) + crop + bias in
- * MXFP8Linear.forward_quantized (src/models/ops/mxfp8_linear.py:61-93).
+ * MXFP8Linear.forward_quantized (src/models/ops/mxfp8_linear.py:61-93); the addend and gated
+ * residual are the block's `out[video] += to_out_linear(...)` (hybrid_attention.py:254) and
+ * `hidden + gate * branch` (src/models/ops/fused_block.py:49-51).
  */
 int vdn_mxfp8_gemm(const void* a, const void* a_scales, int64_t mp, const void* w,
-                   const void* w_scales, int64_t np, int64_t kp, const void* bias, void* out,
-                   int64_t out_rows, int64_t n, int64_t ldc, int mode, uint32_t* nonfinite,
-                   void* stream);
+                   const void* w_scales, int64_t np, int64_t kp, const void* bias,
+                   const void* addend, int64_t ld_add, const void* residual, int64_t ld_res,
+                   const void* gate, void* out, int64_t out_rows, int64_t n, int64_t ldc,
+                   uint32_t* nonfinite, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * VDA linear-attention branch (D = 128). A 4-D operand "(f, h, s, c)" is addressed as
@@ -186,6 +191,7 @@ int vdn_vda_epilogue(const void* readout, const void* weight, int weight_f32, fl
  * strides (token, head, channel); weights [head_dim] with stride (flags bit0 / bit1: fp32
  * q / k weight, else bf16); cos, sin (nullable together): [tokens, rot] with strides, fp32
  * when flags bit2 else bf16 (values rounded to bf16 before use). qo, ko: contiguous bf16.
+ * flags bit3: q only (k, k's weight and ko may be null).
  * Replaces: paper_qk_rmsnorm_rope (src/models/softmax_attention/paper_qk_rope.py:145-211).
  */
 int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64_t q_sd, const void* k,

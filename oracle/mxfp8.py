@@ -27,7 +27,19 @@ def e4m3fn_encode(v: np.ndarray) -> np.ndarray:
     m/8 * 2^-6, no infinities. Used by the reference through torch's
     `.to(torch.float8_e4m3fn)` (mxfp8_quant.py:71-72).
     """
-    bits = np.ascontiguousarray(v, dtype=np.float32).view(np.uint32).astype(np.int64)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    if v.size > _CHUNK:
+        flat = v.reshape(-1)
+        return np.concatenate([_encode(flat[i:i + _CHUNK]) for i in range(0, flat.size, _CHUNK)]
+                              ).reshape(v.shape)
+    return _encode(v)
+
+
+_CHUNK = 1 << 18
+
+
+def _encode(v: np.ndarray) -> np.ndarray:
+    bits = v.view(np.uint32).astype(np.int64)
     sign = (bits >> 31) & 1
     exp = (bits >> 23) & 0xFF
     man = (bits & 0x7FFFFF) | np.where(exp > 0, 0x800000, 0)
@@ -110,6 +122,12 @@ def quantize(x: np.ndarray) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
 
     Reference: mxfp8_quant.py:40-74 / mxfp8_kernels.py:31-46. Padding is zero (scale byte 0).
     """
+    codes, natural = quantize_natural(x)
+    return codes, natural, swizzle(natural)
+
+
+def quantize_natural(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """quantize() without the swizzled copy: (codes [RP,KP], natural scales [RP,KP/32])."""
     x = np.asarray(x, dtype=np.float32)
     r, k = x.shape
     rp, kp = pad128(r), pad128(k)
@@ -122,12 +140,18 @@ def quantize(x: np.ndarray) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
     scaled = (blocks * inv[..., None]).astype(np.float32)
     codes = e4m3fn_encode(scaled).reshape(rp, kp)
     natural = (e + 127).astype(np.uint8)
-    return codes, natural, swizzle(natural)
+    return codes, natural
+
+
+_DECODE = None
 
 
 def dequant(codes: np.ndarray, natural: np.ndarray) -> np.ndarray:
+    global _DECODE
+    if _DECODE is None:
+        _DECODE = e4m3fn_decode(np.arange(256))
     rp, kp = codes.shape
-    vals = e4m3fn_decode(codes).reshape(rp, kp // 32, 32)
+    vals = _DECODE[codes].reshape(rp, kp // 32, 32)
     return (vals * np.exp2(natural.astype(np.float64) - 127)[..., None]).reshape(rp, kp)
 
 

@@ -43,6 +43,6 @@ def test_invalid_arguments_are_rejected_without_a_device():
     # Argument validation happens before any HIP call, so these run on a CPU-only host.
     assert lib.vdn_mxfp8_quantize(None, 4, 0, 4, None, None, None, None) != 0
     assert b"K > 0" in lib.vdn_last_error()
-    assert lib.vdn_mxfp8_gemm(None, None, 128, None, None, 128, 128, None, None, 1, 1, 1, 0,
-                              None, None) != 0
+    assert lib.vdn_mxfp8_gemm(None, None, 128, None, None, 128, 128, None, None, 0, None, 0,
+                              None, None, 1, 1, 1, None, None) != 0
     assert b"null pointer" in lib.vdn_last_error()

@@ -1,0 +1,107 @@
+"""Hybrid DiT block on the GPU against the block oracle: piece by piece on the run's own
+inputs, and end to end. Widths: a small block and the full 5120-wide block (40 x 128 heads,
+FFN 13824, 512 context rows) on a short clip. Tolerance: relative L2 <= 1e-2 on every
+projection, attention output and residual-stage delta."""
+import pytest
+import torch
+
+from oracle import block as ob
+from oracle import window as ow
+from vdn_amd import window as vw
+from vdn_amd.block import (BlockConfig, BlockWeights, HybridDiTBlock, cross_attention_plan,
+                           make_inputs)
+
+pytestmark = pytest.mark.gpu
+
+SMALL = BlockConfig(hidden=256, heads=2, head_dim=128, ffn=384, context=16, lora_rank=8,
+                    lora_scale=0.5)
+WIDE = BlockConfig()
+REL = 1e-2
+
+
+def rel_l2(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def run(cfg, frames, height, width, seed):
+    torch.manual_seed(seed)
+    w = BlockWeights.random(cfg, seed, device="cuda")
+    block = HybridDiTBlock(cfg, w)
+    hidden, temb, ctx, layout, (cos, sin) = make_inputs(cfg, frames, height, width, seed + 1,
+                                                       device="cuda")
+    plan = vw.prepare_paper_window_plan(layout, vw.window_bounds(frames, cfg.radius),
+                                        device="cuda")
+    cplan = cross_attention_plan(hidden.shape[0], ctx.shape[0], "cuda")
+    out, parts = block(hidden, temb, ctx, layout, (cos, sin), plan, cplan, return_parts=True)
+    torch.cuda.synchronize()
+    cpu = {k: v.cpu() for k, v in w.tensors.items()}
+    oracle = ob.BlockOracle(cpu, cfg)
+    parts = {k: (tuple(x.cpu() for x in v) if isinstance(v, tuple) else v.cpu())
+             for k, v in parts.items()}
+    return dict(cfg=cfg, oracle=oracle, hidden=hidden.cpu(), temb=temb.cpu(), ctx=ctx.cpu(),
+                cos=cos.cpu(), sin=sin.cpu(), out=out.cpu(), parts=parts,
+                geometry=(frames, height, width))
+
+
+def check(r):
+    cfg, orc, p = r["cfg"], r["oracle"], r["parts"]
+    frames, height, width = r["geometry"]
+    h0 = r["hidden"].double()
+    tables = orc.tables(r["temb"])
+    for mine, theirs in zip(p["tables"], tables):
+        assert rel_l2(mine, theirs) < 4e-3
+    gpu_tables = tuple(t.double() for t in p["tables"])
+    given = {k: p[k] for k in ("x1", "qkv", "soft", "attn", "far")}
+    h1, own = orc.attention_stage(h0, gpu_tables, frames, height, width, r["cos"], r["sin"],
+                                  given=given)
+    errors = {name: rel_l2(p[name], own[name]) for name in ("x1", "qkv", "soft", "attn", "far")}
+    errors["h1 delta"] = rel_l2(p["h1"].double() - h0, h1 - h0)
+    h1g = p["h1"].double()
+    h2, own = orc.cross_stage(h1g, r["ctx"], given={"co": p["co"]})
+    errors["co"] = rel_l2(p["co"], own["co"])
+    errors["h2 delta"] = rel_l2(p["h2"].double() - h1g, h2 - h1g)
+    h2g = p["h2"].double()
+    h3, own = orc.ffn_stage(h2g, gpu_tables, given={"up": p["up"]})
+    errors["up"] = rel_l2(p["up"], own["up"])
+    errors["h3 delta"] = rel_l2(r["out"].double() - h2g, h3 - h2g)
+    print({k: f"{v:.2e}" for k, v in errors.items()}, flush=True)
+    bad = {k: v for k, v in errors.items() if not v < REL}
+    assert not bad, bad
+    # end to end from the oracle's own tables and stages
+    free, _ = orc.forward(r["hidden"], r["temb"], r["ctx"], frames, height, width, r["cos"],
+                          r["sin"])
+    end = rel_l2(r["out"].double() - h0, free - h0)
+    print(f"end-to-end block delta rel-L2 {end:.2e}", flush=True)
+    assert end < 2 * REL
+
+
+def test_small_block_matches_oracle():
+    check(run(SMALL, 4, 4, 8, seed=11))
+
+
+def test_full_width_block_short_clip_matches_oracle():
+    check(run(WIDE, 4, 4, 8, seed=12))
+
+
+def test_block_input_is_not_mutated_and_padding_rows_are_ignored():
+    cfg = SMALL
+    w = BlockWeights.random(cfg, 3, device="cuda")
+    block = HybridDiTBlock(cfg, w)
+    hidden, temb, ctx, layout, rope = make_inputs(cfg, 3, 5, 7, 4, device="cuda")
+    keep = hidden.clone()
+    plan = vw.prepare_paper_window_plan(layout, vw.window_bounds(3, 1), device="cuda")
+    cplan = cross_attention_plan(hidden.shape[0], ctx.shape[0], "cuda")
+    a = block(hidden, temb, ctx, layout, rope, plan, cplan)
+    b = block(hidden, temb, ctx, layout, rope, plan, cplan)
+    torch.cuda.synchronize()
+    assert torch.equal(hidden, keep)
+    assert torch.equal(a, b), "the block is deterministic run to run"
+    assert torch.isfinite(a.float()).all()
+
+
+def test_rope_tables_match_the_oracle_restatement():
+    cos, sin = vw.rope_tables_3d(3, 5, 7, device="cuda", dtype=torch.float32)
+    oc, os_ = ow.rope_tables_3d(3, 5, 7)
+    assert torch.allclose(cos.cpu().double(), oc, atol=1e-6)
+    assert torch.allclose(sin.cpu().double(), os_, atol=1e-6)

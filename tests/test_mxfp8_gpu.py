@@ -256,6 +256,58 @@ def test_gemm_accumulate_and_bias(device):
     assert (bf16_ulps(got, ref) == 0).mean() > 0.99
 
 
+@pytest.mark.parametrize("in_place", [False, True])
+def test_gemm_gated_residual_epilogue(device, in_place):
+    """out = bf16(res + bf16(gate * bf16(addend + bf16(bf16(acc) + bias)))) with a strided
+    residual/addend, optionally written over the residual itself."""
+    m, n, k = 260, 384, 512
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g) * 0.05).to(torch.bfloat16)
+    bias = torch.randn(n, generator=g).to(torch.bfloat16)
+    gate = torch.randn(n, generator=g).to(torch.bfloat16)
+    wide = torch.randn(m, 2 * n, generator=g).to(torch.bfloat16)
+    res, add = wide[:, :n], wide[:, n:]
+    q, s = vm.quantize_activation(x.to(device))
+    wq, ws = vm.quantize_activation(w.to(device))
+    wide_d = wide.to(device)
+    res_d, add_d = wide_d[:, :n], wide_d[:, n:]
+    out = res_d if in_place else None
+    y = vm.mxfp8_gemm(q, s, wq, ws, n, rows=m, bias=bias.to(device), out=out, addend=add_d,
+                      residual=res_d, gate=gate.to(device))
+    if in_place:
+        assert y.data_ptr() == res_d.data_ptr()
+    ac, an, _ = om.quantize(x.float().numpy())
+    wc, wn, _ = om.quantize(w.float().numpy())
+    f = lambda t: t.float().numpy()
+    y0 = om.bf16_round(om.gemm(ac, an, wc, wn, m, n))
+    y1 = om.bf16_round(y0 + f(bias)[None])
+    y2 = om.bf16_round(f(add) + y1)
+    gy = om.bf16_round(f(gate)[None] * y2)
+    ref = om.bf16_round(f(res) + gy)
+    got = y.float().cpu().numpy()
+    gabs = np.abs(f(gate))[None]
+    mag = om.gemm_magnitude(ac, an, wc, wn, m, n)
+    limit = (gabs * (om.bf16_ulp(y0) + om.bf16_ulp(y1) + om.bf16_ulp(y2)
+                     + om.MFMA_ACCUMULATION_BOUND * mag) + om.bf16_ulp(gy) + om.bf16_ulp(ref))
+    err = np.abs(got.astype(np.float64) - ref)
+    assert (err <= limit).all(), float((err / limit).max())
+    assert (bf16_ulps(got, ref) == 0).mean() > 0.99
+    if not in_place:
+        assert torch.equal(wide_d.cpu(), wide), "inputs are not modified"
+
+
+def test_gemm_epilogue_argument_errors(device):
+    q, s = vm.quantize_activation(torch.ones(4, 32, dtype=torch.bfloat16, device=device))
+    wq, ws = vm.quantize_activation(torch.ones(8, 32, dtype=torch.bfloat16, device=device))
+    gate = torch.ones(8, dtype=torch.bfloat16, device=device)
+    with pytest.raises(ValueError, match="gate needs a residual"):
+        vm.mxfp8_gemm(q, s, wq, ws, 8, rows=4, gate=gate)
+    with pytest.raises(ValueError, match="residual must be"):
+        vm.mxfp8_gemm(q, s, wq, ws, 8, rows=4, residual=torch.ones(4, 7, dtype=torch.bfloat16,
+                                                                    device=device))
+
+
 def test_linear_api_paths_agree(device):
     torch.manual_seed(9)
     x = torch.randn(129, 256, dtype=torch.bfloat16, device=device)

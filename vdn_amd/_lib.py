@@ -28,8 +28,8 @@ SIGNATURES = {
     "vdn_mxfp8_act_quantize": [_ptr, _i64, _i64, _i64, _i32, _ptr, _ptr, _ptr, _ptr],
     "vdn_mxfp8_prenorm_quantize": [_ptr, _i64, _i64, _i64, _ptr, _f32, _ptr, _i64, _ptr, _i64,
                                    _ptr, _i32, _ptr, _ptr, _ptr, _ptr, _ptr],
-    "vdn_mxfp8_gemm": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64, _i64,
-                       _i32, _ptr, _ptr],
+    "vdn_mxfp8_gemm": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _ptr, _ptr, _i64, _ptr, _i64,
+                       _ptr, _ptr, _i64, _i64, _i64, _ptr, _ptr],
     "vdn_vda_prepare": [_ptr, _i64, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _ptr, _ptr],
     "vdn_vda_statistics": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64,
                            _i32, _i32, _i32, _i32, _i32, _ptr, _ptr, _ptr],
@@ -82,11 +82,45 @@ def exported_symbols() -> list[str]:
     return ["vdn_last_error", "vdn_abi_version", *SIGNATURES]
 
 
+class LaunchTimer:
+    """Records a pair of timing events around every call of the named entry points while
+    active (`with LaunchTimer({...}) as t:`). The events go on the caller's current stream,
+    the stream every entry point launches on, so each pair brackets that launch."""
+
+    def __init__(self, names):
+        self.names = set(names)
+        self.records = []
+
+    def __enter__(self):
+        _TIMERS.append(self)
+        return self
+
+    def __exit__(self, *exc):
+        _TIMERS.remove(self)
+
+    def durations(self):
+        """[(name, args, milliseconds)] after synchronising the device."""
+        torch.cuda.synchronize()
+        return [(n, a, s.elapsed_time(e)) for n, a, s, e in self.records]
+
+
+_TIMERS: list[LaunchTimer] = []
+
+
 def call(name: str, *args) -> None:
     lib = load()
+    timers = [t for t in _TIMERS if name in t.names]
+    if timers:
+        start = torch.cuda.Event(enable_timing=True)
+        start.record()
     status = getattr(lib, name)(*args)
     if status != 0:
         raise RuntimeError(f"{name} failed ({status}): {lib.vdn_last_error().decode()}")
+    if timers:
+        end = torch.cuda.Event(enable_timing=True)
+        end.record()
+        for t in timers:
+            t.records.append((name, args, start, end))
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

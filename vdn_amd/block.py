@@ -1,0 +1,283 @@
+"""Hybrid-attention DiT block forward on gfx950 kernels (MXFP8 GEMMs, window softmax, VDA).
+
+Composition (reference: src/models/ops/fused_block.py:134-169 paper_block_forward with fused
+producers; src/inference/utils/tensor_parallel.py:169-228 tp_attention_forward at world size
+1; src/models/hybrid_attention.py:178-255; src/inference/utils/paper_adaln.py:174-188 AdaLN
+tables; src/inference/utils/lora.py:80-107 LoRA merge):
+
+  shift/scale/gate (attn, mlp) = Linear(SiLU(temb.float()).to(bf16))            6 x [1, H]
+  x1, q1 = prenorm-quantize(h; norm1, scale_msa, shift_msa)                       bf16 + MXFP8
+  qkv    = MXFP8 GEMM(q1, W_qkv + B_lora A_lora)                                  [T, 3H]
+  gates  = sigmoid(softmax_gate(x1)), beta = sigmoid(beta_proj(x1)),
+           lin_gate = sigmoid(up(down(x1))), alpha = FrameKDAAlpha(frame mean of x1)
+  soft   = window attention(QK-RMSNorm + 3D RoPE(q, k), v) * gate                 [T, H]
+  far    = VDA(raw q, k, v, beta, lin_gate, alpha)                                [T, H]
+  h      = h + gate_msa * (O(soft) + O_lin(far))            one GEMM epilogue each
+  h      = h + O_c(cross attention(RMSNorm3(h) -> q, context -> k, v))
+  x2, q2 = prenorm-quantize(h; norm2, scale_mlp, shift_mlp)
+  h      = h + gate_mlp * down(GELU-tanh(up(q2)))           GELU fused into its MXFP8 producer
+
+The GELU-tanh FFN and the cross-attention have no reference kernel (the reference block uses
+SwiGLU and packs text into the sequence); they follow the torch definitions (GELU
+approximate='tanh'; cross-attention = QK-RMSNorm'd SDPA over the context rows, unmasked).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import mxfp8 as mx
+from . import vda as vv
+from . import window as vw
+
+
+@dataclass(frozen=True)
+class BlockConfig:
+    hidden: int = 5120
+    heads: int = 40
+    head_dim: int = 128
+    ffn: int = 13824
+    context: int = 512
+    lora_rank: int = 64
+    lora_scale: float = 1.0
+    eps: float = 1e-6
+    radius: int = 1
+    rope_dims: tuple = (44, 42, 42)
+    rope_theta: float = 10000.0
+    vda_chunk: int = 8
+    init_std: float = 0.02
+
+
+@dataclass
+class BlockWeights:
+    """bf16 master weights of one block (random init), the source of both the MXFP8
+    buffers and the oracle."""
+    tensors: dict
+
+    def __getattr__(self, name):
+        try:
+            return self.tensors[name]
+        except KeyError as e:
+            raise AttributeError(name) from e
+
+    @staticmethod
+    def random(cfg: BlockConfig, seed: int = 0, device="cpu") -> "BlockWeights":
+        g = torch.Generator(device=device).manual_seed(seed)
+        hd, h, n, f, r = cfg.hidden, cfg.heads, cfg.head_dim, cfg.ffn, cfg.lora_rank
+
+        def normal(*shape, std=cfg.init_std):
+            return (torch.randn(*shape, generator=g, device=device) * std).to(torch.bfloat16)
+
+        def ones_ish(size):
+            return (1.0 + torch.randn(size, generator=g, device=device) * 0.1).to(torch.bfloat16)
+
+        a = torch.empty(h, device=device).uniform_(1, 16, generator=g)
+        dt = torch.exp(torch.rand(h * n, generator=g, device=device)
+                       * (math.log(0.1) - math.log(0.001)) + math.log(0.001)).clamp(min=1e-4)
+        t = dict(
+            adaln_w=normal(6 * hd, hd), adaln_b=normal(6 * hd),
+            norm1=ones_ish(hd), norm2=ones_ish(hd), norm3=ones_ish(hd),
+            qkv_w=normal(3 * hd, hd), qkv_b=normal(3 * hd),
+            lora_a=normal(3, r, hd), lora_b=normal(3, hd, r),
+            norm_q=ones_ish(n), norm_k=ones_ish(n),
+            o_w=normal(hd, hd), o_b=normal(hd), olin_w=normal(hd, hd),
+            soft_gate_w=normal(h, hd), soft_gate_b=normal(h),
+            beta_w=normal(h, hd),
+            lgate_down_w=normal(n, hd), lgate_up_w=normal(hd, n), lgate_up_b=normal(hd),
+            alpha_down_w=normal(n, hd), alpha_up_w=normal(hd, n),
+            a_log=torch.log(a).float(), dt_bias=(dt + torch.log(-torch.expm1(-dt))).float(),
+            vda_norm=ones_ish(n),
+            cq_w=normal(hd, hd), cq_b=normal(hd), ck_w=normal(hd, hd), ck_b=normal(hd),
+            cv_w=normal(hd, hd), cv_b=normal(hd), co_w=normal(hd, hd), co_b=normal(hd),
+            norm_qc=ones_ish(n), norm_kc=ones_ish(n),
+            up_w=normal(f, hd), up_b=normal(f), down_w=normal(hd, f), down_b=normal(hd),
+        )
+        return BlockWeights(t)
+
+    def merged_qkv(self, scale: float) -> torch.Tensor:
+        """W_qkv with the rank-r LoRA of Q, K, V folded in: W += bf16(scale * (B @ A) in fp32)
+        (lora.py:105-107)."""
+        hd = self.qkv_w.shape[1]
+        w = self.qkv_w.clone()
+        for i in range(3):
+            delta = (self.lora_b[i].float() @ self.lora_a[i].float()) * scale
+            w[i * hd:(i + 1) * hd].add_(delta.to(w.dtype))
+        return w
+
+
+def _linear(weight, bias=None):
+    lin = nn.Linear(weight.shape[1], weight.shape[0], bias=bias is not None, device=weight.device,
+                    dtype=weight.dtype)
+    with torch.no_grad():
+        lin.weight.copy_(weight)
+        if bias is not None:
+            lin.bias.copy_(bias)
+    return lin
+
+
+class HybridDiTBlock(nn.Module):
+    """One hybrid DiT block; every projection in the attention/FFN path is an MXFP8Linear."""
+
+    def __init__(self, cfg: BlockConfig, weights: BlockWeights):
+        super().__init__()
+        self.cfg = cfg
+        w = weights
+        mk = lambda weight, bias=None: mx.MXFP8Linear(_linear(weight, bias), check_finite=False)
+        self.qkv = mk(w.merged_qkv(cfg.lora_scale), w.qkv_b)
+        self.o = mk(w.o_w, w.o_b)
+        self.olin = mk(w.olin_w)
+        self.cq, self.ck, self.cv, self.co = (mk(w.cq_w, w.cq_b), mk(w.ck_w, w.ck_b),
+                                              mk(w.cv_w, w.cv_b), mk(w.co_w, w.co_b))
+        self.up, self.down = mk(w.up_w, w.up_b), mk(w.down_w, w.down_b)
+        # small bf16 projections of the attention input, one GEMM: softmax gate | beta | gate down
+        self.small_w = torch.cat((w.soft_gate_w, w.beta_w, w.lgate_down_w))
+        self.keep = {k: w.tensors[k] for k in (
+            "adaln_w", "adaln_b", "norm1", "norm2", "norm3", "norm_q", "norm_k", "soft_gate_b",
+            "lgate_up_w", "lgate_up_b", "alpha_down_w", "alpha_up_w", "a_log", "dt_bias",
+            "vda_norm", "norm_qc", "norm_kc")}
+        self._zero_table = None
+
+    # ---------------------------------------------------------------- pieces ----
+    def adaln_tables(self, temb):
+        """6 tables [1, H]: shift/scale/gate attention, then MLP (paper_adaln.py:174-188, 205-212)."""
+        k = self.keep
+        projected = F.linear(F.silu(temb.float()).to(k["adaln_w"].dtype), k["adaln_w"], k["adaln_b"])
+        return projected.view(-1, 6 * self.cfg.hidden).chunk(6, dim=-1)
+
+    def frame_alpha(self, frame_mean):
+        k, cfg = self.keep, self.cfg
+        delta = F.linear(F.linear(frame_mean.float(), k["alpha_down_w"].float()),
+                         k["alpha_up_w"].float()) + k["dt_bias"]
+        scale = torch.exp(k["a_log"])[:, None]
+        return torch.exp(-scale * F.softplus(delta.view(-1, cfg.heads, cfg.head_dim))).contiguous()
+
+    def _zeros(self, device):
+        if self._zero_table is None or self._zero_table.device != device:
+            self._zero_table = torch.zeros(1, self.cfg.hidden, dtype=torch.bfloat16, device=device)
+        return self._zero_table
+
+    # --------------------------------------------------------------- forward ----
+    @torch.no_grad()
+    def forward(self, hidden, temb, context, layout: vw.SequenceLayout, rope, window_plan,
+                cross_plan, return_parts=False):
+        """hidden [T, H] bf16 (video rows), temb [1, H], context [L, H] bf16; rope = (cos, sin)
+        [T, 128]; window_plan from prepare_paper_window_plan; cross_plan from cross_attention_plan.
+        Returns the new hidden [T, H] (a fresh tensor); with return_parts also a dict of
+        intermediate copies (tables, x1, qkv, soft, attn, far, h1, co, h2, up) for checking."""
+        cfg, k = self.cfg, self.keep
+        T, hd = hidden.shape
+        heads, d = cfg.heads, cfg.head_dim
+        frames, spatial = layout.num_frames, layout.tokens_per_frame
+        dev = hidden.device
+        shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = self.adaln_tables(temb)
+        idx = torch.zeros(T, dtype=torch.long, device=dev)
+        h = hidden.clone()
+        parts = {} if return_parts else None
+
+        def snap(name, t):
+            if parts is not None:
+                parts[name] = t.clone() if isinstance(t, torch.Tensor) else t
+
+        # ---- hybrid self-attention ----
+        x1, q1, s1, _ = mx.launch_prenorm_quantize(h, k["norm1"], cfg.eps, scale_msa, shift_msa,
+                                                   idx, write_bf16=True)
+        qkv = self.qkv.forward_quantized(q1, s1, rows=T)
+        snap("tables", (shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp))
+        snap("x1", x1)
+        snap("qkv", qkv)
+        raw_q = qkv[:, :hd].view(T, heads, d)
+        raw_k = qkv[:, hd:2 * hd].view(T, heads, d)
+        value = qkv[:, 2 * hd:].view(T, heads, d)
+        small = F.linear(x1, self.small_w)
+        soft_gate = torch.sigmoid(small[:, :heads] + k["soft_gate_b"])
+        beta = torch.sigmoid(small[:, heads:2 * heads])
+        lin_gate = torch.sigmoid(F.linear(small[:, 2 * heads:], k["lgate_up_w"], k["lgate_up_b"]))
+        frame_mean = x1.view(frames, spatial, hd).float().mean(1)
+        alpha = self.frame_alpha(frame_mean)
+        cos, sin = rope
+        q, kk = vw.paper_qk_rmsnorm_rope(raw_q, raw_k, k["norm_q"], k["norm_k"], cfg.eps, cos, sin,
+                                         enabled=True)
+        soft = vw.paper_window_attention(q, kk, value, window_plan, d ** -0.5, enabled=True,
+                                         gate=soft_gate)
+        del q, kk
+        snap("soft", soft.view(T, hd))
+        qs, ss = mx.launch_quantize(soft.view(T, hd))
+        attn = self.o.forward_quantized(qs, ss, rows=T)
+        snap("attn", attn)
+        del soft, qs, ss
+        bounds = window_plan.bounds
+        far = vv.vda_forward(raw_q, raw_k, value, beta, lin_gate.view(T, heads, d), alpha, bounds,
+                             frames, spatial, k["vda_norm"], cfg.eps, chunk_size=cfg.vda_chunk)
+        del qkv, raw_q, raw_k, value, lin_gate
+        snap("far", far)
+        qf, sf = mx.launch_quantize(far)
+        self.olin.forward_quantized(qf, sf, rows=T, out=h, addend=attn, residual=h, gate=gate_msa)
+        snap("h1", h)
+        del far, qf, sf, attn
+
+        # ---- cross-attention to the context rows ----
+        zeros = self._zeros(dev)
+        _, q3, s3, _ = mx.launch_prenorm_quantize(h, k["norm3"], cfg.eps, zeros, zeros, idx,
+                                                  write_bf16=False)
+        cq = self.cq.forward_quantized(q3, s3, rows=T).view(T, heads, d)
+        cx, csx = mx.launch_quantize(context)
+        L = context.shape[0]
+        ck = self.ck.forward_quantized(cx, csx, rows=L).view(L, heads, d)
+        cv = self.cv.forward_quantized(cx, csx, rows=L).view(L, heads, d)
+        cq = vw.qk_rmsnorm(cq, k["norm_qc"], cfg.eps)
+        ck = vw.qk_rmsnorm(ck, k["norm_kc"], cfg.eps)
+        co = cross_attention(cq, ck, cv, cross_plan, d ** -0.5)
+        del cq, ck, cv
+        snap("co", co.view(T, hd))
+        qo, so = mx.launch_quantize(co.view(T, hd))
+        del co
+        self.co.forward_quantized(qo, so, rows=T, out=h, residual=h)
+        del qo, so
+        snap("h2", h)
+
+        # ---- FFN ----
+        _, q4, s4, _ = mx.launch_prenorm_quantize(h, k["norm2"], cfg.eps, scale_mlp, shift_mlp,
+                                                  idx, write_bf16=False)
+        up = self.up.forward_quantized(q4, s4, rows=T)
+        snap("up", up)
+        q5, s5, _ = mx.launch_gelu_quantize(up)
+        del up
+        self.down.forward_quantized(q5, s5, rows=T, out=h, residual=h, gate=gate_mlp)
+        return (h, parts) if return_parts else h
+
+
+def cross_attention_plan(num_queries: int, num_keys: int, device) -> vw.DevicePlan:
+    """Every query sees every context key: one group, one key interval [0, num_keys)."""
+    return vw._device_plan([(((0, num_queries),), ((0, num_keys),))], torch.device(device))
+
+
+def cross_attention(q, k, v, plan: vw.DevicePlan, scale):
+    """Unmasked attention of q [T, H, D] over context k, v [L, H, D] on the window kernel."""
+    from . import _lib
+    T, h, d = q.shape
+    out = torch.empty_like(q)
+    _lib.call("vdn_window_attention", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
+              k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
+              plan.blocks.data_ptr(), plan.nblocks, plan.intervals.data_ptr(),
+              plan.counts.data_ptr(), h, float(scale), None, 0, 0, out.data_ptr(), out.stride(0),
+              out.stride(1), None, 0, 0, _lib.stream(q.device))
+    return out
+
+
+def make_inputs(cfg: BlockConfig, frames: int, height: int, width: int, seed: int = 1,
+                device="cpu"):
+    """Synthetic block inputs: hidden ~ N(0,1) bf16 [F*h*w, H], temb ~ N(0,1) [1, H],
+    context ~ N(0,1) bf16 [cfg.context, H]; 3D RoPE tables; +-radius frame window plan."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    T = frames * height * width
+    hidden = torch.randn(T, cfg.hidden, generator=g, device=device).to(torch.bfloat16)
+    temb = torch.randn(1, cfg.hidden, generator=g, device=device)
+    context = torch.randn(cfg.context, cfg.hidden, generator=g, device=device).to(torch.bfloat16)
+    layout = vw.SequenceLayout(T, 0, frames, height * width, frame_height=height, frame_width=width)
+    cos, sin = vw.rope_tables_3d(frames, height, width, dims=cfg.rope_dims, theta=cfg.rope_theta,
+                                 device=device, dtype=torch.bfloat16)
+    return hidden, temb, context, layout, (cos, sin)

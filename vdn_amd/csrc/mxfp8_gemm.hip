@@ -46,15 +46,29 @@ __device__ __forceinline__ uint32_t scale_word(const uint8_t* __restrict__ s_ste
   return *reinterpret_cast<const uint32_t*>(s_step + row_off);
 }
 
-enum Mode : int { kStore = 0, kAccumulate = 1 };
+// Epilogue of one output element y (the bf16-rounded accumulator), in this order:
+//   y = bf16(y + bias[c])                    (bias: nullable, [n])
+//   y = bf16(addend[r, c] + y)               (addend: nullable)
+//   y = bf16(residual[r, c] + bf16(gate[c] * y))   (residual: nullable; gate nullable = 1)
+// `out` may alias `addend` or `residual`: every element is read and written by one lane.
+struct Epilogue {
+  const uint16_t* bias;
+  const uint16_t* addend;
+  int64_t ld_add;
+  const uint16_t* residual;
+  int64_t ld_res;
+  const uint16_t* gate;
+  uint16_t* out;
+  int64_t ldc;
+  uint32_t* nonfinite;
+};
 
 template <int BM, int BN, int WGM, int WGN>
 __global__ void __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
                   const uint8_t* __restrict__ W, const uint8_t* __restrict__ Ws, int64_t mp,
-                  int64_t np, int64_t kp, const uint16_t* __restrict__ bias,
-                  uint16_t* __restrict__ C, int64_t out_rows, int64_t n, int64_t ldc, int mode,
-                  uint32_t* __restrict__ nonfinite, int tiles_m, int tiles_n, int group_m) {
+                  int64_t np, int64_t kp, Epilogue ep, int64_t out_rows, int64_t n,
+                  int tiles_m, int tiles_n, int group_m) {
   constexpr int kWaves = WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 16, TN = WN / 16;
@@ -199,7 +213,8 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
   for (int nt = 0; nt < TN; ++nt) {
     const int64_t col = n0 + wn * WN + nt * 16 + frag_row;
     if (col >= n) continue;
-    const float b = bias != nullptr ? bf16_bits_to_f32(bias[col]) : 0.f;
+    const float b = ep.bias != nullptr ? bf16_bits_to_f32(ep.bias[col]) : 0.f;
+    const float gt = ep.gate != nullptr ? bf16_bits_to_f32(ep.gate[col]) : 1.f;
 #pragma unroll
     for (int mt = 0; mt < TM; ++mt) {
 #pragma unroll
@@ -207,30 +222,32 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
         const int64_t row = m0 + wm * WM + mt * 16 + (lane >> 4) * 4 + v;
         if (row >= out_rows) continue;
         float y = round_bf16(acc[mt][nt][v]);
-        if (bias != nullptr) y = round_bf16(y + b);
-        uint16_t* dst = C + row * ldc + col;
-        if (mode == kAccumulate) y = round_bf16(bf16_bits_to_f32(*dst) + y);
+        if (ep.bias != nullptr) y = round_bf16(y + b);
+        if (ep.addend != nullptr) y = round_bf16(bf16_bits_to_f32(ep.addend[row * ep.ld_add + col]) + y);
+        if (ep.residual != nullptr) {
+          const float t = ep.gate != nullptr ? round_bf16(gt * y) : y;
+          y = round_bf16(bf16_bits_to_f32(ep.residual[row * ep.ld_res + col]) + t);
+        }
         bad = bad || !(fabsf(y) < INFINITY);
-        *dst = f32_to_bf16_bits(y);
+        ep.out[row * ep.ldc + col] = f32_to_bf16_bits(y);
       }
     }
   }
-  if (nonfinite != nullptr && __ballot(bad) != 0 && lane == 0) atomicOr(nonfinite, 1u);
+  if (ep.nonfinite != nullptr && __ballot(bad) != 0 && lane == 0) atomicOr(ep.nonfinite, 1u);
 }
 
 template <int BM, int BN, int WGM, int WGN>
 int launch_gemm(const uint8_t* a, const uint8_t* as, int64_t mp, const uint8_t* w,
-                const uint8_t* ws, int64_t np, int64_t kp, const uint16_t* bias, uint16_t* out,
-                int64_t out_rows, int64_t n, int64_t ldc, int mode, uint32_t* nonfinite,
-                hipStream_t stream) {
+                const uint8_t* ws, int64_t np, int64_t kp, const Epilogue& ep, int64_t out_rows,
+                int64_t n, hipStream_t stream) {
   const int64_t tiles_m = (mp + BM - 1) / BM, tiles_n = (np + BN - 1) / BN;
   if (tiles_m * tiles_n > (1ll << 31) - 1 || static_cast<int64_t>(BM) * kp >= (1ll << 31) ||
       mp * kp / 32 >= (1ll << 31) || np * kp / 32 >= (1ll << 31))
     return set_error(kUnsupported, "vdn_mxfp8_gemm: problem too large for 32-bit tile offsets");
   const int group_m = 8;
   hipLaunchKernelGGL((mxfp8_gemm_kernel<BM, BN, WGM, WGN>), dim3(tiles_m * tiles_n),
-                     dim3(WGM * WGN * 64), 0, stream, a, as, w, ws, mp, np, kp, bias, out,
-                     out_rows, n, ldc, mode, nonfinite, static_cast<int>(tiles_m),
+                     dim3(WGM * WGN * 64), 0, stream, a, as, w, ws, mp, np, kp, ep, out_rows, n,
+                     static_cast<int>(tiles_m),
                      static_cast<int>(tiles_n), group_m);
   return check_launch("vdn_mxfp8_gemm");
 }
@@ -243,23 +260,26 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 using namespace vdn;
 
 // Reference: src/models/ops/mxfp8_linear.py:61-93 (MXFP8Linear.forward_quantized: scaled_mm
-// BlockWise1x32 + SWIZZLE_32_4_4, crop to [rows, N], + bias in bf16).
-// mode 0 stores, mode 1 adds into the existing bf16 output (out += y, one bf16 rounding per
-// op), as in `out[video] += to_out_linear(...)` (hybrid_attention.py:254). `nonfinite`
-// (nullable) receives 1 when any stored output is not finite (mxfp8_linear.py:91-92).
+// BlockWise1x32 + SWIZZLE_32_4_4, crop to [rows, N], + bias in bf16), with the block's
+// following bf16 steps optionally fused into the epilogue: `addend` for
+// `out[video] += to_out_linear(...)` (hybrid_attention.py:254) and `residual`/`gate` for the
+// gated residual `hidden + gate * branch` (fused_block.py:49-51). `nonfinite` (nullable)
+// receives 1 when any stored output is not finite (mxfp8_linear.py:91-92).
 VDN_API int vdn_mxfp8_gemm(const void* a, const void* a_scales, int64_t mp, const void* w,
                            const void* w_scales, int64_t np, int64_t kp, const void* bias,
-                           void* out, int64_t out_rows, int64_t n, int64_t ldc, int mode,
-                           uint32_t* nonfinite, void* stream) {
+                           const void* addend, int64_t ld_add, const void* residual,
+                           int64_t ld_res, const void* gate, void* out, int64_t out_rows,
+                           int64_t n, int64_t ldc, uint32_t* nonfinite, void* stream) {
   const char* name = "vdn_mxfp8_gemm";
   if (a == nullptr || a_scales == nullptr || w == nullptr || w_scales == nullptr || out == nullptr)
     return set_error(kInvalidArgument, "%s: null pointer argument", name);
   if (mp <= 0 || np <= 0 || kp <= 0 || mp % 128 || np % 128 || kp % 128)
     return set_error(kInvalidArgument, "%s: padded M/N/K must be positive multiples of 128", name);
-  if (n <= 0 || n > np || out_rows < 0 || out_rows > mp || ldc < n)
+  if (n <= 0 || n > np || out_rows < 0 || out_rows > mp || ldc < n ||
+      (addend != nullptr && ld_add < n) || (residual != nullptr && ld_res < n))
     return set_error(kInvalidArgument, "%s: invalid output geometry", name);
-  if (mode != kStore && mode != kAccumulate)
-    return set_error(kInvalidArgument, "%s: unknown mode %d", name, mode);
+  if (gate != nullptr && residual == nullptr)
+    return set_error(kInvalidArgument, "%s: a gate needs a residual", name);
   if (!aligned(a, 16) || !aligned(w, 16) || !aligned(a_scales, 4) || !aligned(w_scales, 4))
     return set_error(kInvalidArgument, "%s: code buffers need 16-byte, scales 4-byte alignment",
                      name);
@@ -269,11 +289,11 @@ VDN_API int vdn_mxfp8_gemm(const void* a, const void* a_scales, int64_t mp, cons
   auto* asp = static_cast<const uint8_t*>(a_scales);
   auto* wp = static_cast<const uint8_t*>(w);
   auto* wsp = static_cast<const uint8_t*>(w_scales);
-  auto* bp = static_cast<const uint16_t*>(bias);
-  auto* op = static_cast<uint16_t*>(out);
+  const Epilogue ep{static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(addend),
+                    ld_add, static_cast<const uint16_t*>(residual), ld_res,
+                    static_cast<const uint16_t*>(gate), static_cast<uint16_t*>(out), ldc,
+                    nonfinite};
   if (mp >= 1024 && np >= 1024)
-    return launch_gemm<256, 256, 2, 2>(ap, asp, mp, wp, wsp, np, kp, bp, op, out_rows, n, ldc,
-                                       mode, nonfinite, st);
-  return launch_gemm<128, 128, 2, 2>(ap, asp, mp, wp, wsp, np, kp, bp, op, out_rows, n, ldc, mode,
-                                     nonfinite, st);
+    return launch_gemm<256, 256, 2, 2>(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
+  return launch_gemm<128, 128, 2, 2>(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
 }

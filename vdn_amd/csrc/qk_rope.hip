@@ -99,6 +99,8 @@ using namespace vdn;
 // q, k: bf16 [tokens, heads, D] with arbitrary element strides; weights [D] (stride w_s,
 // bf16 or fp32 per flags bit0 for q / bit1 for k); cos/sin (nullable: norm only): [tokens, R]
 // with strides, fp32 when flags bit2 else bf16; qo, ko: contiguous bf16 [tokens, heads, D].
+// flags bit3: q only (k, k_w and ko may be null), for a lone RMSNorm'd operand such as the
+// queries of a cross-attention whose keys have another row count.
 VDN_API int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64_t q_sd,
                                 const void* k, int64_t k_st, int64_t k_sh, int64_t k_sd,
                                 const void* q_w, int64_t q_ws, const void* k_w, int64_t k_ws,
@@ -107,8 +109,9 @@ VDN_API int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64
                                 int flags, int64_t tokens, int heads, int head_dim, void* qo,
                                 void* ko, void* stream) {
   const char* name = "vdn_qk_rmsnorm_rope";
-  if (q == nullptr || k == nullptr || q_w == nullptr || k_w == nullptr || qo == nullptr ||
-      ko == nullptr)
+  const bool q_only = (flags >> 3) & 1;
+  if (q == nullptr || q_w == nullptr || qo == nullptr ||
+      (!q_only && (k == nullptr || k_w == nullptr || ko == nullptr)))
     return set_error(kInvalidArgument, "%s: null pointer", name);
   if (heads <= 0 || tokens < 0 || (head_dim != 64 && head_dim != 128 && head_dim != 256))
     return set_error(kInvalidArgument, "%s: heads > 0 and D in {64, 128, 256} required", name);
@@ -126,7 +129,8 @@ VDN_API int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64
   const int tf = (flags >> 2) & 1;
 #define VDN_ROPE(D)                                                                             \
   hipLaunchKernelGGL(qk_rope_kernel<D>, dim3(static_cast<unsigned>((rows + 256 / (D / 8) - 1) /  \
-                                                                    (256 / (D / 8))), 2),       \
+                                                                    (256 / (D / 8))),           \
+                          q_only ? 1 : 2),                                                      \
                      dim3(256), 0, st, qa, ka, tokens, heads, eps, cos_t, sin_t, c_st, c_sd,    \
                      s_st, s_sd, tf, r);
   if (head_dim == 64) {

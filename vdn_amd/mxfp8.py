@@ -234,11 +234,22 @@ def launch_prenorm_quantize(x, weight, eps, scale, shift, indices, *, write_bf16
 # block-scaled GEMM (mxfp8_linear.py:36-142)
 # --------------------------------------------------------------------------------------
 
-def mxfp8_gemm(data, scales, weight_data, weight_scale, n, *, rows=None, bias=None, out=None,
-               accumulate=False, check_finite=False):
-    """y[rows, n] = dequant(data) @ dequant(weight_data).T, bf16, optional + bias.
+def _matrix_arg(t, rows, n, name):
+    if t is None:
+        return None, 0
+    if (t.dtype != torch.bfloat16 or t.ndim != 2 or t.shape[0] < rows or t.shape[1] != n
+            or (t.shape[1] > 1 and t.stride(-1) != 1)):
+        raise ValueError(f"{name} must be bf16 [rows, N] with contiguous N")
+    return t.data_ptr(), (t.stride(0) if rows > 1 else n)
 
-    With `out` and accumulate=True the result is added into `out` (one bf16 rounding).
+
+def mxfp8_gemm(data, scales, weight_data, weight_scale, n, *, rows=None, bias=None, out=None,
+               accumulate=False, addend=None, residual=None, gate=None, check_finite=False):
+    """y[rows, n] = dequant(data) @ dequant(weight_data).T in bf16, then (each step rounded
+    to bf16) + bias, addend + y, residual + gate * y.
+
+    accumulate=True adds into `out` (addend = out), as `out += linear(x)`; `residual` /
+    `gate` ([n]) fuse the block's gated residual `hidden + gate * branch`.
     """
     mp, kp = data.shape
     np_, kpw = weight_data.shape
@@ -247,14 +258,27 @@ def mxfp8_gemm(data, scales, weight_data, weight_scale, n, *, rows=None, bias=No
     rows = mp if rows is None else rows
     if out is None:
         out = torch.empty((rows, n), dtype=torch.bfloat16, device=data.device)
-    elif out.shape != (rows, n) or out.dtype != torch.bfloat16 or out.stride(-1) != 1:
+    elif out.shape != (rows, n) or out.dtype != torch.bfloat16 or (n > 1 and out.stride(-1) != 1):
         raise ValueError("out must be bf16 [rows, N] with contiguous N")
+    if accumulate:
+        if addend is not None:
+            raise ValueError("accumulate and addend are exclusive")
+        addend = out
+    if gate is not None:
+        if residual is None:
+            raise ValueError("a gate needs a residual")
+        gate = gate.reshape(-1)
+        if gate.shape != (n,) or gate.dtype != torch.bfloat16:
+            raise ValueError("gate must be bf16 [N]")
+        gate = gate.contiguous()
+    add_ptr, ld_add = _matrix_arg(addend, rows, n, "addend")
+    res_ptr, ld_res = _matrix_arg(residual, rows, n, "residual")
     flag = torch.zeros(1, dtype=torch.int32, device=data.device) if check_finite else None
     if rows:
         _lib.call("vdn_mxfp8_gemm", data.data_ptr(), scales.data_ptr(), mp,
                   weight_data.data_ptr(), weight_scale.data_ptr(), np_, kp, _lib.ptr(bias),
-                  out.data_ptr(), rows, n, out.stride(0) if rows > 1 else n,
-                  1 if accumulate else 0, _lib.ptr(flag), _lib.stream(data.device))
+                  add_ptr, ld_add, res_ptr, ld_res, _lib.ptr(gate), out.data_ptr(), rows, n,
+                  out.stride(0) if rows > 1 else n, _lib.ptr(flag), _lib.stream(data.device))
     if check_finite and int(flag.item()) != 0:
         raise ValueError("nonfinite MXFP8 result")
     return out
@@ -291,7 +315,7 @@ class MXFP8Linear(nn.Module):
 
     @torch.no_grad()
     def forward_quantized(self, data, scales, *, rows=None, out_dtype=torch.bfloat16, out=None,
-                          accumulate=False):
+                          accumulate=False, addend=None, residual=None, gate=None):
         """Consume padded uint8 codes and swizzled scales, return cropped bf16 [rows, N]."""
         if self.training or out_dtype != torch.bfloat16:
             raise ValueError("MXFP8 supports eval BF16 output only")
@@ -319,8 +343,8 @@ class MXFP8Linear(nn.Module):
         if self.bias is not None:
             bias = self.bias.to(device=data.device, dtype=torch.bfloat16).contiguous()
         return mxfp8_gemm(data, scales, self.weight_data, self.weight_scale, self.out_features,
-                          rows=rows, bias=bias, out=out, accumulate=accumulate,
-                          check_finite=self.check_finite)
+                          rows=rows, bias=bias, out=out, accumulate=accumulate, addend=addend,
+                          residual=residual, gate=gate, check_finite=self.check_finite)
 
     @torch.no_grad()
     def forward(self, x):

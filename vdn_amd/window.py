@@ -393,6 +393,29 @@ def paper_qk_rmsnorm_rope(q, k, q_weight, k_weight, eps=1e-6, cos=None, sin=None
     return qo, ko
 
 
+def qk_rmsnorm(x, weight, eps=1e-6):
+    """RMSNorm of one [T, H, D] bf16 operand per (token, head) row, n = bf16((x * rsqrt(mean
+    x^2 + eps)) * w): the QK norm of paper_qk_rope.py:82-95 without rotary, for operands whose
+    row count differs from their partner's (cross-attention queries vs context keys)."""
+    if torch.is_grad_enabled():
+        raise RuntimeError("qk_rmsnorm is inference-only; use torch.no_grad()")
+    if (x.ndim != 3 or x.dtype != torch.bfloat16 or not x.is_cuda or x.shape[2] not in (64, 128, 256)
+            or weight.shape != (x.shape[2],) or weight.dtype not in (torch.bfloat16, torch.float32)
+            or weight.device != x.device):
+        raise ValueError("expected CUDA bf16 [T, H, D] and a [D] bf16/fp32 weight on its device")
+    if not math.isfinite(eps) or eps <= 0:
+        raise ValueError("eps must be finite and positive")
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    t, h, d = x.shape
+    if t == 0:
+        return out
+    flags = int(weight.dtype == torch.float32) | 8
+    _lib.call("vdn_qk_rmsnorm_rope", x.data_ptr(), *x.stride(), None, 0, 0, 0, weight.data_ptr(),
+              weight.stride(0), None, 0, float(eps), None, 0, 0, None, 0, 0, 0, flags, t, h, d,
+              out.data_ptr(), None, _lib.stream(x.device))
+    return out
+
+
 def rope_tables_3d(frames, height, width, *, dims=(44, 42, 42), theta=10000.0, device="cpu",
                    dtype=torch.float32):
     """Full-width rotate-half cos/sin tables [F*H*W, sum(dims)] for 3D positions (t, h, w).
