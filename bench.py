@@ -123,15 +123,39 @@ def cpu_baseline(cfg, weights, hidden, temb, ctx, cos, sin, frames_total, sample
                         f"to {frames_total} frames"))
 
 
+def summarize_counters(path):
+    """Mean per dispatch of each counter per kernel from a rocprofv3 counter_collection.csv
+    (one row per dispatch and counter), printed as text, largest first."""
+    import csv
+    sums, dispatches = {}, {}
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            key = (row["Kernel_Name"], row["Counter_Name"])
+            sums[key] = sums.get(key, 0.0) + float(row["Counter_Value"])
+            dispatches.setdefault(key, set()).add(row["Dispatch_Id"])
+    rows = sorted(((k, v / len(dispatches[k]), len(dispatches[k])) for k, v in sums.items()),
+                  key=lambda r: -r[1])
+    for (kernel, counter), mean, n in rows:
+        print(f"{counter}\t{mean:.1f}\t{n}\t{kernel[:150]}")
+
+
 def main():
     p = argparse.ArgumentParser()
+    p.add_argument("--summarize-counters", metavar="CSV",
+                   help="print per-kernel mean counters of a rocprofv3 --pmc CSV and exit")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="after the timed steps, copy one 1 GiB buffer (a known-size copy kernel "
+                        "for scaling HBM byte counters)")
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=5)
     p.add_argument("--warmup", type=int, default=2)
     p.add_argument("--frames", type=int, default=30)
-    p.add_argument("--cpu-sample-frames", type=int, default=3)
+    p.add_argument("--cpu-sample-frames", type=int, default=6)
     p.add_argument("--no-cpu-baseline", action="store_true")
     args = p.parse_args()
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the block runs whole on a single MI355X "
               "(no sharding in this build); run with --gpus 1", file=sys.stderr)
@@ -179,6 +203,13 @@ def main():
         torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
     log(f"timed {args.steps} steps: {ms:.2f} ms per block")
+    if args.calibrate_copy:
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copied 1 GiB (calibration kernel)")
+        del src, dst
 
     per = {}
     for name, a, t in timer.durations():
