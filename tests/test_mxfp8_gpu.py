@@ -103,7 +103,9 @@ def test_quantize_rejects_nonfinite(device):
 
 @pytest.mark.parametrize("rows,k,weight_f32,tables_f32", [(300, 5120, False, False),
                                                            (37, 256, True, True),
-                                                           (5, 1000, False, True)])
+                                                           (5, 1000, False, True),
+                                                           (64, 6144, False, False),
+                                                           (9, 1001, True, False)])
 def test_prenorm_quantize(device, rows, k, weight_f32, tables_f32):
     g = torch.Generator().manual_seed(rows)
     x = torch.randn(rows, k, generator=g).to(torch.bfloat16) * 2

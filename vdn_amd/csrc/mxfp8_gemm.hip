@@ -61,7 +61,28 @@ struct Epilogue {
   uint16_t* out;
   int64_t ldc;
   uint32_t* nonfinite;
+  int vec;  // 16-byte accesses: n, every leading dimension and pointer 8-element aligned
 };
+
+// Epilogue arithmetic of one element (see Epilogue).
+__device__ __forceinline__ float epilogue_value(float y, float b, float addend, float res, float gt,
+                                                const Epilogue& ep) {
+  if (ep.bias != nullptr) y = round_bf16(y + b);
+  if (ep.addend != nullptr) y = round_bf16(addend + y);
+  if (ep.residual != nullptr) {
+    const float t = ep.gate != nullptr ? round_bf16(gt * y) : y;
+    y = round_bf16(res + t);
+  }
+  return y;
+}
+
+__device__ __forceinline__ void unpack8(const u32x4 w, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffff));
+    f[2 * i + 1] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
+  }
+}
 
 template <int BM, int BN, int WGM, int WGN>
 __global__ void __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -75,7 +96,14 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
   constexpr int kASegs = BM / 8 / kWaves;  // 1 KB (8-row) segments per wave per K step
   constexpr int kBSegs = BN / 8 / kWaves;
   static_assert(kASegs * kWaves * 8 == BM && kBSegs * kWaves * 8 == BN, "tile/wave mismatch");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2][(BM + BN) * kBK];
+  // Two K-step buffers for the main loop; after it the same memory stages the bf16 tile
+  // (row stride BN * 2 + 32 bytes: the 16-row x 32-byte writes of one instruction then
+  // touch every bank exactly twice).
+  constexpr int kStepBytes = (BM + BN) * kBK;
+  constexpr int kStageStride = BN * 2 + 32;
+  constexpr int kLdsBytes = 2 * kStepBytes > BM * kStageStride ? 2 * kStepBytes : BM * kStageStride;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[kLdsBytes];
+  uint8_t (*lds)[kStepBytes] = reinterpret_cast<uint8_t (*)[kStepBytes]>(lds_raw);
 
   // ---- tile selection: XCD-contiguous ids, then GROUP_M-row grouping ----
   const int num_wg = tiles_m * tiles_n;
@@ -152,18 +180,26 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
     for (int nt = 0; nt < TN; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   issue_loads(0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
 
+  // Step ks: wait for tile ks (issued one step earlier) and for every wave to have finished
+  // reading the other buffer, then prefetch tile ks + 1 into it and run the MFMAs of tile ks.
+  // The wait sits at the top of the step so the MFMAs are the last instructions of the
+  // loop body: nothing can sink them below the wait, and the prefetch overlaps them.
   const int c_lo = lane >> 4;  // 16-byte chunks g and g + 4 of the 128-byte K step
+  uint32_t sa_next[TM], sb_next[TN];
   for (int ks = 0; ks < nk; ++ks) {
     const int buf = ks & 1;
-    const bool more = ks + 1 < nk;
-    // Scale words for the next step are issued before the tile prefetch and consumed only
-    // after the closing vmcnt(0): waiting on them earlier would also wait on the prefetch,
-    // since vector-memory counters retire in order.
-    uint32_t sa_next[TM], sb_next[TN];
-    if (more) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (ks > 0) {
+#pragma unroll
+      for (int mt = 0; mt < TM; ++mt) sa[mt] = sa_next[mt] >> block_shift;
+#pragma unroll
+      for (int nt = 0; nt < TN; ++nt) sb[nt] = sb_next[nt] >> block_shift;
+    }
+    if (ks + 1 < nk) {
+      // the next step's scale words ride with the tile prefetch and are consumed after
+      // the next top-of-step wait
       const uint8_t* as_step = As + static_cast<int64_t>(ks + 1) * 512;
       const uint8_t* ws_step = Ws + static_cast<int64_t>(ks + 1) * 512;
 #pragma unroll
@@ -174,62 +210,101 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
     }
     const uint8_t* abuf = lds[buf];
     const uint8_t* bbuf = lds[buf] + BM * kBK;
+    auto frag = [&](const uint8_t* base, int row) {
+      const int sw = (row >> 1) & 7;
+      const i32x4 lo = *reinterpret_cast<const i32x4*>(base + row * kBK + ((c_lo ^ sw) << 4));
+      const i32x4 hi = *reinterpret_cast<const i32x4*>(base + row * kBK + (((c_lo + 4) ^ sw) << 4));
+      return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
     i32x8 afrag[TM];
 #pragma unroll
-    for (int mt = 0; mt < TM; ++mt) {
-      const int row = wm * WM + mt * 16 + frag_row;
-      const int sw = (row >> 1) & 7;
-      const i32x4 lo = *reinterpret_cast<const i32x4*>(abuf + row * kBK + ((c_lo ^ sw) << 4));
-      const i32x4 hi = *reinterpret_cast<const i32x4*>(abuf + row * kBK + (((c_lo + 4) ^ sw) << 4));
-      afrag[mt] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    }
+    for (int mt = 0; mt < TM; ++mt) afrag[mt] = frag(abuf, wm * WM + mt * 16 + frag_row);
+    // B fragments are double-buffered in registers: the next one is read while the MFMAs
+    // of the current one run.
+    i32x8 bcur = frag(bbuf, wn * WN + frag_row);
 #pragma unroll
     for (int nt = 0; nt < TN; ++nt) {
-      const int row = wn * WN + nt * 16 + frag_row;
-      const int sw = (row >> 1) & 7;
-      const i32x4 lo = *reinterpret_cast<const i32x4*>(bbuf + row * kBK + ((c_lo ^ sw) << 4));
-      const i32x4 hi = *reinterpret_cast<const i32x4*>(bbuf + row * kBK + (((c_lo + 4) ^ sw) << 4));
-      const i32x8 bfrag = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      i32x8 bnext = bcur;
+      if (nt + 1 < TN) bnext = frag(bbuf, wn * WN + (nt + 1) * 16 + frag_row);
 #pragma unroll
       for (int mt = 0; mt < TM; ++mt) {
+        // D = W_frag . A_frag^T: lane l then holds output columns 4(l/16)..+3 of row l%16
         acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            afrag[mt], bfrag, acc[mt][nt], 0, 0, 0, static_cast<int>(sa[mt]), 0,
-            static_cast<int>(sb[nt]));
+            bcur, afrag[mt], acc[mt][nt], 0, 0, 0, static_cast<int>(sb[nt]), 0,
+            static_cast<int>(sa[mt]));
       }
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (more) {
-#pragma unroll
-      for (int mt = 0; mt < TM; ++mt) sa[mt] = sa_next[mt] >> block_shift;
-#pragma unroll
-      for (int nt = 0; nt < TN; ++nt) sb[nt] = sb_next[nt] >> block_shift;
+      bcur = bnext;
     }
   }
 
-  // ---- epilogue: lane holds rows (lane/16)*4 + v of each 16x16 tile, column lane%16 ----
+  // ---- epilogue 1: bf16(acc) staged row-major in LDS ----
+  // Lane l holds, for each (mt, nt), tile row wm*WM + mt*16 + l%16 and the four
+  // consecutive columns wn*WN + nt*16 + 4(l/16) .. +3.
+  __syncthreads();  // every wave is done reading the K-step buffers
+#pragma unroll
+  for (int mt = 0; mt < TM; ++mt) {
+    const int row = wm * WM + mt * 16 + frag_row;
+#pragma unroll
+    for (int nt = 0; nt < TN; ++nt) {
+      const int col = wn * WN + nt * 16 + 4 * (lane >> 4);
+      u32x2 packed;
+      packed[0] = pack_bf16x2(round_bf16(acc[mt][nt][0]), round_bf16(acc[mt][nt][1]));
+      packed[1] = pack_bf16x2(round_bf16(acc[mt][nt][2]), round_bf16(acc[mt][nt][3]));
+      *reinterpret_cast<u32x2*>(lds_raw + row * kStageStride + col * 2) = packed;
+    }
+  }
+  __syncthreads();
+
+  // ---- epilogue 2: each lane finishes 8 consecutive outputs of a row per pass ----
+  constexpr int kThreads = kWaves * 64;
+  constexpr int kChunksPerRow = BN / 8;
+  constexpr int kRowsPerPass = kThreads / kChunksPerRow;
+  static_assert(kThreads % kChunksPerRow == 0 && BM % kRowsPerPass == 0, "epilogue mapping");
+  const int chunk = tid % kChunksPerRow;
+  const int64_t col = n0 + chunk * 8;
   bool bad = false;
+  float bias8[8], gate8[8];
+  if (ep.vec && col + 8 <= n) {
+    if (ep.bias != nullptr) unpack8(*reinterpret_cast<const u32x4*>(ep.bias + col), bias8);
+    if (ep.gate != nullptr) unpack8(*reinterpret_cast<const u32x4*>(ep.gate + col), gate8);
+  } else {
 #pragma unroll
-  for (int nt = 0; nt < TN; ++nt) {
-    const int64_t col = n0 + wn * WN + nt * 16 + frag_row;
-    if (col >= n) continue;
-    const float b = ep.bias != nullptr ? bf16_bits_to_f32(ep.bias[col]) : 0.f;
-    const float gt = ep.gate != nullptr ? bf16_bits_to_f32(ep.gate[col]) : 1.f;
+    for (int e = 0; e < 8; ++e) {
+      const bool in = col + e < n;
+      bias8[e] = ep.bias != nullptr && in ? bf16_bits_to_f32(ep.bias[col + e]) : 0.f;
+      gate8[e] = ep.gate != nullptr && in ? bf16_bits_to_f32(ep.gate[col + e]) : 1.f;
+    }
+  }
+  for (int pass = 0; pass < BM / kRowsPerPass; ++pass) {
+    const int r = pass * kRowsPerPass + tid / kChunksPerRow;
+    const int64_t row = m0 + r;
+    if (row >= out_rows || col >= n) continue;
+    float y[8], add[8], res[8];
+    unpack8(*reinterpret_cast<const u32x4*>(lds_raw + r * kStageStride + chunk * 16), y);
+    if (ep.vec && col + 8 <= n) {
+      if (ep.addend != nullptr)
+        unpack8(*reinterpret_cast<const u32x4*>(ep.addend + row * ep.ld_add + col), add);
+      if (ep.residual != nullptr)
+        unpack8(*reinterpret_cast<const u32x4*>(ep.residual + row * ep.ld_res + col), res);
+      u32x4 packed;
 #pragma unroll
-    for (int mt = 0; mt < TM; ++mt) {
+      for (int e = 0; e < 8; e += 2) {
+        const float y0 = epilogue_value(y[e], bias8[e], add[e], res[e], gate8[e], ep);
+        const float y1 = epilogue_value(y[e + 1], bias8[e + 1], add[e + 1], res[e + 1],
+                                        gate8[e + 1], ep);
+        bad = bad || !(fabsf(y0) < INFINITY) || !(fabsf(y1) < INFINITY);
+        packed[e / 2] = pack_bf16x2(y0, y1);
+      }
+      *reinterpret_cast<u32x4*>(ep.out + row * ep.ldc + col) = packed;
+    } else {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int64_t row = m0 + wm * WM + mt * 16 + (lane >> 4) * 4 + v;
-        if (row >= out_rows) continue;
-        float y = round_bf16(acc[mt][nt][v]);
-        if (ep.bias != nullptr) y = round_bf16(y + b);
-        if (ep.addend != nullptr) y = round_bf16(bf16_bits_to_f32(ep.addend[row * ep.ld_add + col]) + y);
-        if (ep.residual != nullptr) {
-          const float t = ep.gate != nullptr ? round_bf16(gt * y) : y;
-          y = round_bf16(bf16_bits_to_f32(ep.residual[row * ep.ld_res + col]) + t);
-        }
-        bad = bad || !(fabsf(y) < INFINITY);
-        ep.out[row * ep.ldc + col] = f32_to_bf16_bits(y);
+      for (int e = 0; e < 8; ++e) {
+        if (col + e >= n) continue;
+        const float a = ep.addend != nullptr ? bf16_bits_to_f32(ep.addend[row * ep.ld_add + col + e]) : 0.f;
+        const float rs = ep.residual != nullptr ? bf16_bits_to_f32(ep.residual[row * ep.ld_res + col + e]) : 0.f;
+        const float v = epilogue_value(y[e], bias8[e], a, rs, gate8[e], ep);
+        bad = bad || !(fabsf(v) < INFINITY);
+        ep.out[row * ep.ldc + col + e] = f32_to_bf16_bits(v);
       }
     }
   }
@@ -289,10 +364,14 @@ VDN_API int vdn_mxfp8_gemm(const void* a, const void* a_scales, int64_t mp, cons
   auto* asp = static_cast<const uint8_t*>(a_scales);
   auto* wp = static_cast<const uint8_t*>(w);
   auto* wsp = static_cast<const uint8_t*>(w_scales);
+  const bool vec = n % 8 == 0 && ldc % 8 == 0 && aligned(out, 16) &&
+                   (bias == nullptr || aligned(bias, 16)) && (gate == nullptr || aligned(gate, 16)) &&
+                   (addend == nullptr || (ld_add % 8 == 0 && aligned(addend, 16))) &&
+                   (residual == nullptr || (ld_res % 8 == 0 && aligned(residual, 16)));
   const Epilogue ep{static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(addend),
                     ld_add, static_cast<const uint16_t*>(residual), ld_res,
                     static_cast<const uint16_t*>(gate), static_cast<uint16_t*>(out), ldc,
-                    nonfinite};
+                    nonfinite, vec ? 1 : 0};
   if (mp >= 1024 && np >= 1024)
     return launch_gemm<256, 256, 2, 2>(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
   return launch_gemm<128, 128, 2, 2>(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);

@@ -152,6 +152,96 @@ mxfp8_quantize_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t k, i
 // One workgroup per padded row. The row stays in registers: slice j of thread t is
 // columns [8(t + 256 j), +8), so 4 consecutive lanes share a 32-block and 16 share a
 // 128-column chunk, exactly as in the plain quantizer.
+// Loads 8 consecutive table values (bf16 or fp32) at element offset `off` as floats.
+__device__ __forceinline__ void load_table8(const void* __restrict__ t, int f32, int64_t off,
+                                            float* out) {
+  if (f32) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(static_cast<const float*>(t) + off);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(static_cast<const float*>(t) + off + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[i] = a[i];
+      out[4 + i] = b[i];
+    }
+  } else {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(t) + off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffff));
+      out[2 * i + 1] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
+    }
+  }
+}
+
+// One wave per padded row, kS 8-column slices per lane (slice = lane + 64 j), so the row's
+// sum of squares is a wave reduction (no LDS, no barrier) and four rows share a block.
+// Requires the vector path (k % 8 == 0, 16-byte aligned rows) and 16-byte aligned tables
+// with strides that are multiples of 8 elements. Arithmetic and rounding are the same as
+// prenorm_quantize_kernel's.
+template <int kS>
+__global__ void __launch_bounds__(kThreads)
+prenorm_quantize_wave_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t k,
+                             int64_t stride, const void* __restrict__ weight, int weight_f32,
+                             float eps, const void* __restrict__ scale, int64_t scale_stride,
+                             const void* __restrict__ shift, int64_t shift_stride,
+                             int tables_f32, const int64_t* __restrict__ indices,
+                             uint16_t* __restrict__ y, uint8_t* __restrict__ q,
+                             uint8_t* __restrict__ s, uint8_t* __restrict__ finite, int64_t kp,
+                             int64_t rp) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+  if (r >= rp) return;  // whole wave
+  const bool in_row = r < rows;
+  const int64_t slices = kp >> 3;
+  const int64_t table_row = in_row ? indices[r] : 0;
+  float v[kS][8];
+  bool bad = false;
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kS; ++j) {
+    const int64_t sl = lane + 64 * j;
+    load_row8<true>(x, sl < slices ? r : rows, sl * 8, rows, k, stride, v[j], bad);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += v[j][i] * v[j][i];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+  const float ms = ss / static_cast<float>(k) + eps;
+  const float inv_rms = static_cast<float>(1.0 / sqrt(static_cast<double>(ms)));
+#pragma unroll
+  for (int j = 0; j < kS; ++j) {
+    const int64_t sl = lane + 64 * j;
+    if (sl >= slices) break;  // slices beyond KP: none of this lane's later ones exist
+    const int64_t c0 = sl * 8;
+    if (in_row && c0 < k) {
+      float w[8], sc[8], sh[8];
+      load_table8(weight, weight_f32, c0, w);
+      load_table8(scale, tables_f32, table_row * scale_stride + c0, sc);
+      load_table8(shift, tables_f32, table_row * shift_stride + c0, sh);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float t = (v[j][i] * inv_rms) * w[i];
+        const float u = 1.0f + sc[i];
+        v[j][i] = round_bf16(t * u + sh[i]);
+        bad |= !(fabsf(v[j][i]) < INFINITY);
+      }
+      if (y != nullptr) {
+        u32x4 packed;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) packed[i] = pack_bf16x2(v[j][2 * i], v[j][2 * i + 1]);
+        *reinterpret_cast<u32x4*>(y + r * k + c0) = packed;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[j][i] = 0.f;
+    }
+    quantize_store8(v[j], lane & 15, r, sl >> 4, kp, q, s);
+  }
+  const bool any_bad = __ballot(bad) != 0;
+  if (lane == 0) finite[r] = any_bad ? 0 : 1;
+}
+
 template <int kMaxSlices, bool kVec>
 __global__ void __launch_bounds__(kThreads)
 prenorm_quantize_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t k, int64_t stride,
@@ -333,6 +423,27 @@ VDN_API int vdn_mxfp8_prenorm_quantize(const void* x, int64_t rows, int64_t k, i
     hipLaunchKernelGGL((prenorm_quantize_kernel<MS, false>), dim3(rp), dim3(kThreads), 0, st, \
                        xp, rows, k, row_stride, weight, wf, eps, scale, scale_stride, shift,   \
                        shift_stride, tf, indices, yp, qp, sp, finite, kp);
+  const int64_t tab_align = tf ? 4 : 8;
+  const bool wave_ok = vec && aligned16(weight) && aligned16(scale) && aligned16(shift) &&
+                       scale_stride % tab_align == 0 && shift_stride % tab_align == 0;
+  if (wave_ok && slices <= 64 * 10) {
+    const dim3 grid(static_cast<unsigned>((rp + kThreads / 64 - 1) / (kThreads / 64)));
+#define VDN_PRENORM_WAVE(S)                                                                   \
+    hipLaunchKernelGGL((prenorm_quantize_wave_kernel<S>), grid, dim3(kThreads), 0, st, xp, rows, \
+                       k, row_stride, weight, wf, eps, scale, scale_stride, shift,              \
+                       shift_stride, tf, indices, yp, qp, sp, finite, kp, rp);
+    if (slices <= 64 * 2) {
+      VDN_PRENORM_WAVE(2)
+    } else if (slices <= 64 * 4) {
+      VDN_PRENORM_WAVE(4)
+    } else if (slices <= 64 * 8) {
+      VDN_PRENORM_WAVE(8)
+    } else {
+      VDN_PRENORM_WAVE(10)
+    }
+#undef VDN_PRENORM_WAVE
+    return check_launch(name);
+  }
   if (slices <= kThreads * 1) {
     VDN_PRENORM(1)
   } else if (slices <= kThreads * 3) {

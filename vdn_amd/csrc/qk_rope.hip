@@ -24,7 +24,31 @@ struct RopeArgs {
   uint16_t* out;  // contiguous [T, H, D]
 };
 
-template <int kD>
+// Eight consecutive values (bf16 storage or fp32) starting at element `off`, as floats;
+// fp32 values are rounded to bf16 when `round` is set.
+__device__ __forceinline__ void load8(const void* __restrict__ p, int f32, int64_t off, bool round,
+                                      float* out) {
+  if (f32) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + off);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + off + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[i] = round ? round_bf16(a[i]) : a[i];
+      out[4 + i] = round ? round_bf16(b[i]) : b[i];
+    }
+  } else {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p) + off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffff));
+      out[2 * i + 1] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
+    }
+  }
+}
+
+// kVec: unit channel strides, 16-byte aligned rows, weights and table rows, rot % 8 == 0;
+// every load is one (or two, fp32) 16-byte access per lane.
+template <int kD, bool kVec>
 __global__ void __launch_bounds__(256)
 qk_rope_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float eps,
                const void* __restrict__ cos_t, const void* __restrict__ sin_t, int64_t c_st,
@@ -43,8 +67,17 @@ qk_rope_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float eps,
   const int h = live ? static_cast<int>(row % heads) : 0;
   float v[8];
   const uint16_t* src = a.x + t * a.st + h * a.sh + static_cast<int64_t>(sub) * 8 * a.sd;
+  if (kVec) {
+    if (live) {
+      load8(src, 0, 0, false, v);
+    } else {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = live ? bf16_bits_to_f32(src[i * a.sd]) : 0.f;
+      for (int i = 0; i < 8; ++i) v[i] = 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = live ? bf16_bits_to_f32(src[i * a.sd]) : 0.f;
+  }
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
@@ -52,21 +85,38 @@ qk_rope_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float eps,
   for (int off = 1; off < kLanes; off <<= 1) ss += __shfl_xor(ss, off, kLanes);
   const float inv = 1.0f / sqrtf(ss / static_cast<float>(kD) + eps);
   float n[8];
+  float wv[8];
+  if (kVec) {
+    load8(a.w, a.w_f32, sub * 8, false, wv);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = sub * 8 + i;
+      wv[i] = a.w_f32 ? static_cast<const float*>(a.w)[c * a.ws]
+                      : bf16_bits_to_f32(static_cast<const uint16_t*>(a.w)[c * a.ws]);
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int c = sub * 8 + i;
-    const float w = a.w_f32 ? static_cast<const float*>(a.w)[c * a.ws]
-                            : bf16_bits_to_f32(static_cast<const uint16_t*>(a.w)[c * a.ws]);
-    n[i] = round_bf16((v[i] * inv) * w);
+    n[i] = round_bf16((v[i] * inv) * wv[i]);
     line[slot][c] = n[i];
   }
   __syncthreads();
   float o[8];
   const int half = rot / 2;
+  float cvv[8], svv[8];
+  if (kVec && sub * 8 < rot) {
+    load8(cos_t, table_f32, t * c_st + sub * 8, true, cvv);
+    load8(sin_t, table_f32, t * s_st + sub * 8, true, svv);
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int c = sub * 8 + i;
-    if (c < rot) {
+    if (kVec && c < rot) {
+      const float other = c < half ? -line[slot][c + half] : line[slot][c - half];
+      o[i] = round_bf16(round_bf16(n[i] * cvv[i]) + round_bf16(other * svv[i]));
+    } else if (c < rot) {
       const float other = c < half ? -line[slot][c + half] : line[slot][c - half];
       float cv, sv;
       if (table_f32) {
@@ -127,8 +177,18 @@ VDN_API int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64
   auto st = static_cast<hipStream_t>(stream);
   const int r = cos_t == nullptr ? 0 : rot;
   const int tf = (flags >> 2) & 1;
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const int64_t tab_align = tf ? 4 : 8;
+  auto operand_vec = [&](const RopeArgs& o) {
+    return o.sd == 1 && o.st % 8 == 0 && o.sh % 8 == 0 && al16(o.x) && o.ws == 1 && al16(o.w);
+  };
+  const bool vec = operand_vec(qa) && (q_only || operand_vec(ka)) && r % 8 == 0 &&
+                   (r == 0 || (c_sd == 1 && s_sd == 1 && c_st % tab_align == 0 &&
+                               s_st % tab_align == 0 && al16(cos_t) && al16(sin_t)));
 #define VDN_ROPE(D)                                                                             \
-  hipLaunchKernelGGL(qk_rope_kernel<D>, dim3(static_cast<unsigned>((rows + 256 / (D / 8) - 1) /  \
+  if (vec) VDN_ROPE_V(D, true) else VDN_ROPE_V(D, false)
+#define VDN_ROPE_V(D, V)                                                                        \
+  hipLaunchKernelGGL((qk_rope_kernel<D, V>), dim3(static_cast<unsigned>((rows + 256 / (D / 8) - 1) / \
                                                                     (256 / (D / 8))),           \
                           q_only ? 1 : 2),                                                      \
                      dim3(256), 0, st, qa, ka, tokens, heads, eps, cos_t, sin_t, c_st, c_sd,    \
@@ -141,5 +201,6 @@ VDN_API int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64
     VDN_ROPE(256)
   }
 #undef VDN_ROPE
+#undef VDN_ROPE_V
   return check_launch(name);
 }
