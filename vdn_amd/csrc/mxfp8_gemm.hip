@@ -35,16 +35,14 @@ __device__ __forceinline__ void load_to_lds16(const void* src, void* lds_wave_ba
   __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)lds_wave_base, 16, 0, 0);
 }
 
-// Offset of row r's scale dword for K step 0; K step ks adds 512 * ks.
-__device__ __forceinline__ uint32_t scale_row_offset(int64_t r, int64_t col_tiles) {
-  return static_cast<uint32_t>((r >> 7) * col_tiles * 512 + (r & 31) * 16 + ((r & 127) >> 5) * 4);
+__device__ __forceinline__ void load_to_lds4(const void* src, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)lds_wave_base, 4, 0, 0);
 }
 
-// `s_step` is wave-uniform (scale base + 512 * ks); the per-lane part is a 32-bit unsigned
-// offset, which lets the compiler use the SGPR-base + 32-bit VGPR-offset addressing form.
-__device__ __forceinline__ uint32_t scale_word(const uint8_t* __restrict__ s_step, uint32_t row_off) {
-  return *reinterpret_cast<const uint32_t*>(s_step + row_off);
-}
+// SWIZZLE_32_4_4 keeps the scale dwords (4 K-blocks of one 128-K step) of a 128-row block
+// in one contiguous 512-byte run: row r's dword sits at 16 (r % 32) + 4 ((r % 128) / 32)
+// of it. The run of block b for K step ks starts at (b * col_tiles + ks) * 512.
+__device__ __forceinline__ int scale_in_block(int r) { return (r & 31) * 16 + ((r & 127) >> 5) * 4; }
 
 // Epilogue of one output element y (the bf16-rounded accumulator), in this order:
 //   y = bf16(y + bias[c])                    (bias: nullable, [n])
@@ -99,7 +97,10 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
   // Two K-step buffers for the main loop; after it the same memory stages the bf16 tile
   // (row stride BN * 2 + 32 bytes: the 16-row x 32-byte writes of one instruction then
   // touch every bank exactly twice).
-  constexpr int kStepBytes = (BM + BN) * kBK;
+  // step buffer: A tile (BM x 128 B), W tile (BN x 128 B), then the step's scale runs
+  // (BM / 128 A blocks, then BN / 128 W blocks, 512 B each)
+  constexpr int kScaleOff = (BM + BN) * kBK;
+  constexpr int kStepBytes = kScaleOff + (BM + BN) * 4;
   constexpr int kStageStride = BN * 2 + 32;
   constexpr int kLdsBytes = 2 * kStepBytes > BM * kStageStride ? 2 * kStepBytes : BM * kStageStride;
   __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[kLdsBytes];
@@ -141,7 +142,22 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
   const int a_last = static_cast<int>(min<int64_t>(BM, mp - m0)) - 1;
   const int b_last = static_cast<int>(min<int64_t>(BN, np - n0)) - 1;
   const uint32_t kpu = static_cast<uint32_t>(kp);
+  // Scale runs: wave w loads runs w, w + kWaves, ... (two 256-byte dword DMAs each); row
+  // blocks past the padded end are clamped (their rows are never stored).
+  constexpr int kARuns = BM / 128, kRuns = (BM + BN) / 128;
+  const int64_t a_blocks = mp >> 7, w_blocks = np >> 7;
   auto issue_loads = [&](int ks, int buf) {
+#pragma unroll
+    for (int run = wave; run < kRuns; run += kWaves) {
+      const bool is_a = run < kARuns;
+      const int blk = is_a ? run : run - kARuns;
+      const int64_t row_block = is_a ? min<int64_t>((m0 >> 7) + blk, a_blocks - 1)
+                                     : min<int64_t>((n0 >> 7) + blk, w_blocks - 1);
+      const uint8_t* src = (is_a ? As : Ws) + (row_block * col_tiles + ks) * 512 + lane * 4;
+      uint8_t* dst = &lds[buf][kScaleOff + run * 512];
+      load_to_lds4(src, dst);
+      load_to_lds4(src + 256, dst + 256);
+    }
     const uint8_t* a_k = a_tile + static_cast<int64_t>(ks) * kBK;
     const uint8_t* w_k = w_tile + static_cast<int64_t>(ks) * kBK;
 #pragma unroll
@@ -156,22 +172,19 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
     }
   };
 
-  // ---- scale offsets of this lane (32-bit: the host guarantees mp * kp / 32 < 2^31) ----
   const int frag_row = lane & 15;
   const int block_shift = 8 * (lane >> 4);
-  uint32_t a_soff[TM], b_soff[TN];
+  int a_sidx[TM], b_sidx[TN];  // LDS offsets of this lane's scale dwords within a step buffer
 #pragma unroll
-  for (int mt = 0; mt < TM; ++mt)
-    a_soff[mt] = scale_row_offset(min(m0 + wm * WM + mt * 16 + frag_row, mp - 1), col_tiles);
+  for (int mt = 0; mt < TM; ++mt) {
+    const int r = wm * WM + mt * 16 + frag_row;
+    a_sidx[mt] = kScaleOff + (r >> 7) * 512 + scale_in_block(r);
+  }
 #pragma unroll
-  for (int nt = 0; nt < TN; ++nt)
-    b_soff[nt] = scale_row_offset(min(n0 + wn * WN + nt * 16 + frag_row, np - 1), col_tiles);
-
-  uint32_t sa[TM], sb[TN];
-#pragma unroll
-  for (int mt = 0; mt < TM; ++mt) sa[mt] = scale_word(As, a_soff[mt]) >> block_shift;
-#pragma unroll
-  for (int nt = 0; nt < TN; ++nt) sb[nt] = scale_word(Ws, b_soff[nt]) >> block_shift;
+  for (int nt = 0; nt < TN; ++nt) {
+    const int r = wn * WN + nt * 16 + frag_row;
+    b_sidx[nt] = kScaleOff + (kARuns + (r >> 7)) * 512 + scale_in_block(r);
+  }
 
   f32x4 acc[TM][TN];
 #pragma unroll
@@ -186,28 +199,18 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
   // The wait sits at the top of the step so the MFMAs are the last instructions of the
   // loop body: nothing can sink them below the wait, and the prefetch overlaps them.
   const int c_lo = lane >> 4;  // 16-byte chunks g and g + 4 of the 128-byte K step
-  uint32_t sa_next[TM], sb_next[TN];
   for (int ks = 0; ks < nk; ++ks) {
     const int buf = ks & 1;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (ks > 0) {
+    if (ks + 1 < nk) issue_loads(ks + 1, buf ^ 1);
+    uint32_t sa[TM], sb[TN];
 #pragma unroll
-      for (int mt = 0; mt < TM; ++mt) sa[mt] = sa_next[mt] >> block_shift;
+    for (int mt = 0; mt < TM; ++mt)
+      sa[mt] = *reinterpret_cast<const uint32_t*>(&lds[buf][a_sidx[mt]]) >> block_shift;
 #pragma unroll
-      for (int nt = 0; nt < TN; ++nt) sb[nt] = sb_next[nt] >> block_shift;
-    }
-    if (ks + 1 < nk) {
-      // the next step's scale words ride with the tile prefetch and are consumed after
-      // the next top-of-step wait
-      const uint8_t* as_step = As + static_cast<int64_t>(ks + 1) * 512;
-      const uint8_t* ws_step = Ws + static_cast<int64_t>(ks + 1) * 512;
-#pragma unroll
-      for (int mt = 0; mt < TM; ++mt) sa_next[mt] = scale_word(as_step, a_soff[mt]);
-#pragma unroll
-      for (int nt = 0; nt < TN; ++nt) sb_next[nt] = scale_word(ws_step, b_soff[nt]);
-      issue_loads(ks + 1, buf ^ 1);
-    }
+    for (int nt = 0; nt < TN; ++nt)
+      sb[nt] = *reinterpret_cast<const uint32_t*>(&lds[buf][b_sidx[nt]]) >> block_shift;
     const uint8_t* abuf = lds[buf];
     const uint8_t* bbuf = lds[buf] + BM * kBK;
     auto frag = [&](const uint8_t* base, int row) {
