@@ -23,6 +23,8 @@
 //     each XCD's L2 working set to a few A row-panels and W column-panels.
 #include "mxfp8_common.h"
 
+#include <type_traits>
+
 namespace vdn {
 namespace {
 
@@ -146,7 +148,7 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
   // blocks past the padded end are clamped (their rows are never stored).
   constexpr int kARuns = BM / 128, kRuns = (BM + BN) / 128;
   const int64_t a_blocks = mp >> 7, w_blocks = np >> 7;
-  auto issue_loads = [&](int ks, int buf) {
+  auto issue_scale_loads = [&](int ks, int buf) {
 #pragma unroll
     for (int run = wave; run < kRuns; run += kWaves) {
       const bool is_a = run < kARuns;
@@ -158,18 +160,24 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
       load_to_lds4(src, dst);
       load_to_lds4(src + 256, dst + 256);
     }
-    const uint8_t* a_k = a_tile + static_cast<int64_t>(ks) * kBK;
-    const uint8_t* w_k = w_tile + static_cast<int64_t>(ks) * kBK;
-#pragma unroll
-    for (int i = 0; i < kASegs; ++i) {
-      const uint32_t row = min((i * kWaves + wave) * 8 + seg_row, a_last);
-      load_to_lds16(a_k + (row * kpu + logical16), &lds[buf][(i * kWaves + wave) * 1024]);
-    }
-#pragma unroll
-    for (int i = 0; i < kBSegs; ++i) {
+  };
+  // Tile segment `seg` (0 .. kASegs + kBSegs - 1) of K step ks: 8 rows x 128 bytes.
+  auto issue_segment = [&](int ks, int buf, int seg) {
+    if (seg < kASegs) {
+      const uint32_t row = min((seg * kWaves + wave) * 8 + seg_row, a_last);
+      load_to_lds16(a_tile + static_cast<int64_t>(ks) * kBK + (row * kpu + logical16),
+                    &lds[buf][(seg * kWaves + wave) * 1024]);
+    } else {
+      const int i = seg - kASegs;
       const uint32_t row = min((i * kWaves + wave) * 8 + seg_row, b_last);
-      load_to_lds16(w_k + (row * kpu + logical16), &lds[buf][BM * kBK + (i * kWaves + wave) * 1024]);
+      load_to_lds16(w_tile + static_cast<int64_t>(ks) * kBK + (row * kpu + logical16),
+                    &lds[buf][BM * kBK + (i * kWaves + wave) * 1024]);
     }
+  };
+  auto issue_loads = [&](int ks, int buf) {
+    issue_scale_loads(ks, buf);
+#pragma unroll
+    for (int seg = 0; seg < kASegs + kBSegs; ++seg) issue_segment(ks, buf, seg);
   };
 
   const int frag_row = lane & 15;
@@ -199,11 +207,12 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
   // The wait sits at the top of the step so the MFMAs are the last instructions of the
   // loop body: nothing can sink them below the wait, and the prefetch overlaps them.
   const int c_lo = lane >> 4;  // 16-byte chunks g and g + 4 of the 128-byte K step
-  for (int ks = 0; ks < nk; ++ks) {
+  auto step = [&](int ks, auto more_tag) {
+    constexpr bool more = decltype(more_tag)::value;
     const int buf = ks & 1;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (ks + 1 < nk) issue_loads(ks + 1, buf ^ 1);
+    if constexpr (more) issue_scale_loads(ks + 1, buf ^ 1);
     uint32_t sa[TM], sb[TN];
 #pragma unroll
     for (int mt = 0; mt < TM; ++mt)
@@ -219,26 +228,36 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
       const i32x4 hi = *reinterpret_cast<const i32x4*>(base + row * kBK + (((c_lo + 4) ^ sw) << 4));
       return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
-    i32x8 afrag[TM];
+    // All B fragments stay in registers for the step; A fragments are read one ahead, so the
+    // first MFMA waits for two fragments only. The next tile's segments are issued between
+    // the MFMA groups, which spreads their address work over the step.
+    constexpr int kSegs = kASegs + kBSegs;
+    constexpr int kSegsPerGroup = (kSegs + TM - 1) / TM;
+    i32x8 acur = frag(abuf, wm * WM + frag_row);
+    i32x8 bfrag[TN];
 #pragma unroll
-    for (int mt = 0; mt < TM; ++mt) afrag[mt] = frag(abuf, wm * WM + mt * 16 + frag_row);
-    // B fragments are double-buffered in registers: the next one is read while the MFMAs
-    // of the current one run.
-    i32x8 bcur = frag(bbuf, wn * WN + frag_row);
+    for (int nt = 0; nt < TN; ++nt) bfrag[nt] = frag(bbuf, wn * WN + nt * 16 + frag_row);
 #pragma unroll
-    for (int nt = 0; nt < TN; ++nt) {
-      i32x8 bnext = bcur;
-      if (nt + 1 < TN) bnext = frag(bbuf, wn * WN + (nt + 1) * 16 + frag_row);
+    for (int mt = 0; mt < TM; ++mt) {
+      i32x8 anext = acur;
+      if (mt + 1 < TM) anext = frag(abuf, wm * WM + (mt + 1) * 16 + frag_row);
 #pragma unroll
-      for (int mt = 0; mt < TM; ++mt) {
+      for (int nt = 0; nt < TN; ++nt) {
         // D = W_frag . A_frag^T: lane l then holds output columns 4(l/16)..+3 of row l%16
         acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            bcur, afrag[mt], acc[mt][nt], 0, 0, 0, static_cast<int>(sb[nt]), 0,
+            bfrag[nt], acur, acc[mt][nt], 0, 0, 0, static_cast<int>(sb[nt]), 0,
             static_cast<int>(sa[mt]));
       }
-      bcur = bnext;
+      if constexpr (more) {
+#pragma unroll
+        for (int j = 0; j < kSegsPerGroup; ++j)
+          if (mt * kSegsPerGroup + j < kSegs) issue_segment(ks + 1, buf ^ 1, mt * kSegsPerGroup + j);
+      }
+      acur = anext;
     }
-  }
+  };
+  for (int ks = 0; ks + 1 < nk; ++ks) step(ks, std::true_type{});
+  step(nk - 1, std::false_type{});
 
   // ---- epilogue 1: bf16(acc) staged row-major in LDS ----
   // Lane l holds, for each (mt, nt), tile row wm*WM + mt*16 + l%16 and the four
