@@ -297,28 +297,54 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
       gate8[e] = ep.gate != nullptr && in ? bf16_bits_to_f32(ep.gate[col + e]) : 1.f;
     }
   }
-  for (int pass = 0; pass < BM / kRowsPerPass; ++pass) {
-    const int r = pass * kRowsPerPass + tid / kChunksPerRow;
-    const int64_t row = m0 + r;
-    if (row >= out_rows || col >= n) continue;
-    float y[8], add[8], res[8];
-    unpack8(*reinterpret_cast<const u32x4*>(lds_raw + r * kStageStride + chunk * 16), y);
-    if (ep.vec && col + 8 <= n) {
-      if (ep.addend != nullptr)
-        unpack8(*reinterpret_cast<const u32x4*>(ep.addend + row * ep.ld_add + col), add);
-      if (ep.residual != nullptr)
-        unpack8(*reinterpret_cast<const u32x4*>(ep.residual + row * ep.ld_res + col), res);
-      u32x4 packed;
+  constexpr int kPasses = BM / kRowsPerPass;
+  constexpr int kBatch = kPasses < 8 ? kPasses : 8;
+  static_assert(kPasses % kBatch == 0, "epilogue batching");
+  if (ep.vec && col + 8 <= n) {
+    // Batches of kBatch rows: every load of a batch is issued before any arithmetic, so
+    // the addend/residual latency is paid once per batch rather than once per row.
+    for (int b0 = 0; b0 < kPasses; b0 += kBatch) {
+      u32x4 yv[kBatch], av[kBatch], rv[kBatch];
 #pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const float y0 = epilogue_value(y[e], bias8[e], add[e], res[e], gate8[e], ep);
-        const float y1 = epilogue_value(y[e + 1], bias8[e + 1], add[e + 1], res[e + 1],
-                                        gate8[e + 1], ep);
-        bad = bad || !(fabsf(y0) < INFINITY) || !(fabsf(y1) < INFINITY);
-        packed[e / 2] = pack_bf16x2(y0, y1);
+      for (int j = 0; j < kBatch; ++j) {
+        const int r = (b0 + j) * kRowsPerPass + tid / kChunksPerRow;
+        const int64_t row = m0 + r;
+        yv[j] = *reinterpret_cast<const u32x4*>(lds_raw + r * kStageStride + chunk * 16);
+        if (row < out_rows) {
+          if (ep.addend != nullptr)
+            av[j] = *reinterpret_cast<const u32x4*>(ep.addend + row * ep.ld_add + col);
+          if (ep.residual != nullptr)
+            rv[j] = *reinterpret_cast<const u32x4*>(ep.residual + row * ep.ld_res + col);
+        }
       }
-      *reinterpret_cast<u32x4*>(ep.out + row * ep.ldc + col) = packed;
-    } else {
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int r = (b0 + j) * kRowsPerPass + tid / kChunksPerRow;
+        const int64_t row = m0 + r;
+        if (row >= out_rows) continue;
+        float y[8], add[8], res[8];
+        unpack8(yv[j], y);
+        if (ep.addend != nullptr) unpack8(av[j], add);
+        if (ep.residual != nullptr) unpack8(rv[j], res);
+        u32x4 packed;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const float y0 = epilogue_value(y[e], bias8[e], add[e], res[e], gate8[e], ep);
+          const float y1 = epilogue_value(y[e + 1], bias8[e + 1], add[e + 1], res[e + 1],
+                                          gate8[e + 1], ep);
+          bad = bad || !(fabsf(y0) < INFINITY) || !(fabsf(y1) < INFINITY);
+          packed[e / 2] = pack_bf16x2(y0, y1);
+        }
+        *reinterpret_cast<u32x4*>(ep.out + row * ep.ldc + col) = packed;
+      }
+    }
+  } else if (col < n) {
+    for (int pass = 0; pass < kPasses; ++pass) {
+      const int r = pass * kRowsPerPass + tid / kChunksPerRow;
+      const int64_t row = m0 + r;
+      if (row >= out_rows) continue;
+      float y[8];
+      unpack8(*reinterpret_cast<const u32x4*>(lds_raw + r * kStageStride + chunk * 16), y);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         if (col + e >= n) continue;
