@@ -21,6 +21,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace vdn {
 namespace {
 
@@ -55,14 +57,18 @@ struct Layout {
   int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh;  // token / head strides (elements)
 };
 
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restrict__ grp_kv,
                    const int* __restrict__ grp_n, int nblocks, int heads, float scale_log2,
                    const uint16_t* __restrict__ gate, int64_t g_st, int64_t g_sh,
                    uint16_t* __restrict__ out, int64_t o_st, int64_t o_sh,
                    float* __restrict__ lse, int64_t l_st, int64_t l_sh) {
-  __shared__ __attribute__((aligned(1024))) uint16_t sK[2][kBN * kD];
-  __shared__ __attribute__((aligned(1024))) uint16_t sV[2][kBN * kD];
+  // Separate arrays per buffer: with distinct LDS objects the compiler can tell a tile
+  // prefetch into one buffer from reads of the other and does not wait on the prefetch.
+  __shared__ __attribute__((aligned(1024))) uint16_t sK0[kBN * kD];
+  __shared__ __attribute__((aligned(1024))) uint16_t sK1[kBN * kD];
+  __shared__ __attribute__((aligned(1024))) uint16_t sV0[kBN * kD];
+  __shared__ __attribute__((aligned(1024))) uint16_t sV1[kBN * kD];
 
   // ---- work item: (head, query block); consecutive ids of a head land on one XCD ----
   const int total = nblocks * heads;
@@ -95,24 +101,9 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     }
   }
 
-  // ---- tile schedule over the key intervals ----
-  int ntiles = 0;
-  for (int i = 0; i < nint; ++i) ntiles += (kv[2 * i + 1] - kv[2 * i] + kBN - 1) / kBN;
-  auto tile_range = [&](int t, int& a, int& b) {
-    int i = 0;
-    for (; i < nint; ++i) {
-      const int n = (kv[2 * i + 1] - kv[2 * i] + kBN - 1) / kBN;
-      if (t < n) break;
-      t -= n;
-    }
-    a = kv[2 * i] + t * kBN;
-    b = min(a + kBN, kv[2 * i + 1]);
-  };
   // lane's share of a tile load: 4 x 1 KB segments (4 rows each) per tensor per wave
   const int seg_row = lane >> 4, phys = lane & 15;
-  auto issue_tile = [&](int t, int buf) {
-    int a, b;
-    tile_range(t, a, b);
+  auto issue_tile = [&](int a, int b, uint16_t* dk, uint16_t* dv) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int seg = j * 4 + wave;
@@ -120,8 +111,8 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
       const int key = min(a + row, b - 1);
       const uint16_t* ksrc = in.k + static_cast<int64_t>(key) * in.k_st + h * in.k_sh;
       const uint16_t* vsrc = in.v + static_cast<int64_t>(key) * in.v_st + h * in.v_sh;
-      load_to_lds16(ksrc + 8 * (phys ^ swz_k(row)), &sK[buf][seg * 4 * kD]);
-      load_to_lds16(vsrc + 8 * (phys ^ swz_v(row)), &sV[buf][seg * 4 * kD]);
+      load_to_lds16(ksrc + 8 * (phys ^ swz_k(row)), dk + seg * 4 * kD);
+      load_to_lds16(vsrc + 8 * (phys ^ swz_v(row)), dv + seg * 4 * kD);
     }
   };
 
@@ -132,22 +123,29 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
   float m = -INFINITY, l = 0.f;
 
-  if (ntiles > 0) issue_tile(0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-
   // transpose-read coordinates (16-lane group G = lane/16)
   const int G = lane >> 4, L = lane & 15;
   const int tr_row = 4 * (G >> 1) + (L >> 2);
   const int tr_col = 16 * (G & 1) + 4 * (L & 3);
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) issue_tile(t + 1, buf ^ 1);
-    int a, b;
-    tile_range(t, a, b);
-    const uint16_t* tk = sK[buf];
-    const uint16_t* tv = sV[buf];
+  // One key tile: tile t is resident in buffer kBuf (sK0/sV0 or sK1/sV1); the next tile is
+  // prefetched into the other buffer. Running max m is kept in scaled (exp2) units and may
+  // lag the true maximum by up to kLazy: the accumulators are rescaled only when a lane's
+  // maximum grows by more than that, so exp2 arguments stay <= kLazy (p <= 2^kLazy) and
+  // most tiles skip the rescale.
+  constexpr float kLazy = 8.f;
+  auto process = [&](int t, int ntiles, int a0, int b0, auto buf_tag) __attribute__((always_inline)) {
+    constexpr int kBuf = decltype(buf_tag)::value;
+    const uint16_t* tk = kBuf == 0 ? sK0 : sK1;
+    const uint16_t* tv = kBuf == 0 ? sV0 : sV1;
+    // tile t is resident and every wave is done with the other buffer
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t + 1 < ntiles) {
+      const int na = a0 + (t + 1) * kBN;
+      issue_tile(na, min(na + kBN, b0), kBuf == 0 ? sK1 : sK0, kBuf == 0 ? sV1 : sV0);
+    }
+    const int a = a0 + t * kBN, b = min(a + kBN, b0);
 
     // ---- Sᵀ = K Qᵀ for the tile's 64 keys (two 32-key accumulators) ----
     f32x16 s[2];
@@ -163,36 +161,44 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
         s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[ks], s[kt], 0, 0, 0);
       }
     }
-    // ---- online softmax (exp2 domain) ----
+    // ---- online softmax (exp2 domain; scores scaled inside the exponent's fma) ----
+    if (b - a < kBN) {  // tail tile: keys past the interval end do not exist
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = a + kt * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+          if (key >= b) s[kt][v] = -INFINITY;
+        }
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int key = a + kt * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
-        const float x = key < b ? s[kt][v] * scale_log2 : -INFINITY;
-        s[kt][v] = x;
-        mx = fmaxf(mx, x);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx);
-    const float corr = __builtin_amdgcn_exp2f(m - m_new);
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kt][v]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+    const bool grow = mx > m + kLazy;
+    if (__any(grow)) {
+      const float m_new = grow ? mx : m;
+      const float corr = __builtin_amdgcn_exp2f(m - m_new);
+      l *= corr;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[db][v] *= corr;
+      m = m_new;
+    }
     float rs = 0.f;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const float p = __builtin_amdgcn_exp2f(s[kt][v] - m_new);
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][v], scale_log2, -m));
         s[kt][v] = p;
         rs += p;
       }
     rs += __shfl_xor(rs, 32);
-    l = l * corr + rs;
-    m = m_new;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) o[db][v] *= corr;
+    l += rs;
 
     // ---- Oᵀ += Vᵀ Pᵀ, 16 keys per MFMA ----
 #pragma unroll
@@ -219,14 +225,30 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, o[db], 0, 0, 0);
       }
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+  };
+  // ---- key intervals of the group, one after another ----
+  // Each interval is a contiguous key range walked in 64-key tiles; its bounds are read
+  // before its first tile load, so the tile loop itself reads no memory besides the tiles.
+  // The online softmax state carries over from one interval to the next.
+  for (int i = 0; i < nint; ++i) {
+    const int a0 = __builtin_amdgcn_readfirstlane(kv[2 * i]);
+    const int b0 = __builtin_amdgcn_readfirstlane(kv[2 * i + 1]);
+    const int ntiles = (b0 - a0 + kBN - 1) / kBN;
+    if (ntiles <= 0) continue;
+    __syncthreads();  // every wave is done reading the buffers of the previous interval
+    issue_tile(a0, min(a0 + kBN, b0), sK0, sV0);
+    for (int t = 0; t < ntiles; t += 2) {
+      process(t, ntiles, a0, b0, std::integral_constant<int, 0>{});
+      if (t + 1 < ntiles) process(t + 1, ntiles, a0, b0, std::integral_constant<int, 1>{});
+    }
   }
+  __syncthreads();  // the epilogue reuses the K buffers
 
   // ---- epilogue: O / l, optional gate, through LDS to coalesced rows ----
   const float inv_l = l > 0.f ? 1.0f / l : 0.f;
-  uint16_t* sO = sK[0];  // [128 queries][128 channels] bf16 = 32 KB (spans sK[0..1])
+  // [128 queries][128 channels] bf16: queries 0-63 in sK0, 64-127 in sK1 (wave-uniform)
   const int qr = wave * 32 + col;
+  uint16_t* sO = qr < 64 ? sK0 : sK1;
   float gv = 1.f;
   if (gate != nullptr && q_live) gv = bf16_bits_to_f32(gate[static_cast<int64_t>(my_q) * g_st + h * g_sh]);
 #pragma unroll
@@ -236,7 +258,7 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
       const int d = 32 * db + (v >> 2) * 8 + g * 4 + (v & 3);
       float y = round_bf16(o[db][v] * inv_l);
       if (gate != nullptr) y = y * gv;
-      sO[qr * kD + d] = f32_to_bf16_bits(y);
+      sO[(qr & 63) * kD + d] = f32_to_bf16_bits(y);
     }
   if (lse != nullptr && q_live && g == 0)
     lse[static_cast<int64_t>(my_q) * l_st + h * l_sh] = (m + log2f(l)) * kLn2;
@@ -246,8 +268,9 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     const int q = q0 + r;
     if (q >= q1) continue;
     const int c8 = (tid & 15) * 8;
+    const uint16_t* src = r < 64 ? sK0 : sK1;
     *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(q) * o_st + h * o_sh + c8) =
-        *reinterpret_cast<const u32x4*>(&sO[r * kD + c8]);
+        *reinterpret_cast<const u32x4*>(&src[(r & 63) * kD + c8]);
   }
 }
 
