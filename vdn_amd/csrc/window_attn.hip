@@ -101,18 +101,40 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     }
   }
 
-  // lane's share of a tile load: 4 x 1 KB segments (4 rows each) per tensor per wave
+  // lane's share of a tile load: 4 x 1 KB segments (4 rows each) per tensor per wave. The
+  // per-lane byte offsets within a tile are fixed; a tile adds a wave-uniform base, so the
+  // loads take the scalar-base + 32-bit-offset form with no per-tile vector address math.
   const int seg_row = lane >> 4, phys = lane & 15;
-  auto issue_tile = [&](int a, int b, uint16_t* dk, uint16_t* dv) __attribute__((always_inline)) {
+  uint32_t koff[4], voff[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int seg = j * 4 + wave;
-      const int row = seg * 4 + seg_row;
-      const int key = min(a + row, b - 1);
-      const uint16_t* ksrc = in.k + static_cast<int64_t>(key) * in.k_st + h * in.k_sh;
-      const uint16_t* vsrc = in.v + static_cast<int64_t>(key) * in.v_st + h * in.v_sh;
-      load_to_lds16(ksrc + 8 * (phys ^ swz_k(row)), dk + seg * 4 * kD);
-      load_to_lds16(vsrc + 8 * (phys ^ swz_v(row)), dv + seg * 4 * kD);
+  for (int j = 0; j < 4; ++j) {
+    const int row = (j * 4 + wave) * 4 + seg_row;
+    koff[j] = static_cast<uint32_t>(row * in.k_st * 2 + 16 * (phys ^ swz_k(row)));
+    voff[j] = static_cast<uint32_t>(row * in.v_st * 2 + 16 * (phys ^ swz_v(row)));
+  }
+  const char* k_head = reinterpret_cast<const char*>(in.k + h * in.k_sh);
+  const char* v_head = reinterpret_cast<const char*>(in.v + h * in.v_sh);
+  auto issue_tile = [&](int a, int b, uint16_t* dk, uint16_t* dv) __attribute__((always_inline)) {
+    const char* kb = k_head + static_cast<int64_t>(a) * in.k_st * 2;
+    const char* vb = v_head + static_cast<int64_t>(a) * in.v_st * 2;
+    if (b - a == kBN) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int seg = j * 4 + wave;
+        load_to_lds16(kb + koff[j], dk + seg * 4 * kD);
+        load_to_lds16(vb + voff[j], dv + seg * 4 * kD);
+      }
+    } else {  // tail tile: rows past the interval end repeat its last key
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int seg = j * 4 + wave;
+        const int row = seg * 4 + seg_row;
+        const int r = min(row, b - a - 1);
+        const uint32_t ko = static_cast<uint32_t>(r * in.k_st * 2 + 16 * (phys ^ swz_k(row)));
+        const uint32_t vo = static_cast<uint32_t>(r * in.v_st * 2 + 16 * (phys ^ swz_v(row)));
+        load_to_lds16(kb + ko, dk + seg * 4 * kD);
+        load_to_lds16(vb + vo, dv + seg * 4 * kD);
+      }
     }
   };
 
@@ -305,6 +327,8 @@ VDN_API int vdn_window_attention(const void* q, int64_t q_st, int64_t q_sh, cons
       q_sh % 8 || k_st % 8 || k_sh % 8 || v_st % 8 || v_sh % 8 || o_st % 8 || o_sh % 8)
     return set_error(kInvalidArgument, "%s: rows need 16-byte alignment", name);
   if (!(scale > 0.f) || !isfinite(scale)) return set_error(kInvalidArgument, "%s: bad scale", name);
+  if (k_st <= 0 || v_st <= 0 || k_st > (1 << 24) || v_st > (1 << 24))
+    return set_error(kUnsupported, "%s: K/V token strides must be in (0, 2^24] elements", name);
   if (nblocks == 0) return kOk;
   const Layout in{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                   static_cast<const uint16_t*>(v), q_st, q_sh, k_st, k_sh, v_st, v_sh};
