@@ -28,6 +28,7 @@ PEAK_HBM_GBS = 8000.0        # HBM3E, MI355X
 HEIGHT, WIDTH = 45, 80
 D = 128
 
+GEMMS = ("vdn_mxfp8_gemm", "vdn_mxfp8_gemm_act_quantize")
 VDA_ENTRIES = ("vdn_vda_statistics", "vdn_vda_factors", "vdn_vda_compose", "vdn_vda_scan",
                "vdn_vda_log_prefix", "vdn_vda_gather", "vdn_vda_readout")
 
@@ -47,6 +48,10 @@ def work(name, a, plans):
         ops = [a[7], a[8], a[10], a[12]]  # bias, addend, residual, gate
         extra = rows * n * 2 * sum(1 for p in ops[1:3] if p is not None)
         return 2.0 * rows * n * kp, rows * kp + n * kp + (rows + n) * kp / 32 + rows * n * 2 + extra
+    if name == "vdn_mxfp8_gemm_act_quantize":
+        kp, rows, n = a[6], a[11], a[12]
+        kp_out = padded(n)
+        return 2.0 * rows * n * kp, rows * kp + n * kp + (rows + n) * kp / 32 + rows * kp_out * (1 + 1 / 32)
     if name == "vdn_mxfp8_quantize":
         rows, k = a[1], a[2]
         return 0.0, rows * k * 2 + padded(rows) * padded(k) * (1 + 1 / 32)
@@ -223,12 +228,12 @@ def main():
     for name, (count, t, flop, nbytes) in sorted(per.items(), key=lambda kv: -kv[1][1]):
         row = dict(ms_per_step=round(t / args.steps, 3), launches_per_step=count // args.steps,
                    avg_launch_ms=round(t / count, 4))
-        if flop and name in ("vdn_mxfp8_gemm", "vdn_window_attention"):
+        if flop and name in GEMMS + ("vdn_window_attention",):
             row["tflops"] = round(flop / (t * 1e-3) / 1e12, 1)
-        if nbytes and name not in ("vdn_mxfp8_gemm", "vdn_window_attention"):
+        if nbytes and name not in GEMMS + ("vdn_window_attention",):
             row["gbs"] = round(nbytes / (t * 1e-3) / 1e9, 1)
         breakdown[name] = row
-    g = per["vdn_mxfp8_gemm"]
+    g = [sum(per[nm][i] for nm in GEMMS if nm in per) for i in range(4)]
     gemm_tflops = g[2] / (g[1] * 1e-3) / 1e12
     vda_t = sum(per[n][1] for n in VDA_ENTRIES if n in per)
     vda_bytes = sum(per[n][3] for n in VDA_ENTRIES if n in per)
@@ -253,7 +258,8 @@ def main():
                    "tokens": tokens, "hidden": cfg.hidden, "heads": cfg.heads,
                    "head_dim": cfg.head_dim, "ffn": cfg.ffn, "context": ctx.shape[0],
                    "parallelism": "single GPU"},
-        "roofline": {"kernel": "vdn_mxfp8_gemm (all 9 block projections)", "bound": "mfma",
+        "roofline": {"kernel": "mxfp8_gemm_kernel (all block projections: vdn_mxfp8_gemm and "
+                               "the FFN-up vdn_mxfp8_gemm_act_quantize)", "bound": "mfma",
                      "achieved": round(gemm_tflops, 1), "peak": PEAK_MXFP8_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_MXFP8_TFLOPS, 4),
                      "traffic": traffic,

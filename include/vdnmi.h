@@ -79,6 +79,21 @@ int vdn_mxfp8_gemm(const void* a, const void* a_scales, int64_t mp, const void* 
                    const void* gate, void* out, int64_t out_rows, int64_t n, int64_t ldc,
                    uint32_t* nonfinite, void* stream);
 
+/*
+ * Block-scaled GEMM feeding the next MXFP8 projection directly: y = bf16(bf16(acc) + bias),
+ * act = 1 applies GELU-tanh (rounded to bf16; act = 0: none), and y is stored as MXFP8 codes
+ * q [mp, pad128(n)] + swizzled scales (mp * pad128(n) / 32 bytes), exactly what
+ * vdn_mxfp8_act_quantize / vdn_mxfp8_quantize write for that bf16 matrix. Rows >= out_rows
+ * and columns >= n are zero. *nonfinite (nullable) becomes 1 on a nonfinite activation.
+ * Replaces: the FFN up projection + activation producer of tp_ff_forward
+ * (src/inference/utils/tensor_parallel.py:147-161: MXFP8Linear.forward_quantized,
+ * mxfp8_linear.py:61-93, then the producer of mxfp8_kernels.py:62-84, 113-124).
+ */
+int vdn_mxfp8_gemm_act_quantize(const void* a, const void* a_scales, int64_t mp, const void* w,
+                                const void* w_scales, int64_t np, int64_t kp, const void* bias,
+                                int act, void* q, void* scales, int64_t out_rows, int64_t n,
+                                uint32_t* nonfinite, void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * VDA linear-attention branch (D = 128). A 4-D operand "(f, h, s, c)" is addressed as
  * base + f*sf + h*sh + s*ss + c (element strides, channels contiguous); raw token-major
@@ -203,7 +218,7 @@ int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64_t q_sd,
 
 /*
  * Exact softmax attention of query blocks over key intervals (head_dim 128, bf16):
- * blocks int32 [nblocks, 3] = (first query, end of its query range, group), <= 128 queries
+ * blocks int32 [nblocks, 3] = (first query, end of its query range, group), <= 256 queries
  * each; grp_kv int32 [groups, 8, 2] key intervals [a, b); grp_n int32 [groups].
  * q, k, v addressed by (token, head) strides with unit channel stride. gate (nullable): bf16
  * per (token, head) scalar applied as out = bf16(bf16(o) * gate). out: bf16 (token, head)

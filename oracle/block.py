@@ -107,8 +107,9 @@ class BlockOracle:
         self.cfg, self.w = cfg, w
         self.qkv = QuantizedLinear(merge_lora(w["qkv_w"], w["lora_a"], w["lora_b"], cfg.lora_scale),
                                    w["qkv_b"])
-        self.o = QuantizedLinear(w["o_w"], w["o_b"])
-        self.olin = QuantizedLinear(w["olin_w"])
+        # to_out and to_out_linear as one projection of the concatenated branch outputs:
+        # bf16(acc_o + acc_lin) + b_o (one accumulation, then the epilogue's roundings)
+        self.o_cat = QuantizedLinear(torch.cat((w["o_w"], w["olin_w"]), dim=1), w["o_b"])
         self.cq = QuantizedLinear(w["cq_w"], w["cq_b"])
         self.ck = QuantizedLinear(w["ck_w"], w["ck_b"])
         self.cv = QuantizedLinear(w["cv_w"], w["cv_b"])
@@ -149,7 +150,7 @@ class BlockOracle:
     def attention_stage(self, h, tables, frames, height, width, cos, sin, given=None):
         """h + gate_msa * (O(gated window softmax) + O_lin(VDA)); bf16-valued float64.
 
-        `given` (optional) maps x1, qkv, soft, attn, far to another run's values: each piece is
+        `given` (optional) maps x1, qkv, soft, far to another run's values: each piece is
         still computed here, from the given upstream values where present, so a run can be
         checked piece by piece on its own inputs."""
         cfg, w = self.cfg, self.w
@@ -175,13 +176,13 @@ class BlockOracle:
         mask = _win.dense_mask(t, 0, frames, spatial, bounds)
         o, _ = _win.attention_dense(q, k, value, mask, d ** -0.5)
         soft = _win.softmax_gate(o, soft_gate).double()
-        attn = self.o(use("soft", soft))
         far, _ = _vda.paper_branch(raw_q, raw_k, value, beta, lin_gate.reshape(t, heads, d), alpha,
                                    bounds, frames, spatial, w["vda_norm"].double(), cfg.eps,
                                    chunk_size=cfg.vda_chunk)
         far = bf16(far)
-        out = self.olin(use("far", far), addend=use("attn", attn), residual=h, gate=gate)
-        return out, dict(x1=x1, qkv=qkv, soft=soft, far=far, attn=attn, alpha=alpha)
+        both = torch.cat((use("soft", soft), use("far", far)), dim=1)
+        out = self.o_cat(both, residual=h, gate=gate)
+        return out, dict(x1=x1, qkv=qkv, soft=soft, far=far, alpha=alpha)
 
     def cross_stage(self, h, context, given=None):
         """h + O_c(attention(RMSNorm(norm3(h)) W_q, context W_k, context W_v)); `given` may
@@ -205,14 +206,14 @@ class BlockOracle:
 
     def ffn_stage(self, h, tables, given=None):
         """h + gate_mlp * down(GELU_tanh(up(prenorm(h; norm2, scale_mlp, shift_mlp)))); `given`
-        may hold another run's up projection."""
+        may hold another run's activation as dequantized MXFP8 ("act")."""
         w = self.w
         shift, scale, gate = tables[3], tables[4], tables[5]
         x2 = self.prenorm(h, w["norm2"], scale, shift)
         up = self.up(x2)
-        up_in = (given or {}).get("up", up).double()
-        act = torch.from_numpy(_mx.gelu_tanh(up_in.float().numpy())).double()
-        return self.down(act, residual=h, gate=gate), dict(up=up, act=act)
+        act = torch.from_numpy(_mx.gelu_tanh(up.float().numpy())).double()
+        act_in = (given or {}).get("act", act).double()
+        return self.down(act_in, residual=h, gate=gate), dict(up=up, act=act)
 
     def forward(self, h, temb, context, frames, height, width, cos, sin):
         tables = self.tables(temb)

@@ -7,6 +7,7 @@ import pytest
 import torch
 
 from oracle import block as ob
+from oracle import mxfp8 as omx
 from oracle import window as ow
 from vdn_amd import window as vw
 from vdn_amd.block import (BlockConfig, BlockWeights, HybridDiTBlock, cross_attention_plan,
@@ -46,6 +47,20 @@ def run(cfg, frames, height, width, seed):
                 geometry=(frames, height, width))
 
 
+def ffn_activation(codes_scales, rows, n):
+    """Dequantized FFN activation from the fused producer's MXFP8 codes and scales."""
+    codes, flat = (t.numpy() for t in codes_scales)
+    rp, kp = codes.shape
+    natural = omx.unswizzle(flat, rp, kp)
+    return torch.from_numpy(omx.dequant(codes, natural)[:rows, :n])
+
+
+def mxfp8_value(x):
+    """The MXFP8 value (oracle quantizer, dequantized) of a bf16-valued matrix."""
+    codes, natural, _ = omx.quantize(x.float().numpy())
+    return torch.from_numpy(omx.dequant(codes, natural)[:x.shape[0], :x.shape[1]])
+
+
 def check(r):
     cfg, orc, p = r["cfg"], r["oracle"], r["parts"]
     frames, height, width = r["geometry"]
@@ -54,18 +69,19 @@ def check(r):
     for mine, theirs in zip(p["tables"], tables):
         assert rel_l2(mine, theirs) < 4e-3
     gpu_tables = tuple(t.double() for t in p["tables"])
-    given = {k: p[k] for k in ("x1", "qkv", "soft", "attn", "far")}
+    given = {k: p[k] for k in ("x1", "qkv", "soft", "far")}
     h1, own = orc.attention_stage(h0, gpu_tables, frames, height, width, r["cos"], r["sin"],
                                   given=given)
-    errors = {name: rel_l2(p[name], own[name]) for name in ("x1", "qkv", "soft", "attn", "far")}
+    errors = {name: rel_l2(p[name], own[name]) for name in ("x1", "qkv", "soft", "far")}
     errors["h1 delta"] = rel_l2(p["h1"].double() - h0, h1 - h0)
     h1g = p["h1"].double()
     h2, own = orc.cross_stage(h1g, r["ctx"], given={"co": p["co"]})
     errors["co"] = rel_l2(p["co"], own["co"])
     errors["h2 delta"] = rel_l2(p["h2"].double() - h1g, h2 - h1g)
     h2g = p["h2"].double()
-    h3, own = orc.ffn_stage(h2g, gpu_tables, given={"up": p["up"]})
-    errors["up"] = rel_l2(p["up"], own["up"])
+    act = ffn_activation(p["ffn_codes"], r["hidden"].shape[0], cfg.ffn)
+    h3, own = orc.ffn_stage(h2g, gpu_tables, given={"act": act})
+    errors["act"] = rel_l2(act, mxfp8_value(own["act"]))
     errors["h3 delta"] = rel_l2(r["out"].double() - h2g, h3 - h2g)
     print({k: f"{v:.2e}" for k, v in errors.items()}, flush=True)
     bad = {k: v for k, v in errors.items() if not v < REL}

@@ -299,6 +299,29 @@ def test_gemm_gated_residual_epilogue(device, in_place):
         assert torch.equal(wide_d.cpu(), wide), "inputs are not modified"
 
 
+@pytest.mark.parametrize("m,n,k,act", [(300, 384, 256, "gelu_tanh"), (1100, 1408, 512, "gelu_tanh"),
+                                       (1100, 1408, 512, None), (129, 200, 128, "gelu_tanh")])
+def test_gemm_producer_epilogue_matches_separate_passes(device, m, n, k, act):
+    """The fused FFN producer (GEMM + bias -> act -> MXFP8 in the epilogue) writes the same
+    bytes as the GEMM's bf16 output fed to the stand-alone producer kernel. Shapes cover both
+    tile sizes, rows and columns past a 256 tile, and N not a multiple of 128."""
+    g = torch.Generator().manual_seed(m + n)
+    x = (torch.randn(m, k, generator=g) * 2).to(torch.bfloat16).to(device)
+    w = (torch.randn(n, k, generator=g) * 0.05).to(torch.bfloat16).to(device)
+    bias = torch.randn(n, generator=g).to(torch.bfloat16).to(device)
+    q, s = vm.quantize_activation(x)
+    wq, ws = vm.quantize_activation(w)
+    fq, fs = vm.mxfp8_gemm_act_quantize(q, s, wq, ws, n, rows=m, bias=bias, act=act)
+    y = vm.mxfp8_gemm(q, s, wq, ws, n, rows=m, bias=bias)
+    if act == "gelu_tanh":
+        rq, rs, _ = vm.launch_gelu_quantize(y)
+    else:
+        rq, rs = vm.launch_quantize(y)
+    assert fq.shape == rq.shape and fs.shape == rs.shape
+    assert torch.equal(fq, rq)
+    assert torch.equal(fs, rs)
+
+
 def test_gemm_epilogue_argument_errors(device):
     q, s = vm.quantize_activation(torch.ones(4, 32, dtype=torch.bfloat16, device=device))
     wq, ws = vm.quantize_activation(torch.ones(8, 32, dtype=torch.bfloat16, device=device))

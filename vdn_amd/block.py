@@ -12,10 +12,10 @@ tables; src/inference/utils/lora.py:80-107 LoRA merge):
            lin_gate = sigmoid(up(down(x1))), alpha = FrameKDAAlpha(frame mean of x1)
   soft   = window attention(QK-RMSNorm + 3D RoPE(q, k), v) * gate                 [T, H]
   far    = VDA(raw q, k, v, beta, lin_gate, alpha)                                [T, H]
-  h      = h + gate_msa * (O(soft) + O_lin(far))            one GEMM epilogue each
+  h      = h + gate_msa * [O | O_lin]([soft | far])          one K = 2H GEMM, residual fused
   h      = h + O_c(cross attention(RMSNorm3(h) -> q, context -> k, v))
   x2, q2 = prenorm-quantize(h; norm2, scale_mlp, shift_mlp)
-  h      = h + gate_mlp * down(GELU-tanh(up(q2)))           GELU fused into its MXFP8 producer
+  h      = h + gate_mlp * down(GELU-tanh(up(q2)))           GELU + MXFP8 in the up GEMM epilogue
 
 The GELU-tanh FFN and the cross-attention have no reference kernel (the reference block uses
 SwiGLU and packs text into the sequence); they follow the torch definitions (GELU
@@ -128,8 +128,8 @@ class HybridDiTBlock(nn.Module):
         w = weights
         mk = lambda weight, bias=None: mx.MXFP8Linear(_linear(weight, bias), check_finite=False)
         self.qkv = mk(w.merged_qkv(cfg.lora_scale), w.qkv_b)
-        self.o = mk(w.o_w, w.o_b)
-        self.olin = mk(w.olin_w)
+        # to_out and to_out_linear share one GEMM over the concatenated branch outputs
+        self.o_cat = mk(torch.cat((w.o_w, w.olin_w), dim=1), w.o_b)
         self.cq, self.ck, self.cv, self.co = (mk(w.cq_w, w.cq_b), mk(w.ck_w, w.ck_b),
                                               mk(w.cv_w, w.cv_b), mk(w.co_w, w.co_b))
         self.up, self.down = mk(w.up_w, w.up_b), mk(w.down_w, w.down_b)
@@ -167,7 +167,7 @@ class HybridDiTBlock(nn.Module):
         """hidden [T, H] bf16 (video rows), temb [1, H], context [L, H] bf16; rope = (cos, sin)
         [T, 128]; window_plan from prepare_paper_window_plan; cross_plan from cross_attention_plan.
         Returns the new hidden [T, H] (a fresh tensor); with return_parts also a dict of
-        intermediate copies (tables, x1, qkv, soft, attn, far, h1, co, h2, up) for checking."""
+        intermediate copies (tables, x1, qkv, soft, far, h1, co, h2) for checking."""
         cfg, k = self.cfg, self.keep
         T, hd = hidden.shape
         heads, d = cfg.heads, cfg.head_dim
@@ -201,23 +201,23 @@ class HybridDiTBlock(nn.Module):
         cos, sin = rope
         q, kk = vw.paper_qk_rmsnorm_rope(raw_q, raw_k, k["norm_q"], k["norm_k"], cfg.eps, cos, sin,
                                          enabled=True)
-        soft = vw.paper_window_attention(q, kk, value, window_plan, d ** -0.5, enabled=True,
-                                         gate=soft_gate)
+        # the two branch outputs land side by side in one [T, 2H] buffer
+        both = torch.empty((T, 2 * hd), dtype=torch.bfloat16, device=dev)
+        vw.paper_window_attention(q, kk, value, window_plan, d ** -0.5, enabled=True,
+                                  gate=soft_gate, out=both[:, :hd].view(T, heads, d))
         del q, kk
-        snap("soft", soft.view(T, hd))
-        qs, ss = mx.launch_quantize(soft.view(T, hd))
-        attn = self.o.forward_quantized(qs, ss, rows=T)
-        snap("attn", attn)
-        del soft, qs, ss
         bounds = window_plan.bounds
-        far = vv.vda_forward(raw_q, raw_k, value, beta, lin_gate.view(T, heads, d), alpha, bounds,
-                             frames, spatial, k["vda_norm"], cfg.eps, chunk_size=cfg.vda_chunk)
+        vv.vda_forward(raw_q, raw_k, value, beta, lin_gate.view(T, heads, d), alpha, bounds,
+                       frames, spatial, k["vda_norm"], cfg.eps, chunk_size=cfg.vda_chunk,
+                       out=both[:, hd:])
         del qkv, raw_q, raw_k, value, lin_gate
-        snap("far", far)
-        qf, sf = mx.launch_quantize(far)
-        self.olin.forward_quantized(qf, sf, rows=T, out=h, addend=attn, residual=h, gate=gate_msa)
+        snap("soft", both[:, :hd])
+        snap("far", both[:, hd:])
+        qb, sb = mx.launch_quantize(both)
+        del both
+        self.o_cat.forward_quantized(qb, sb, rows=T, out=h, residual=h, gate=gate_msa)
         snap("h1", h)
-        del far, qf, sf, attn
+        del qb, sb
 
         # ---- cross-attention to the context rows ----
         zeros = self._zeros(dev)
@@ -242,10 +242,8 @@ class HybridDiTBlock(nn.Module):
         # ---- FFN ----
         _, q4, s4, _ = mx.launch_prenorm_quantize(h, k["norm2"], cfg.eps, scale_mlp, shift_mlp,
                                                   idx, write_bf16=False)
-        up = self.up.forward_quantized(q4, s4, rows=T)
-        snap("up", up)
-        q5, s5, _ = mx.launch_gelu_quantize(up)
-        del up
+        q5, s5 = self.up.forward_act_quantized(q4, s4, rows=T, act="gelu_tanh")
+        snap("ffn_codes", (q5, s5))
         self.down.forward_quantized(q5, s5, rows=T, out=h, residual=h, gate=gate_mlp)
         return (h, parts) if return_parts else h
 

@@ -62,6 +62,14 @@ struct Epilogue {
   int64_t ldc;
   uint32_t* nonfinite;
   int vec;  // 16-byte accesses: n, every leading dimension and pointer 8-element aligned
+  // Producer mode (q_out non-null): instead of bf16 `out`, y = bf16(bf16(acc) + bias) goes
+  // through `act` (0 none, 1 GELU-tanh, rounded to bf16) and is stored as MXFP8 codes
+  // q_out [mp, kp_out] + swizzled scales s_out, exactly what the producer kernels write
+  // for that bf16 matrix. Rows >= out_rows and columns >= n are stored as zero.
+  uint8_t* q_out;
+  uint8_t* s_out;
+  int64_t kp_out;
+  int act;
 };
 
 // Epilogue arithmetic of one element (see Epilogue).
@@ -300,7 +308,34 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
   constexpr int kPasses = BM / kRowsPerPass;
   constexpr int kBatch = kPasses < 8 ? kPasses : 8;
   static_assert(kPasses % kBatch == 0, "epilogue batching");
-  if (ep.vec && col + 8 <= n) {
+  if (ep.q_out != nullptr) {
+    // Eight consecutive columns per lane; the four lanes of a 32-column block and the
+    // sixteen of a 128-column chunk are consecutive lanes of one row (kChunksPerRow is a
+    // multiple of 16), which is the lane layout quantize_store8 expects.
+    static_assert(kChunksPerRow % 16 == 0, "producer epilogue lane layout");
+    const int64_t chunk128 = (n0 >> 7) + (chunk >> 4);
+    // a 256-wide tile can reach past the padded output (rows >= mp, chunks >= kp_out / 128);
+    // both tests are uniform over the 16 lanes of a chunk
+    const bool chunk_in = chunk128 < (ep.kp_out >> 7);
+    for (int pass = 0; pass < kPasses; ++pass) {
+      const int r = pass * kRowsPerPass + tid / kChunksPerRow;
+      const int64_t row = m0 + r;
+      if (row >= mp || !chunk_in) continue;
+      float y[8];
+      unpack8(*reinterpret_cast<const u32x4*>(lds_raw + r * kStageStride + chunk * 16), y);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float v = 0.f;
+        if (row < out_rows && col + e < n) {
+          v = ep.bias != nullptr ? round_bf16(y[e] + bias8[e]) : y[e];
+          if (ep.act == 1) v = round_bf16(gelu_tanh(v));
+          bad = bad || !(fabsf(v) < INFINITY);
+        }
+        y[e] = v;
+      }
+      quantize_store8(y, tid & 15, row, chunk128, ep.kp_out, ep.q_out, ep.s_out);
+    }
+  } else if (ep.vec && col + 8 <= n) {
     // Batches of kBatch rows: every load of a batch is issued before any arithmetic, so
     // the addend/residual latency is paid once per batch rather than once per row.
     for (int b0 = 0; b0 < kPasses; b0 += kBatch) {
@@ -419,7 +454,49 @@ VDN_API int vdn_mxfp8_gemm(const void* a, const void* a_scales, int64_t mp, cons
   const Epilogue ep{static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(addend),
                     ld_add, static_cast<const uint16_t*>(residual), ld_res,
                     static_cast<const uint16_t*>(gate), static_cast<uint16_t*>(out), ldc,
-                    nonfinite, vec ? 1 : 0};
+                    nonfinite, vec ? 1 : 0, nullptr, nullptr, 0, 0};
+  if (mp >= 1024 && np >= 1024)
+    return launch_gemm<256, 256, 2, 2>(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
+  return launch_gemm<128, 128, 2, 2>(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
+}
+
+// Fused FFN producer: the GEMM of vdn_mxfp8_gemm (+ bias), then act (0 none, 1 GELU-tanh)
+// rounded to bf16 and quantized to MXFP8 in the epilogue, in place of the bf16 output and
+// a separate producer pass. Output: codes q [mp, pad128(n)] and swizzled scales s
+// (mp * pad128(n) / 32 bytes); rows >= out_rows and columns >= n are zero. nonfinite
+// (nullable) receives 1 when an activated value is not finite.
+// Reference: MXFP8Linear.forward_quantized (src/models/ops/mxfp8_linear.py:61-93) followed
+// by the activation producer (mxfp8_kernels.py:62-84, 113-124) in tp_ff_forward
+// (src/inference/utils/tensor_parallel.py:147-161).
+VDN_API int vdn_mxfp8_gemm_act_quantize(const void* a, const void* a_scales, int64_t mp,
+                                        const void* w, const void* w_scales, int64_t np,
+                                        int64_t kp, const void* bias, int act, void* q,
+                                        void* scales, int64_t out_rows, int64_t n,
+                                        uint32_t* nonfinite, void* stream) {
+  const char* name = "vdn_mxfp8_gemm_act_quantize";
+  if (a == nullptr || a_scales == nullptr || w == nullptr || w_scales == nullptr || q == nullptr ||
+      scales == nullptr)
+    return set_error(kInvalidArgument, "%s: null pointer argument", name);
+  if (mp <= 0 || np <= 0 || kp <= 0 || mp % 128 || np % 128 || kp % 128)
+    return set_error(kInvalidArgument, "%s: padded M/N/K must be positive multiples of 128", name);
+  if (n <= 0 || n > np || out_rows < 0 || out_rows > mp)
+    return set_error(kInvalidArgument, "%s: invalid output geometry", name);
+  if (act != 0 && act != 1) return set_error(kInvalidArgument, "%s: unknown activation %d", name, act);
+  if (!aligned(a, 16) || !aligned(w, 16) || !aligned(a_scales, 4) || !aligned(w_scales, 4) ||
+      !aligned(q, 16) || !aligned(scales, 4) || (bias != nullptr && !aligned(bias, 16)))
+    return set_error(kInvalidArgument, "%s: misaligned buffer", name);
+  if (out_rows == 0) return kOk;
+  const int64_t kp_out = (n + 127) / 128 * 128;
+  // Every column chunk up to kp_out must be produced: the padded GEMM width covers it.
+  if (kp_out > np) return set_error(kInvalidArgument, "%s: padded N smaller than pad128(n)", name);
+  const Epilogue ep{static_cast<const uint16_t*>(bias), nullptr, 0, nullptr, 0, nullptr, nullptr,
+                    0, nonfinite, n % 8 == 0 ? 1 : 0, static_cast<uint8_t*>(q),
+                    static_cast<uint8_t*>(scales), kp_out, act};
+  auto st = static_cast<hipStream_t>(stream);
+  auto* ap = static_cast<const uint8_t*>(a);
+  auto* asp = static_cast<const uint8_t*>(a_scales);
+  auto* wp = static_cast<const uint8_t*>(w);
+  auto* wsp = static_cast<const uint8_t*>(w_scales);
   if (mp >= 1024 && np >= 1024)
     return launch_gemm<256, 256, 2, 2>(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
   return launch_gemm<128, 128, 2, 2>(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);

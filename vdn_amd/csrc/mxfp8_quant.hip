@@ -62,46 +62,11 @@ __device__ __forceinline__ void load_row8(const uint16_t* __restrict__ x, int64_
 }
 
 #pragma clang fp contract(off)
-__device__ __forceinline__ float gelu_tanh(float x) {
-  // torch's approximate="tanh" GELU, evaluated in fp32 and rounded once by the caller.
-  const float kBeta = 0.7978845608028654f;  // sqrt(2/pi)
-  const float kKappa = 0.044715f;
-  const float cube = x * x * x;
-  const float inner = kBeta * (x + kKappa * cube);
-  return 0.5f * x * (1.f + tanhf(inner));
-}
-
 __device__ __forceinline__ float silu_mul(float a, float g) {
   const float sig = 1.f / (1.f + expf(-g));
   return a * (g * sig);
 }
 #pragma clang fp contract(on)
-
-// Quantizes the 8 values a lane holds (one quarter of a 32-block), stores the 8 codes
-// and, from lane 0 of each 16-lane group, the chunk's 4 scale bytes.
-__device__ __forceinline__ void quantize_store8(const float* v, int lane16, int64_t r, int64_t chunk,
-                                                int64_t kp, uint8_t* __restrict__ q,
-                                                uint8_t* __restrict__ s) {
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 16));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 16));
-  float inv;
-  const uint32_t scale = e8m0_from_amax(amax, &inv);
-  float scaled[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) scaled[i] = v[i] * inv;
-  const u32x2 codes = e4m3x8(scaled);
-  *reinterpret_cast<u32x2*>(q + r * kp + chunk * 128 + lane16 * 8) = codes;
-  const uint32_t s1 = __shfl_down(scale, 4, 16);
-  const uint32_t s2 = __shfl_down(scale, 8, 16);
-  const uint32_t s3 = __shfl_down(scale, 12, 16);
-  if (lane16 == 0) {
-    const uint32_t word = scale | (s1 << 8) | (s2 << 16) | (s3 << 24);
-    *reinterpret_cast<uint32_t*>(s + swizzled_scale_offset(r, chunk * 4, kp >> 7)) = word;
-  }
-}
 
 template <int kAct, bool kVec>
 __global__ void __launch_bounds__(kThreads)

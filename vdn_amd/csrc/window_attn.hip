@@ -5,7 +5,7 @@
 // (softmax_attention/kernels.py:51-67). Each query block attends to a short list of key
 // intervals (the frame window, global rows, anchor frames), so no K/V gather copies exist.
 //
-// Per workgroup: 128 queries of one head (4 waves x 32), key tiles of 64.
+// Per workgroup: 256 queries of one head (8 waves x 32), key tiles of 64.
 //   Sᵀ[key][q] = K · Qᵀ   on v_mfma_f32_32x32x16_bf16 (A = K rows, B = Q rows; Q fragments for
 //                         all 128 channels stay in registers for the whole kernel);
 //   online softmax in the exp2 domain, fp32 running max / sum per query;
@@ -27,9 +27,9 @@ namespace vdn {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kBM = 128;
 constexpr int kBN = 64;
 constexpr int kMaxIntervals = 8;
+constexpr int kBlockWaves = 8;  // queries per block = 32 * kBlockWaves (must match the plan)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -57,7 +57,10 @@ struct Layout {
   int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh;  // token / head strides (elements)
 };
 
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// kWaves waves of 32 queries each: a workgroup owns kBM = 32 kWaves queries, and every K/V
+// tile it loads serves all of them.
+template <int kWaves>
+__global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restrict__ grp_kv,
                    const int* __restrict__ grp_n, int nblocks, int heads, float scale_log2,
                    const uint16_t* __restrict__ gate, int64_t g_st, int64_t g_sh,
@@ -69,6 +72,11 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
   __shared__ __attribute__((aligned(1024))) uint16_t sK1[kBN * kD];
   __shared__ __attribute__((aligned(1024))) uint16_t sV0[kBN * kD];
   __shared__ __attribute__((aligned(1024))) uint16_t sV1[kBN * kD];
+  constexpr int kBM = 32 * kWaves;
+  constexpr int kThreads = 64 * kWaves;
+  constexpr int kSegs = kBN / 4 / kWaves;  // 1 KB (4-row) segments per tensor per wave
+  static_assert(kSegs * kWaves * 4 == kBN && kWaves % 4 == 0, "segment mapping");
+  static_assert(kBM * kD <= 4 * kBN * kD, "the epilogue stages the block in the tile buffers");
 
   // ---- work item: (head, query block); consecutive ids of a head land on one XCD ----
   const int total = nblocks * heads;
@@ -105,10 +113,10 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
   // per-lane byte offsets within a tile are fixed; a tile adds a wave-uniform base, so the
   // loads take the scalar-base + 32-bit-offset form with no per-tile vector address math.
   const int seg_row = lane >> 4, phys = lane & 15;
-  uint32_t koff[4], voff[4];
+  uint32_t koff[kSegs], voff[kSegs];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int row = (j * 4 + wave) * 4 + seg_row;
+  for (int j = 0; j < kSegs; ++j) {
+    const int row = (j * kWaves + wave) * 4 + seg_row;
     koff[j] = static_cast<uint32_t>(row * in.k_st * 2 + 16 * (phys ^ swz_k(row)));
     voff[j] = static_cast<uint32_t>(row * in.v_st * 2 + 16 * (phys ^ swz_v(row)));
   }
@@ -119,15 +127,15 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     const char* vb = v_head + static_cast<int64_t>(a) * in.v_st * 2;
     if (b - a == kBN) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int seg = j * 4 + wave;
+      for (int j = 0; j < kSegs; ++j) {
+        const int seg = j * kWaves + wave;
         load_to_lds16(kb + koff[j], dk + seg * 4 * kD);
         load_to_lds16(vb + voff[j], dv + seg * 4 * kD);
       }
     } else {  // tail tile: rows past the interval end repeat its last key
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int seg = j * 4 + wave;
+      for (int j = 0; j < kSegs; ++j) {
+        const int seg = j * kWaves + wave;
         const int row = seg * 4 + seg_row;
         const int r = min(row, b - a - 1);
         const uint32_t ko = static_cast<uint32_t>(r * in.k_st * 2 + 16 * (phys ^ swz_k(row)));
@@ -268,9 +276,13 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
 
   // ---- epilogue: O / l, optional gate, through LDS to coalesced rows ----
   const float inv_l = l > 0.f ? 1.0f / l : 0.f;
-  // [128 queries][128 channels] bf16: queries 0-63 in sK0, 64-127 in sK1 (wave-uniform)
+  // [kBM queries][128 channels] bf16 staged across the tile buffers, 64 queries per buffer
+  auto stage_rows = [&](int r) -> uint16_t* {
+    const int which = r >> 6;  // uniform per wave for both uses below
+    return which == 0 ? sK0 : which == 1 ? sK1 : which == 2 ? sV0 : sV1;
+  };
   const int qr = wave * 32 + col;
-  uint16_t* sO = qr < 64 ? sK0 : sK1;
+  uint16_t* sO = stage_rows(qr);
   float gv = 1.f;
   if (gate != nullptr && q_live) gv = bf16_bits_to_f32(gate[static_cast<int64_t>(my_q) * g_st + h * g_sh]);
 #pragma unroll
@@ -286,11 +298,11 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     lse[static_cast<int64_t>(my_q) * l_st + h * l_sh] = (m + log2f(l)) * kLn2;
   __syncthreads();
   // 16 lanes write one query row (256 bytes)
-  for (int r = tid >> 4; r < kBM; r += 16) {
+  for (int r = tid >> 4; r < kBM; r += kThreads / 16) {
     const int q = q0 + r;
     if (q >= q1) continue;
     const int c8 = (tid & 15) * 8;
-    const uint16_t* src = r < 64 ? sK0 : sK1;
+    const uint16_t* src = stage_rows(r);
     *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(q) * o_st + h * o_sh + c8) =
         *reinterpret_cast<const u32x4*>(&src[(r & 63) * kD + c8]);
   }
@@ -307,7 +319,7 @@ using namespace vdn;
 // window_softmax_reference (window.py:56-111), apply_softmax_gate (kernels.py:51-67).
 // q, k, v: bf16 [rows, heads, 128] (token / head strides, unit channel stride);
 // blocks: int32 [nblocks, 3] = (first query, end of its query group, group index), each
-// block at most 128 queries; grp_kv: int32 [groups, 8, 2] key intervals [a, b); grp_n:
+// block at most 256 queries; grp_kv: int32 [groups, 8, 2] key intervals [a, b); grp_n:
 // int32 [groups] interval counts. gate (nullable): bf16 per (token, head) scalar multiplied
 // into the bf16 output. out: bf16 rows of 128 channels; lse (nullable): fp32 natural-log
 // sum of exp of the scaled scores.
@@ -334,7 +346,8 @@ VDN_API int vdn_window_attention(const void* q, int64_t q_st, int64_t q_sh, cons
                   static_cast<const uint16_t*>(v), q_st, q_sh, k_st, k_sh, v_st, v_sh};
   const int64_t total = static_cast<int64_t>(nblocks) * heads;
   if (total > (1ll << 31) - 1) return set_error(kUnsupported, "%s: too many blocks", name);
-  hipLaunchKernelGGL(window_attn_kernel, dim3(static_cast<unsigned>(total)), dim3(256), 0,
+  hipLaunchKernelGGL(window_attn_kernel<kBlockWaves>, dim3(static_cast<unsigned>(total)),
+                     dim3(kBlockWaves * 64), 0,
                      static_cast<hipStream_t>(stream), in, blocks, grp_kv, grp_n, nblocks, heads,
                      scale * kLog2e, static_cast<const uint16_t*>(gate), g_st, g_sh,
                      static_cast<uint16_t*>(out), o_st, o_sh, lse, l_st, l_sh);

@@ -284,6 +284,36 @@ def mxfp8_gemm(data, scales, weight_data, weight_scale, n, *, rows=None, bias=No
     return out
 
 
+def mxfp8_gemm_act_quantize(data, scales, weight_data, weight_scale, n, *, rows=None, bias=None,
+                            act="gelu_tanh", check_finite=False):
+    """MXFP8 codes/scales of act(bf16(dequant(data) @ dequant(weight)ᵀ + bias)) for the next
+    projection, produced in the GEMM epilogue. Bit-identical to mxfp8_gemm followed by
+    launch_gelu_quantize (act "gelu_tanh") or launch_quantize (act None).
+    Returns (codes u8 [RP, pad128(n)], flat swizzled scales u8)."""
+    mp, kp = data.shape
+    np_, kpw = weight_data.shape
+    if kp != kpw:
+        raise ValueError("activation and weight padded K differ")
+    if act not in ("gelu_tanh", None):
+        raise ValueError("act must be 'gelu_tanh' or None")
+    rows = mp if rows is None else rows
+    kp_out = -(-n // 128) * 128
+    q = torch.empty((mp, kp_out), dtype=torch.uint8, device=data.device)
+    s = torch.empty(mp * kp_out // 32, dtype=torch.uint8, device=data.device)
+    flag = torch.zeros(1, dtype=torch.int32, device=data.device) if check_finite else None
+    if rows:
+        _lib.call("vdn_mxfp8_gemm_act_quantize", data.data_ptr(), scales.data_ptr(), mp,
+                  weight_data.data_ptr(), weight_scale.data_ptr(), np_, kp, _lib.ptr(bias),
+                  1 if act == "gelu_tanh" else 0, q.data_ptr(), s.data_ptr(), rows, n,
+                  _lib.ptr(flag), _lib.stream(data.device))
+    else:
+        q.zero_()
+        s.zero_()
+    if check_finite and int(flag.item()) != 0:
+        raise ValueError("nonfinite MXFP8 activation")
+    return q, s
+
+
 class MXFP8Linear(nn.Module):
     """Inference-only effective weight as two uint8 buffers (mxfp8_linear.py:36-102).
 
@@ -345,6 +375,24 @@ class MXFP8Linear(nn.Module):
         return mxfp8_gemm(data, scales, self.weight_data, self.weight_scale, self.out_features,
                           rows=rows, bias=bias, out=out, accumulate=accumulate, addend=addend,
                           residual=residual, gate=gate, check_finite=self.check_finite)
+
+    @torch.no_grad()
+    def forward_act_quantized(self, data, scales, *, rows=None, act="gelu_tanh"):
+        """Consume MXFP8 input and return the MXFP8 codes/scales of act(bf16 output): the
+        producer of the next projection fused into this GEMM's epilogue."""
+        if data.device.type != "cuda":
+            raise RuntimeError("native MXFP8 requires a HIP device; no fallback")
+        np_, kp = padded_shape(self.out_features, self.in_features)
+        if data.ndim != 2 or data.shape[1] != kp or data.shape[0] % 128 or data.dtype != torch.uint8:
+            raise ValueError("invalid padded activation shape")
+        if scales.shape != (scale_numel(data.shape[0], kp),):
+            raise ValueError("invalid activation scale layout")
+        bias = None
+        if self.bias is not None:
+            bias = self.bias.to(device=data.device, dtype=torch.bfloat16).contiguous()
+        return mxfp8_gemm_act_quantize(data, scales, self.weight_data, self.weight_scale,
+                                       self.out_features, rows=rows, bias=bias, act=act,
+                                       check_finite=self.check_finite)
 
     @torch.no_grad()
     def forward(self, x):

@@ -18,7 +18,7 @@ import torch
 
 from . import _lib
 
-BLOCK_M = 128
+BLOCK_M = 256
 MAX_INTERVALS = 8
 
 
@@ -244,10 +244,12 @@ def prepare_paper_window_plan(layout: SequenceLayout, bounds, anchor_frames="non
 # ---------------------------------------------------------------------- attention ----
 
 def paper_window_attention(query, key, value, plan: PaperWindowPlan, scale=None, *,
-                           enabled=False, return_lse=False, nvtx=True, gate=None):
+                           enabled=False, return_lse=False, nvtx=True, gate=None, out=None):
     """[used+padding, H, D] -> fresh output of the same shape; padding rows are zero
     (paper_window.py:182-243). LSE (fp32 [rows, H], natural log) is -inf on padding.
-    `gate` ([rows, H] or [rows, H, 1]) fuses apply_softmax_gate: out = bf16(bf16(o) * gate)."""
+    `gate` ([rows, H] or [rows, H, 1]) fuses apply_softmax_gate: out = bf16(bf16(o) * gate).
+    `out` (optional bf16 [rows, H, D] view with unit channel stride) receives the result
+    instead of a fresh tensor, e.g. a column slice of a wider buffer."""
     if not enabled:
         raise RuntimeError("paper window attention is disabled; retain the existing caller path "
                            "or explicitly enable")
@@ -270,7 +272,11 @@ def paper_window_attention(query, key, value, plan: PaperWindowPlan, scale=None,
     if not math.isfinite(scale):
         raise ValueError("scale must be finite")
     rows, h, d = query.shape
-    out = torch.empty((rows, h, d), dtype=query.dtype, device=query.device)
+    if out is None:
+        out = torch.empty((rows, h, d), dtype=query.dtype, device=query.device)
+    elif (out.shape != (rows, h, d) or out.dtype != query.dtype or out.device != query.device
+          or out.stride(-1) != 1):
+        raise ValueError("out must be a [rows, H, D] view like the queries, unit channel stride")
     lse = torch.empty((rows, h), dtype=torch.float32, device=query.device) if return_lse else None
     used = plan.layout.seq_len
     if rows > used:
