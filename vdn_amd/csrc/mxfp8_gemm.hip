@@ -222,12 +222,29 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
     __syncthreads();
     if constexpr (more) issue_scale_loads(ks + 1, buf ^ 1);
     uint32_t sa[TM], sb[TN];
+    if constexpr (WM == 128 && WN == 128) {
+      // Rows 16 mt + frag_row of a 128-row wave tile: the even-mt words are the 16 bytes at
+      // a_sidx[0] and the odd-mt words the 16 bytes at a_sidx[1], so four 16-byte reads
+      // fetch every scale word of the step before any fragment read.
+      const u32x4 ae = *reinterpret_cast<const u32x4*>(&lds[buf][a_sidx[0]]);
+      const u32x4 ao = *reinterpret_cast<const u32x4*>(&lds[buf][a_sidx[1]]);
+      const u32x4 be = *reinterpret_cast<const u32x4*>(&lds[buf][b_sidx[0]]);
+      const u32x4 bo = *reinterpret_cast<const u32x4*>(&lds[buf][b_sidx[1]]);
 #pragma unroll
-    for (int mt = 0; mt < TM; ++mt)
-      sa[mt] = *reinterpret_cast<const uint32_t*>(&lds[buf][a_sidx[mt]]) >> block_shift;
+      for (int i = 0; i < 4; ++i) {
+        sa[2 * i] = ae[i] >> block_shift;
+        sa[2 * i + 1] = ao[i] >> block_shift;
+        sb[2 * i] = be[i] >> block_shift;
+        sb[2 * i + 1] = bo[i] >> block_shift;
+      }
+    } else {
 #pragma unroll
-    for (int nt = 0; nt < TN; ++nt)
-      sb[nt] = *reinterpret_cast<const uint32_t*>(&lds[buf][b_sidx[nt]]) >> block_shift;
+      for (int mt = 0; mt < TM; ++mt)
+        sa[mt] = *reinterpret_cast<const uint32_t*>(&lds[buf][a_sidx[mt]]) >> block_shift;
+#pragma unroll
+      for (int nt = 0; nt < TN; ++nt)
+        sb[nt] = *reinterpret_cast<const uint32_t*>(&lds[buf][b_sidx[nt]]) >> block_shift;
+    }
     const uint8_t* abuf = lds[buf];
     const uint8_t* bbuf = lds[buf] + BM * kBK;
     auto frag = [&](const uint8_t* base, int row) {
@@ -249,6 +266,9 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
     for (int mt = 0; mt < TM; ++mt) {
       i32x8 anext = acur;
       if (mt + 1 < TM) anext = frag(abuf, wm * WM + (mt + 1) * 16 + frag_row);
+      // The next A fragment's reads stay ahead of this group's MFMAs (the scheduler would
+      // otherwise sink them below, making the next group wait on their full latency).
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int nt = 0; nt < TN; ++nt) {
         // D = W_frag . A_frag^T: lane l then holds output columns 4(l/16)..+3 of row l%16
@@ -261,6 +281,7 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
         for (int j = 0; j < kSegsPerGroup; ++j)
           if (mt * kSegsPerGroup + j < kSegs) issue_segment(ks + 1, buf ^ 1, mt * kSegsPerGroup + j);
       }
+      __builtin_amdgcn_sched_barrier(0);
       acur = anext;
     }
   };
