@@ -27,7 +27,8 @@ namespace vdn {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kBN = 64;
+constexpr int kBN = 128;
+constexpr int kKT = kBN / 32;  // 32-key score accumulators per tile
 constexpr int kMaxIntervals = 8;
 constexpr int kBlockWaves = 8;  // queries per block = 32 * kBlockWaves (must match the plan)
 constexpr float kLog2e = 1.4426950408889634f;
@@ -178,9 +179,9 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     const int a = a0 + t * kBN, b = min(a + kBN, b0);
 
     // ---- Sᵀ = K Qᵀ for the tile's 64 keys (two 32-key accumulators) ----
-    f32x16 s[2];
+    f32x16 s[kKT];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
+    for (int kt = 0; kt < kKT; ++kt) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) s[kt][v] = 0.f;
       const int row = kt * 32 + col;
@@ -194,7 +195,7 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     // ---- online softmax (exp2 domain; scores scaled inside the exponent's fma) ----
     if (b - a < kBN) {  // tail tile: keys past the interval end do not exist
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      for (int kt = 0; kt < kKT; ++kt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int key = a + kt * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
@@ -203,7 +204,7 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     }
     float mx = -INFINITY;
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+    for (int kt = 0; kt < kKT; ++kt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kt][v]);
     mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
@@ -220,7 +221,7 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     }
     float rs = 0.f;
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+    for (int kt = 0; kt < kKT; ++kt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][v], scale_log2, -m));
@@ -232,7 +233,7 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
 
     // ---- Oᵀ += Vᵀ Pᵀ, 16 keys per MFMA ----
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < kBN / 16; ++c) {
       bf16x8 pb;
 #pragma unroll
       for (int j = 0; j < 8; ++j) pb[j] = static_cast<__bf16>(s[c >> 1][(c & 1) * 8 + j]);
@@ -278,7 +279,7 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
   const float inv_l = l > 0.f ? 1.0f / l : 0.f;
   // [kBM queries][128 channels] bf16 staged across the tile buffers, 64 queries per buffer
   auto stage_rows = [&](int r) -> uint16_t* {
-    const int which = r >> 6;  // uniform per wave for both uses below
+    const int which = r / kBN;  // uniform per wave for both uses below
     return which == 0 ? sK0 : which == 1 ? sK1 : which == 2 ? sV0 : sV1;
   };
   const int qr = wave * 32 + col;
@@ -292,7 +293,7 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
       const int d = 32 * db + (v >> 2) * 8 + g * 4 + (v & 3);
       float y = round_bf16(o[db][v] * inv_l);
       if (gate != nullptr) y = y * gv;
-      sO[(qr & 63) * kD + d] = f32_to_bf16_bits(y);
+      sO[(qr % kBN) * kD + d] = f32_to_bf16_bits(y);
     }
   if (lse != nullptr && q_live && g == 0)
     lse[static_cast<int64_t>(my_q) * l_st + h * l_sh] = (m + log2f(l)) * kLn2;
@@ -304,7 +305,7 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     const int c8 = (tid & 15) * 8;
     const uint16_t* src = stage_rows(r);
     *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(q) * o_st + h * o_sh + c8) =
-        *reinterpret_cast<const u32x4*>(&src[(r & 63) * kD + c8]);
+        *reinterpret_cast<const u32x4*>(&src[(r % kBN) * kD + c8]);
   }
 }
 
