@@ -196,7 +196,7 @@ class HybridDiTBlock(nn.Module):
         soft_gate = torch.sigmoid(small[:, :heads] + k["soft_gate_b"])
         beta = torch.sigmoid(small[:, heads:2 * heads])
         lin_gate = torch.sigmoid(F.linear(small[:, 2 * heads:], k["lgate_up_w"], k["lgate_up_b"]))
-        frame_mean = x1.view(frames, spatial, hd).float().mean(1)
+        frame_mean = x1.view(frames, spatial, hd).mean(1, dtype=torch.float32)
         alpha = self.frame_alpha(frame_mean)
         cos, sin = rope
         q, kk = vw.paper_qk_rmsnorm_rope(raw_q, raw_k, k["norm_q"], k["norm_k"], cfg.eps, cos, sin,

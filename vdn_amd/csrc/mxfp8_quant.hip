@@ -138,14 +138,17 @@ __device__ __forceinline__ void load_table8(const void* __restrict__ t, int f32,
   }
 }
 
-// One wave per padded row, kS 8-column slices per lane (slice = lane + 64 j), so the row's
-// sum of squares is a wave reduction (no LDS, no barrier) and four rows share a block.
-// Requires the vector path (k % 8 == 0, 16-byte aligned rows) and 16-byte aligned tables
-// with strides that are multiples of 8 elements. Arithmetic and rounding are the same as
-// prenorm_quantize_kernel's.
+// Sixteen padded rows per workgroup (one per wave, kS 8-column slices per lane). When the
+// rows share one AdaLN table row (the usual case: one timestep for a whole clip) the weight,
+// scale and shift rows are staged once in LDS as fp32, so they are read from L2 once per 16
+// rows instead of once per row; otherwise each row reads its own table row. Arithmetic and
+// rounding are those of prenorm_quantize_kernel.
+constexpr int kPrenormRows = 16;
+constexpr int kPrenormThreads = 64 * kPrenormRows;
+
 template <int kS>
-__global__ void __launch_bounds__(kThreads)
-prenorm_quantize_wave_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t k,
+__global__ void __launch_bounds__(kPrenormThreads)
+prenorm_quantize_rows_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t k,
                              int64_t stride, const void* __restrict__ weight, int weight_f32,
                              float eps, const void* __restrict__ scale, int64_t scale_stride,
                              const void* __restrict__ shift, int64_t shift_stride,
@@ -154,57 +157,104 @@ prenorm_quantize_wave_kernel(const uint16_t* __restrict__ x, int64_t rows, int64
                              uint8_t* __restrict__ s, uint8_t* __restrict__ finite, int64_t kp,
                              int64_t rp) {
 #pragma clang fp contract(off)
-  const int lane = threadIdx.x & 63;
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
-  if (r >= rp) return;  // whole wave
-  const bool in_row = r < rows;
+  constexpr int kCols = 64 * kS * 8;
+  __shared__ __attribute__((aligned(16))) float tab[3][kCols];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kPrenormRows;
   const int64_t slices = kp >> 3;
-  const int64_t table_row = in_row ? indices[r] : 0;
-  float v[kS][8];
-  bool bad = false;
-  float ss = 0.f;
+  // one table row for the whole workgroup?
+  const int64_t idx0 = r0 < rows ? indices[r0] : 0;
+  int same = 1;
+  if (tid < kPrenormRows && r0 + tid < rows) same = indices[r0 + tid] == idx0;
+  const bool shared_row = __syncthreads_and(same) != 0;
+  if (shared_row) {
+    for (int64_t c = tid * 4; c < kp; c += kPrenormThreads * 4) {
 #pragma unroll
-  for (int j = 0; j < kS; ++j) {
-    const int64_t sl = lane + 64 * j;
-    load_row8<true>(x, sl < slices ? r : rows, sl * 8, rows, k, stride, v[j], bad);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ss += v[j][i] * v[j][i];
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-  const float ms = ss / static_cast<float>(k) + eps;
-  const float inv_rms = static_cast<float>(1.0 / sqrt(static_cast<double>(ms)));
-#pragma unroll
-  for (int j = 0; j < kS; ++j) {
-    const int64_t sl = lane + 64 * j;
-    if (sl >= slices) break;  // slices beyond KP: none of this lane's later ones exist
-    const int64_t c0 = sl * 8;
-    if (in_row && c0 < k) {
-      float w[8], sc[8], sh[8];
-      load_table8(weight, weight_f32, c0, w);
-      load_table8(scale, tables_f32, table_row * scale_stride + c0, sc);
-      load_table8(shift, tables_f32, table_row * shift_stride + c0, sh);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float t = (v[j][i] * inv_rms) * w[i];
-        const float u = 1.0f + sc[i];
-        v[j][i] = round_bf16(t * u + sh[i]);
-        bad |= !(fabsf(v[j][i]) < INFINITY);
+      for (int e = 0; e < 4; ++e) {
+        const int64_t cc = c + e;
+        float wv = 0.f, sv = 0.f, hv = 0.f;
+        if (cc < k) {
+          wv = weight_f32 ? static_cast<const float*>(weight)[cc]
+                          : bf16_bits_to_f32(static_cast<const uint16_t*>(weight)[cc]);
+          const int64_t so = idx0 * scale_stride + cc, ho = idx0 * shift_stride + cc;
+          sv = tables_f32 ? static_cast<const float*>(scale)[so]
+                          : bf16_bits_to_f32(static_cast<const uint16_t*>(scale)[so]);
+          hv = tables_f32 ? static_cast<const float*>(shift)[ho]
+                          : bf16_bits_to_f32(static_cast<const uint16_t*>(shift)[ho]);
+        }
+        tab[0][cc] = wv;
+        tab[1][cc] = sv;
+        tab[2][cc] = hv;
       }
-      if (y != nullptr) {
-        u32x4 packed;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) packed[i] = pack_bf16x2(v[j][2 * i], v[j][2 * i + 1]);
-        *reinterpret_cast<u32x4*>(y + r * k + c0) = packed;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[j][i] = 0.f;
     }
-    quantize_store8(v[j], lane & 15, r, sl >> 4, kp, q, s);
   }
-  const bool any_bad = __ballot(bad) != 0;
-  if (lane == 0) finite[r] = any_bad ? 0 : 1;
+  __syncthreads();
+  {
+    const int64_t r = r0 + wave;
+    if (r >= rp) return;  // whole wave (no barrier follows)
+    const bool in_row = r < rows;
+    const int64_t table_row = in_row ? indices[r] : 0;
+    float v[kS][8];
+    bool bad = false;
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < kS; ++j) {
+      const int64_t sl = lane + 64 * j;
+      load_row8<true>(x, sl < slices ? r : rows, sl * 8, rows, k, stride, v[j], bad);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += v[j][i] * v[j][i];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    const float ms = ss / static_cast<float>(k) + eps;
+    const float inv_rms = static_cast<float>(1.0 / sqrt(static_cast<double>(ms)));
+#pragma unroll
+    for (int j = 0; j < kS; ++j) {
+      const int64_t sl = lane + 64 * j;
+      if (sl >= slices) break;  // slices beyond KP: none of this lane's later ones exist
+      const int64_t c0 = sl * 8;
+      if (in_row && c0 < k) {
+        float w[8], sc[8], sh[8];
+        if (shared_row) {
+#pragma unroll
+          for (int i = 0; i < 8; i += 4) {
+            const f32x4 a = *reinterpret_cast<const f32x4*>(&tab[0][c0 + i]);
+            const f32x4 b = *reinterpret_cast<const f32x4*>(&tab[1][c0 + i]);
+            const f32x4 c = *reinterpret_cast<const f32x4*>(&tab[2][c0 + i]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              w[i + e] = a[e];
+              sc[i + e] = b[e];
+              sh[i + e] = c[e];
+            }
+          }
+        } else {
+          load_table8(weight, weight_f32, c0, w);
+          load_table8(scale, tables_f32, table_row * scale_stride + c0, sc);
+          load_table8(shift, tables_f32, table_row * shift_stride + c0, sh);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float t = (v[j][i] * inv_rms) * w[i];
+          const float u = 1.0f + sc[i];
+          v[j][i] = round_bf16(t * u + sh[i]);
+          bad |= !(fabsf(v[j][i]) < INFINITY);
+        }
+        if (y != nullptr) {
+          u32x4 packed;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) packed[i] = pack_bf16x2(v[j][2 * i], v[j][2 * i + 1]);
+          *reinterpret_cast<u32x4*>(y + r * k + c0) = packed;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[j][i] = 0.f;
+      }
+      quantize_store8(v[j], lane & 15, r, sl >> 4, kp, q, s);
+    }
+    const bool any_bad = __ballot(bad) != 0;
+    if (lane == 0) finite[r] = any_bad ? 0 : 1;
+  }
 }
 
 template <int kMaxSlices, bool kVec>
@@ -392,9 +442,9 @@ VDN_API int vdn_mxfp8_prenorm_quantize(const void* x, int64_t rows, int64_t k, i
   const bool wave_ok = vec && aligned16(weight) && aligned16(scale) && aligned16(shift) &&
                        scale_stride % tab_align == 0 && shift_stride % tab_align == 0;
   if (wave_ok && slices <= 64 * 10) {
-    const dim3 grid(static_cast<unsigned>((rp + kThreads / 64 - 1) / (kThreads / 64)));
+    const dim3 grid(static_cast<unsigned>((rp + kPrenormRows - 1) / kPrenormRows));
 #define VDN_PRENORM_WAVE(S)                                                                   \
-    hipLaunchKernelGGL((prenorm_quantize_wave_kernel<S>), grid, dim3(kThreads), 0, st, xp, rows, \
+    hipLaunchKernelGGL((prenorm_quantize_rows_kernel<S>), grid, dim3(kPrenormThreads), 0, st, xp, rows, \
                        k, row_stride, weight, wf, eps, scale, scale_stride, shift,              \
                        shift_stride, tf, indices, yp, qp, sp, finite, kp, rp);
     if (slices <= 64 * 2) {
