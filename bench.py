@@ -144,13 +144,93 @@ def summarize_counters(path):
         print(f"{counter}\t{mean:.1f}\t{n}\t{kernel[:150]}")
 
 
+TRAFFIC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "gemm_block_108k_traffic.md")
+CALIBRATION_KERNEL = "neg_kernel_cuda"   # torch.neg over 2**29 bf16: 1 GiB read, 1 GiB written
+CALIBRATION_KIB = float(1 << 20)
+
+
+def _counter_rows(path, counter):
+    """[(dispatch id, kernel name, KiB)] of one counter from a rocprofv3 --pmc CSV (a dispatch
+    may span several rows; they are summed)."""
+    import csv
+    per = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] == counter:
+                d = int(r["Dispatch_Id"])
+                name, kib = per.get(d, (r["Kernel_Name"], 0.0))
+                per[d] = (name, kib + float(r["Counter_Value"]))
+    return [(d, name, kib) for d, (name, kib) in per.items()]
+
+
+def summarize_traffic(fetch_csv, write_csv):
+    """Markdown summary of the HBM traffic per MXFP8 GEMM launch from a FETCH_SIZE pass and a
+    WRITE_SIZE pass (each run with --calibrate-copy). Each counter is scaled by the factor
+    that maps its reading for the calibration kernel onto the kernel's known 1 GiB."""
+    passes = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rows = _counter_rows(path, counter)
+        # the calibration launch is the process's last negation (the block negates small
+        # tensors of its own earlier)
+        cal = max(((d, kib) for d, name, kib in rows if CALIBRATION_KERNEL in name), default=None)
+        if cal is None:
+            raise SystemExit(f"{path}: no {CALIBRATION_KERNEL} dispatch (run with --calibrate-copy)")
+        gemm = sorted((d, name, kib) for d, name, kib in rows if "mxfp8_gemm_kernel" in name)
+        passes[counter] = (CALIBRATION_KIB / cal[1], gemm)
+    fetch_factor, fetch = passes["FETCH_SIZE"]
+    write_factor, write = passes["WRITE_SIZE"]
+    if len(fetch) != len(write) or not fetch:
+        raise SystemExit("the two passes hold different GEMM launches")
+    total = 0.0
+    lines = []
+    for (d, name, fk), (_, _, wk) in zip(fetch, write):
+        nbytes = (fk * fetch_factor + wk * write_factor) * 1024
+        total += nbytes
+        tile = name[name.index("<"):name.index(">") + 1] if "<" in name else ""
+        lines.append(f"| {len(lines)} | `mxfp8_gemm_kernel{tile}` | {fk * fetch_factor / 2**20:.3f} | "
+                     f"{wk * write_factor / 2**20:.3f} | {nbytes / 1e9:.3f} |")
+    per_launch = total / len(fetch)
+    out = ["# HBM traffic per MXFP8 GEMM launch, hybrid DiT block at 108,000 tokens", "",
+           "Commands (from the repository root, on one MI355X; one block forward, no warmup):", "",
+           "    rocprofv3 --pmc FETCH_SIZE -d gpurun_out/pmc_fetch -o f --output-format csv -- "
+           "python3 bench.py --steps 1 --warmup 0 --no-cpu-baseline --calibrate-copy",
+           "    rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_write -o w --output-format csv -- "
+           "python3 bench.py --steps 1 --warmup 0 --no-cpu-baseline --calibrate-copy",
+           "    python3 bench.py --summarize-traffic gpurun_out/pmc_fetch/f_counter_collection.csv "
+           "gpurun_out/pmc_write/w_counter_collection.csv", "",
+           "Calibration: `torch.neg` over 2^29 bf16 values (1 GiB read, 1 GiB written) reads "
+           f"FETCH_SIZE x{fetch_factor:.4f} and WRITE_SIZE x{write_factor:.4f} of its true bytes; "
+           "each GEMM reading below is scaled by that factor.", "",
+           "FETCH_SIZE counts L2 misses sent to the fabric. Those served by the MALL are counted too, "
+           "so this is an upper bound on DRAM bytes.", "",
+           "| launch | kernel | read GiB | written GiB | GB |", "|---:|---|---:|---:|---:|",
+           *lines, "",
+           f"bytes_per_launch: {per_launch:.0f}"]
+    print("\n".join(out))
+
+
+def traffic_per_launch():
+    """HBM bytes per GEMM launch recorded by --summarize-traffic, or None."""
+    if not os.path.exists(TRAFFIC_SUMMARY):
+        return None
+    with open(TRAFFIC_SUMMARY) as f:
+        for line in f:
+            if line.startswith("bytes_per_launch:"):
+                return int(line.split(":")[1])
+    return None
+
+
 def main():
     p = argparse.ArgumentParser()
     p.add_argument("--summarize-counters", metavar="CSV",
                    help="print per-kernel mean counters of a rocprofv3 --pmc CSV and exit")
+    p.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                   help="print the GEMM HBM-traffic summary of a FETCH_SIZE and a WRITE_SIZE "
+                        "pass and exit")
     p.add_argument("--calibrate-copy", action="store_true",
-                   help="after the timed steps, copy one 1 GiB buffer (a known-size copy kernel "
-                        "for scaling HBM byte counters)")
+                   help="after the timed steps, negate one 1 GiB bf16 buffer into another (an "
+                        "elementwise kernel of known traffic for scaling HBM byte counters)")
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=5)
     p.add_argument("--warmup", type=int, default=2)
@@ -160,6 +240,9 @@ def main():
     args = p.parse_args()
     if args.summarize_counters:
         summarize_counters(args.summarize_counters)
+        return
+    if args.summarize_traffic:
+        summarize_traffic(*args.summarize_traffic)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the block runs whole on a single MI355X "
@@ -211,9 +294,9 @@ def main():
     if args.calibrate_copy:
         src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda")
         dst = torch.empty_like(src)
-        dst.copy_(src)
+        torch.neg(src, out=dst)
         torch.cuda.synchronize()
-        log("copied 1 GiB (calibration kernel)")
+        log("negated 1 GiB into 1 GiB (calibration kernel: 1 GiB read, 1 GiB written)")
         del src, dst
 
     per = {}
@@ -239,11 +322,7 @@ def main():
     vda_bytes = sum(per[n][3] for n in VDA_ENTRIES if n in per)
     vda_gbs = vda_bytes / (vda_t * 1e-3) / 1e9
     w = per["vdn_window_attention"]
-    traffic = None
-    traffic_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                                "gemm_block_108k_traffic.json")
-    if os.path.exists(traffic_path):
-        traffic = json.load(open(traffic_path)).get("bytes_per_launch")
+    traffic = traffic_per_launch()
 
     result = {
         "metric": METRIC, "value": round(ms, 3), "unit": "ms", "n_gpus": 1,
