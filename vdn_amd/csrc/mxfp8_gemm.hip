@@ -415,6 +415,440 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
   if (ep.nonfinite != nullptr && __ballot(bad) != 0 && lane == 0) atomicOr(ep.nonfinite, 1u);
 }
 
+// ---------------------------------------------------------------------------------------
+// Persistent 256 x 256 kernel (the large-problem path).
+//
+// One workgroup per CU walks its tiles (XCD-contiguous order as above) with one K-step
+// pipeline that runs across tile boundaries: step s of the workgroup's (tile, K step)
+// sequence lives in LDS buffer s % 2. Each step has one barrier, in the middle:
+//   head  A groups mt < kHead: 8 MFMAs each against all 8 B fragments (in registers),
+//         reading the remaining A fragments of the step;
+//   mid   wait for step s+1's tiles (DMA issued one step earlier) and barrier: every wave
+//         is then done reading buffer s % 2 and buffer (s+1) % 2 is complete;
+//   tail  A groups mt >= kHead in N order: after the MFMAs of B fragment nt, fragment nt of
+//         step s+1 is read into the same registers; step s+2's tiles are DMA'd into buffer
+//         s % 2 between the MFMA groups.
+// So the next step starts with its B fragments and first A fragment already in registers,
+// and a tile's epilogue (accumulators staged through a per-wave LDS strip, 16-byte stores)
+// runs while the next tile's first steps are in flight.
+// Tiles are fetched with buffer_load ... lds through buffer resources: rows past the padded
+// end read as zero, and the LDS DMA counts on vmcnt only, so fragment reads keep exact
+// lgkmcnt waits.
+constexpr int kPTile = 256;
+constexpr int kPScaleOff = 2 * kPTile * kBK;                 // A tile, then W tile
+constexpr int kPStep = kPScaleOff + 2 * kPTile * 4;          // + four 512-byte scale runs
+constexpr int kPStageStride = 272;                           // 128 bf16 + 16 pad bytes
+constexpr int kPStageBytes = 16 * kPStageStride;             // one wave's 16-row strip
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int64_t n = bytes < 0x7fffffffll ? bytes : 0x7fffffffll;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(n),
+                                           0x00020000);
+}
+
+// LDS DMA through a buffer resource, written as inline asm: lane l's 16 (4) bytes at
+// voffset land at LDS byte lds_base + 16 l (4 l); M0 carries lds_base. The compiler does not
+// see these as LDS writes, so it does not make every later LDS read wait for them (it
+// cannot tell the two step buffers apart); the kernel orders them itself with explicit
+// vmcnt waits before its barriers. They are issued where the compiler has no vector memory
+// access of its own in flight, so its own vmcnt counts stay conservative.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)p));
+}
+
+__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, uint32_t voffset,
+                                                uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               ::"s"(lds_base), "v"(voffset), "s"(r) : "memory");
+}
+
+__device__ __forceinline__ void buffer_to_lds4(__amdgpu_buffer_rsrc_t r, uint32_t voffset,
+                                               uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               ::"s"(lds_base), "v"(voffset), "s"(r) : "memory");
+}
+
+// Virtual tile id b (b % 8 is the XCD that runs it) -> (tile row, tile column).
+__device__ __forceinline__ void tile_coords(int b, int num_wg, int tiles_m, int tiles_n,
+                                            int group_m, int& tm, int& tn) {
+  const int xcd = b & 7, local = b >> 3;
+  const int per = num_wg >> 3, rem = num_wg & 7;
+  const int pid = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  const int in_group = group_m * tiles_n;
+  const int first_m = (pid / in_group) * group_m;
+  const int gm = min(tiles_m - first_m, group_m);
+  tm = first_m + (pid % in_group) % gm;
+  tn = (pid % in_group) / gm;
+}
+
+// Empty asm statements that take accumulators as operands: the MFMAs producing them are
+// then issued before the statement, and memory operations stay on their side of it
+// ("memory" clobber). This keeps each MFMA group between the LDS reads and the barrier
+// it is meant to overlap; without it the pure MFMA calls may be sunk past the barrier.
+__device__ __forceinline__ void pin_group(const f32x4 (&g)[8]) {
+  asm volatile("" ::"a"(g[0]), "a"(g[1]), "a"(g[2]), "a"(g[3]), "a"(g[4]), "a"(g[5]), "a"(g[6]),
+               "a"(g[7]) : "memory");
+}
+
+template <int kFirst>
+__device__ __forceinline__ void pin_column_from(const f32x4 (&acc)[8][8], int nt) {
+  if constexpr (kFirst == 4) {
+    asm volatile("" ::"a"(acc[4][nt]), "a"(acc[5][nt]), "a"(acc[6][nt]), "a"(acc[7][nt]) : "memory");
+  } else if constexpr (kFirst == 3) {
+    asm volatile("" ::"a"(acc[3][nt]), "a"(acc[4][nt]), "a"(acc[5][nt]), "a"(acc[6][nt]),
+                 "a"(acc[7][nt]) : "memory");
+  } else if constexpr (kFirst == 2) {
+    asm volatile("" ::"a"(acc[2][nt]), "a"(acc[3][nt]), "a"(acc[4][nt]), "a"(acc[5][nt]),
+                 "a"(acc[6][nt]), "a"(acc[7][nt]) : "memory");
+  } else {
+    static_assert(kFirst >= 2 && kFirst <= 4, "tail width");
+  }
+}
+
+// kProducer: the MXFP8 producer epilogue (Epilogue::q_out); otherwise bf16 output with
+// 16-byte accesses (Epilogue::vec must hold).
+template <int kHead, bool kProducer>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
+                             const uint8_t* __restrict__ W, const uint8_t* __restrict__ Ws,
+                             int64_t mp, int64_t np, int64_t kp, Epilogue ep, int64_t out_rows,
+                             int64_t n, int tiles_m, int tiles_n, int group_m) {
+  constexpr int TM = 8, TN = 8;
+  static_assert(kHead >= 1 && kHead < TM, "head groups");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kPStep + 4 * kPStageBytes];
+
+  const int num_wg = tiles_m * tiles_n;
+  const int grid = gridDim.x;
+  const int my_tiles = (num_wg - static_cast<int>(blockIdx.x) + grid - 1) / grid;
+  const int nk = static_cast<int>(kp / kBK);
+  const int total_steps = my_tiles * nk;
+  const int64_t col_tiles = kp >> 7;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // ---- DMA side: a cursor over the workgroup's (tile, K step) sequence ----
+  // Segment i of a tile (i < 8: A rows, else W rows) is rows 32 (i % 8) + 8 wave + lane / 8;
+  // lane l writes 16 bytes at LDS offset 16 l of its 1 KB slot, i.e. physical chunk l % 8,
+  // so it fetches logical chunk (l % 8) ^ ((row >> 1) & 7), the same for every segment.
+  const int seg_row = lane >> 3;
+  const uint32_t kpu = static_cast<uint32_t>(kp);
+  const uint32_t dma_voff =
+      (wave * 8 + seg_row) * kpu + ((lane & 7) ^ (((wave * 8 + seg_row) >> 1) & 7)) * 16;
+  const __amdgpu_buffer_rsrc_t as_rsrc = make_rsrc(As, mp * kp / 32);
+  const __amdgpu_buffer_rsrc_t ws_rsrc = make_rsrc(Ws, np * kp / 32);
+  int d_step = 0, d_tile = 0, d_ks = 0;
+  int64_t d_m0 = 0, d_n0 = 0;
+  __amdgpu_buffer_rsrc_t d_a, d_w;
+  auto dma_tile = [&](int j) __attribute__((always_inline)) {
+    int tm, tn;
+    tile_coords(static_cast<int>(blockIdx.x) + j * grid, num_wg, tiles_m, tiles_n, group_m, tm, tn);
+    d_m0 = static_cast<int64_t>(tm) * kPTile;
+    d_n0 = static_cast<int64_t>(tn) * kPTile;
+    d_a = make_rsrc(A + d_m0 * kp, (mp - d_m0) * kp);
+    d_w = make_rsrc(W + d_n0 * kp, (np - d_n0) * kp);
+  };
+  // Past the last step the cursor stays on it: those DMAs rewrite a buffer whose reads are
+  // finished with the same bytes, and the workgroup waits for them before it exits.
+  auto dma_advance = [&]() __attribute__((always_inline)) {
+    if (d_step + 1 < total_steps) {
+      ++d_step;
+      if (++d_ks == nk) {
+        d_ks = 0;
+        dma_tile(++d_tile);
+      }
+    }
+  };
+  auto dma_scales = [&](uint8_t* buf) __attribute__((always_inline)) {
+    // wave w loads run w: A 128-row blocks 0, 1, then W blocks 0, 1 (two 256-byte DMAs)
+    const bool is_a = wave < 2;
+    const int64_t blk = (is_a ? d_m0 : d_n0) / 128 + (wave & 1);
+    const uint32_t off = static_cast<uint32_t>((blk * col_tiles + d_ks) * 512) + lane * 4;
+    const uint32_t dst = lds_addr(buf + kPScaleOff + wave * 512);
+    buffer_to_lds4(is_a ? as_rsrc : ws_rsrc, off, dst);
+    buffer_to_lds4(is_a ? as_rsrc : ws_rsrc, off + 256, dst + 256);
+  };
+  auto dma_segment = [&](uint8_t* buf, int seg) __attribute__((always_inline)) {
+    const uint32_t off = dma_voff + static_cast<uint32_t>(d_ks) * kBK + (seg & 7) * 32 * kpu;
+    if (seg < 8)
+      buffer_to_lds16(d_a, off, lds_addr(buf + ((seg & 7) * 4 + wave) * 1024));
+    else
+      buffer_to_lds16(d_w, off, lds_addr(buf + kPTile * kBK + ((seg & 7) * 4 + wave) * 1024));
+  };
+
+  // ---- consumer side ----
+  const int frag_row = lane & 15;
+  const int c_lo = lane >> 4;
+  const int block_shift = 8 * c_lo;
+  auto frag = [&](const uint8_t* base, int row) __attribute__((always_inline)) {
+    const int sw = (row >> 1) & 7;
+    const i32x4 lo = *reinterpret_cast<const i32x4*>(base + row * kBK + ((c_lo ^ sw) << 4));
+    const i32x4 hi = *reinterpret_cast<const i32x4*>(base + row * kBK + (((c_lo + 4) ^ sw) << 4));
+    return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  };
+  // Scale words of rows 16 mt + frag_row of the wave tile: even mt in the 16 bytes at
+  // `ae`, odd mt at `ao` (SWIZZLE_32_4_4 run layout); the same for W.
+  const int sa_off = kPScaleOff + wm * 512 + frag_row * 16;
+  const int sb_off = kPScaleOff + (2 + wn) * 512 + frag_row * 16;
+  u32x4 ae, ao, be, bo;
+  auto read_scales = [&](const uint8_t* buf) __attribute__((always_inline)) {
+    ae = *reinterpret_cast<const u32x4*>(buf + sa_off);
+    ao = *reinterpret_cast<const u32x4*>(buf + sa_off + 256);
+    be = *reinterpret_cast<const u32x4*>(buf + sb_off);
+    bo = *reinterpret_cast<const u32x4*>(buf + sb_off + 256);
+  };
+  uint32_t sa[TM], sb[TN];
+  auto unpack_scales = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sa[2 * i] = ae[i] >> block_shift;
+      sa[2 * i + 1] = ao[i] >> block_shift;
+      sb[2 * i] = be[i] >> block_shift;
+      sb[2 * i + 1] = bo[i] >> block_shift;
+    }
+  };
+
+  f32x4 acc[TM][TN];
+
+  // ---- epilogue of one tile: per wave, 16 rows at a time through its LDS strip ----
+  uint8_t* stage = lds + 2 * kPStep + wave * kPStageBytes;
+  bool bad = false;
+  auto epilogue = [&](int64_t m0, int64_t n0) __attribute__((always_inline)) {
+    const int chunk = lane & 15;                       // 8 columns of the wave's 128
+    const int64_t col = n0 + wn * 128 + chunk * 8;
+    // bias and gate of the lane's 8 columns as bf16 pairs (unpacked where used)
+    u32x4 bias_w = {0u, 0u, 0u, 0u}, gate_w = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    if (ep.vec && col + 8 <= n) {
+      if (ep.bias != nullptr) bias_w = *reinterpret_cast<const u32x4*>(ep.bias + col);
+      if (ep.gate != nullptr) gate_w = *reinterpret_cast<const u32x4*>(ep.gate + col);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bool in = col + e < n;
+        const uint32_t bb = ep.bias != nullptr && in ? ep.bias[col + e] : 0u;
+        const uint32_t gg = ep.gate != nullptr && in ? ep.gate[col + e] : 0x3f80u;
+        bias_w[e / 2] |= bb << (16 * (e & 1));
+        gate_w[e / 2] = (gate_w[e / 2] & ~(0xffffu << (16 * (e & 1)))) | (gg << (16 * (e & 1)));
+      }
+    }
+    auto word_elem = [](const u32x4& w, int e) __attribute__((always_inline)) {
+      return bf16_bits_to_f32(static_cast<uint16_t>(w[e / 2] >> (16 * (e & 1))));
+    };
+    const int64_t chunk128 = (n0 + wn * 128) >> 7;
+    // A rolled loop over the 8 row groups keeps one copy of the store code; the
+    // accumulators (registers) are picked by a uniform branch chain, not indexed.
+#pragma nounroll
+    for (int mt = 0; mt < TM; ++mt) {
+      // lane l holds columns nt * 16 + 4 (l / 16) .. +3 of strip row l % 16
+#pragma unroll
+      for (int m = 0; m < TM; ++m) {
+        if (m != mt) continue;
+#pragma unroll
+        for (int nt = 0; nt < TN; ++nt) {
+          u32x2 packed;
+          packed[0] = pack_bf16x2(round_bf16(acc[m][nt][0]), round_bf16(acc[m][nt][1]));
+          packed[1] = pack_bf16x2(round_bf16(acc[m][nt][2]), round_bf16(acc[m][nt][3]));
+          *reinterpret_cast<u32x2*>(stage + frag_row * kPStageStride + nt * 32 + c_lo * 8) = packed;
+        }
+      }
+      const int64_t row0 = m0 + wm * 128 + mt * 16 + c_lo;   // + 4 pass
+      u32x4 yv[4];
+#pragma unroll
+      for (int pass = 0; pass < 4; ++pass)
+        yv[pass] = *reinterpret_cast<const u32x4*>(stage + (pass * 4 + c_lo) * kPStageStride +
+                                                   chunk * 16);
+      if constexpr (kProducer) {
+        // the 16 lanes of a row hold its 128-column chunk in order: quantize_store8's layout
+        const bool chunk_in = chunk128 < (ep.kp_out >> 7);
+#pragma unroll
+        for (int pass = 0; pass < 4; ++pass) {
+          const int64_t row = row0 + pass * 4;
+          if (row >= mp || !chunk_in) continue;
+          float y[8];
+          unpack8(yv[pass], y);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float v = 0.f;
+            if (row < out_rows && col + e < n) {
+              v = ep.bias != nullptr ? round_bf16(y[e] + word_elem(bias_w, e)) : y[e];
+              if (ep.act == 1) v = round_bf16(gelu_tanh(v));
+              bad = bad || !(fabsf(v) < INFINITY);
+            }
+            y[e] = v;
+          }
+          quantize_store8(y, chunk, row, chunk128, ep.kp_out, ep.q_out, ep.s_out);
+        }
+      } else if (col < n) {
+        // two rows per batch: both rows' addend/residual loads are issued before either
+        // row's arithmetic
+#pragma unroll
+        for (int p0 = 0; p0 < 4; p0 += 2) {
+          u32x4 av[2], rv[2];
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int64_t row = row0 + (p0 + j) * 4;
+            if (row < out_rows) {
+              if (ep.addend != nullptr)
+                av[j] = *reinterpret_cast<const u32x4*>(ep.addend + row * ep.ld_add + col);
+              if (ep.residual != nullptr)
+                rv[j] = *reinterpret_cast<const u32x4*>(ep.residual + row * ep.ld_res + col);
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int64_t row = row0 + (p0 + j) * 4;
+            if (row >= out_rows) continue;
+            u32x4 packed;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+              float yy[2];
+#pragma unroll
+              for (int h = 0; h < 2; ++h) {
+                const float a = ep.addend != nullptr ? word_elem(av[j], e + h) : 0.f;
+                const float rs = ep.residual != nullptr ? word_elem(rv[j], e + h) : 0.f;
+                yy[h] = epilogue_value(word_elem(yv[p0 + j], e + h), word_elem(bias_w, e + h), a,
+                                       rs, word_elem(gate_w, e + h), ep);
+              }
+              bad = bad || !(fabsf(yy[0]) < INFINITY) || !(fabsf(yy[1]) < INFINITY);
+              packed[e / 2] = pack_bf16x2(yy[0], yy[1]);
+            }
+            *reinterpret_cast<u32x4*>(ep.out + row * ep.ldc + col) = packed;
+          }
+        }
+      }
+    }
+  };
+
+  // ---- prologue: steps 0 and 1 in flight, step 0's fragments in registers ----
+  dma_tile(0);
+  dma_scales(lds);
+#pragma unroll
+  for (int seg = 0; seg < 16; ++seg) dma_segment(lds, seg);
+  dma_advance();
+  dma_scales(lds + kPStep);
+#pragma unroll
+  for (int seg = 0; seg < 16; ++seg) dma_segment(lds + kPStep, seg);
+  dma_advance();
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  i32x8 bfrag[TN];
+  i32x8 a0;
+  // Fragments and scales of the step in buffer `buf`, read at a tile's start.
+  auto load_fragments = [&](const uint8_t* buf) __attribute__((always_inline)) {
+    read_scales(buf);
+    unpack_scales();
+#pragma unroll
+    for (int nt = 0; nt < TN; ++nt) bfrag[nt] = frag(buf + kPTile * kBK, wn * 128 + nt * 16 + frag_row);
+    a0 = frag(buf, wm * 128 + frag_row);
+  };
+
+  // The K steps of all the workgroup's tiles as one sequence: the tail of the last step of a
+  // tile already reads the next tile's first fragments, but those are read again after the
+  // epilogue (load_fragments), so no fragment register is live across the epilogue.
+  int s = 0;
+  for (int c_tile = 0; c_tile < my_tiles; ++c_tile) {
+    load_fragments(lds + (s & 1) * kPStep);
+#pragma unroll
+    for (int mt = 0; mt < TM; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < TN; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < nk; ++ks, ++s) {
+      uint8_t* cur = lds + (s & 1) * kPStep;
+      uint8_t* nxt = lds + ((s & 1) ^ 1) * kPStep;
+      // head: A groups 0 .. kHead-1, each against all B fragments; the A fragments of the
+      // tail groups are read with the last head group
+      i32x8 af[TM];
+      af[0] = a0;
+#pragma unroll
+      for (int mt = 0; mt < kHead; ++mt) {
+        if (mt + 1 < kHead) {
+          af[mt + 1] = frag(cur, wm * 128 + (mt + 1) * 16 + frag_row);
+        } else {
+#pragma unroll
+          for (int t = kHead; t < TM; ++t) af[t] = frag(cur, wm * 128 + t * 16 + frag_row);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int nt = 0; nt < TN; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              bfrag[nt], af[mt], acc[mt][nt], 0, 0, 0, static_cast<int>(sb[nt]), 0,
+              static_cast<int>(sa[mt]));
+        pin_group(acc[mt]);
+      }
+      // mid: step s+1's tiles have landed (its DMAs went out during step s-1) and every
+      // wave is done reading this step's buffer
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      dma_scales(cur);
+      a0 = frag(nxt, wm * 128 + frag_row);
+      // tail: A groups kHead .. 7 in N order; B fragment nt of step s+1 replaces fragment
+      // nt after its last MFMA here; step s+2's segments go out two per N column
+#pragma unroll
+      for (int nt = 0; nt < TN; ++nt) {
+        // step s+1's scale words are read late: the current ones are mostly dead by then
+        if (nt == TN - 2) read_scales(nxt);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int mt = kHead; mt < TM; ++mt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              bfrag[nt], af[mt], acc[mt][nt], 0, 0, 0, static_cast<int>(sb[nt]), 0,
+              static_cast<int>(sa[mt]));
+        pin_column_from<kHead>(acc, nt);
+        bfrag[nt] = frag(nxt + kPTile * kBK, wn * 128 + nt * 16 + frag_row);
+        dma_segment(cur, 2 * nt);
+        dma_segment(cur, 2 * nt + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      dma_advance();
+      unpack_scales();
+    }
+    int tm, tn;
+    tile_coords(static_cast<int>(blockIdx.x) + c_tile * grid, num_wg, tiles_m, tiles_n, group_m,
+                tm, tn);
+    epilogue(static_cast<int64_t>(tm) * kPTile, static_cast<int64_t>(tn) * kPTile);
+  }
+  // the DMAs issued past the last step must land before the workgroup's LDS is released
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (ep.nonfinite != nullptr && __ballot(bad) != 0 && lane == 0) atomicOr(ep.nonfinite, 1u);
+}
+
+#ifndef VDN_GEMM_HEAD
+#define VDN_GEMM_HEAD 4
+#endif
+
+int cu_count() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  if (dev >= 0 && dev < 64 && cached[dev] > 0) return cached[dev];
+  int cu = 0;
+  if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cu <= 0)
+    cu = 256;
+  if (dev >= 0 && dev < 64) cached[dev] = cu;
+  return cu;
+}
+
+int launch_persistent(const uint8_t* a, const uint8_t* as, int64_t mp, const uint8_t* w,
+                      const uint8_t* ws, int64_t np, int64_t kp, const Epilogue& ep,
+                      int64_t out_rows, int64_t n, hipStream_t stream) {
+  const int64_t tiles_m = (mp + kPTile - 1) / kPTile, tiles_n = (np + kPTile - 1) / kPTile;
+  if (tiles_m * tiles_n > (1ll << 31) - 1 || static_cast<int64_t>(kPTile) * kp >= (1ll << 31) ||
+      mp * kp / 32 >= (1ll << 31) || np * kp / 32 >= (1ll << 31))
+    return set_error(kUnsupported, "vdn_mxfp8_gemm: problem too large for 32-bit tile offsets");
+  const int64_t tiles = tiles_m * tiles_n;
+  const int grid = static_cast<int>(tiles < cu_count() ? tiles : cu_count());
+  if (ep.q_out != nullptr)
+    hipLaunchKernelGGL((mxfp8_gemm_persistent_kernel<VDN_GEMM_HEAD, true>), dim3(grid), dim3(256),
+                       0, stream, a, as, w, ws, mp, np, kp, ep, out_rows, n,
+                       static_cast<int>(tiles_m), static_cast<int>(tiles_n), 8);
+  else
+    hipLaunchKernelGGL((mxfp8_gemm_persistent_kernel<VDN_GEMM_HEAD, false>), dim3(grid), dim3(256),
+                       0, stream, a, as, w, ws, mp, np, kp, ep, out_rows, n,
+                       static_cast<int>(tiles_m), static_cast<int>(tiles_n), 8);
+  return check_launch("vdn_mxfp8_gemm");
+}
+
 template <int BM, int BN, int WGM, int WGN>
 int launch_gemm(const uint8_t* a, const uint8_t* as, int64_t mp, const uint8_t* w,
                 const uint8_t* ws, int64_t np, int64_t kp, const Epilogue& ep, int64_t out_rows,
@@ -476,8 +910,10 @@ VDN_API int vdn_mxfp8_gemm(const void* a, const void* a_scales, int64_t mp, cons
                     ld_add, static_cast<const uint16_t*>(residual), ld_res,
                     static_cast<const uint16_t*>(gate), static_cast<uint16_t*>(out), ldc,
                     nonfinite, vec ? 1 : 0, nullptr, nullptr, 0, 0};
-  if (mp >= 1024 && np >= 1024)
+  if (mp >= 1024 && np >= 1024) {
+    if (vec) return launch_persistent(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
     return launch_gemm<256, 256, 2, 2>(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
+  }
   return launch_gemm<128, 128, 2, 2>(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
 }
 
@@ -519,6 +955,6 @@ VDN_API int vdn_mxfp8_gemm_act_quantize(const void* a, const void* a_scales, int
   auto* wp = static_cast<const uint8_t*>(w);
   auto* wsp = static_cast<const uint8_t*>(w_scales);
   if (mp >= 1024 && np >= 1024)
-    return launch_gemm<256, 256, 2, 2>(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
+    return launch_persistent(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
   return launch_gemm<128, 128, 2, 2>(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
 }
