@@ -431,9 +431,8 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
 // So the next step starts with its B fragments and first A fragment already in registers,
 // and a tile's epilogue (accumulators staged through a per-wave LDS strip, 16-byte stores)
 // runs while the next tile's first steps are in flight.
-// Tiles are fetched with buffer_load ... lds through buffer resources: rows past the padded
-// end read as zero, and the LDS DMA counts on vmcnt only, so fragment reads keep exact
-// lgkmcnt waits.
+// Tiles are fetched with buffer_load ... lds through buffer resources (rows past the padded
+// end read as zero) issued from inline asm (see buffer_to_lds16).
 constexpr int kPTile = 256;
 constexpr int kPScaleOff = 2 * kPTile * kBK;                 // A tile, then W tile
 constexpr int kPStep = kPScaleOff + 2 * kPTile * 4;          // + four 512-byte scale runs
@@ -492,22 +491,14 @@ __device__ __forceinline__ void pin_group(const f32x4 (&g)[8]) {
 
 template <int kFirst>
 __device__ __forceinline__ void pin_column_from(const f32x4 (&acc)[8][8], int nt) {
-  if constexpr (kFirst == 4) {
-    asm volatile("" ::"a"(acc[4][nt]), "a"(acc[5][nt]), "a"(acc[6][nt]), "a"(acc[7][nt]) : "memory");
-  } else if constexpr (kFirst == 3) {
-    asm volatile("" ::"a"(acc[3][nt]), "a"(acc[4][nt]), "a"(acc[5][nt]), "a"(acc[6][nt]),
-                 "a"(acc[7][nt]) : "memory");
-  } else if constexpr (kFirst == 2) {
-    asm volatile("" ::"a"(acc[2][nt]), "a"(acc[3][nt]), "a"(acc[4][nt]), "a"(acc[5][nt]),
-                 "a"(acc[6][nt]), "a"(acc[7][nt]) : "memory");
-  } else {
-    static_assert(kFirst >= 2 && kFirst <= 4, "tail width");
-  }
+#pragma unroll
+  for (int mt = kFirst; mt < 8; ++mt) asm volatile("" ::"a"(acc[mt][nt]) : "memory");
 }
 
-// kProducer: the MXFP8 producer epilogue (Epilogue::q_out); otherwise bf16 output with
-// 16-byte accesses (Epilogue::vec must hold).
-template <int kHead, bool kProducer>
+// kMode: 0 bf16 output, 1 bf16 output with a residual (Epilogue::residual, prefetched one
+// row group ahead), 2 the MXFP8 producer epilogue (Epilogue::q_out). The bf16 modes need
+// 16-byte accesses (Epilogue::vec) and no addend.
+template <int kHead, int kMode>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
                              const uint8_t* __restrict__ W, const uint8_t* __restrict__ Ws,
@@ -617,48 +608,73 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
   auto epilogue = [&](int64_t m0, int64_t n0) __attribute__((always_inline)) {
     const int chunk = lane & 15;                       // 8 columns of the wave's 128
     const int64_t col = n0 + wn * 128 + chunk * 8;
-    // bias and gate of the lane's 8 columns as bf16 pairs (unpacked where used)
-    u32x4 bias_w = {0u, 0u, 0u, 0u}, gate_w = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    // Bias and gate of the lane's 8 columns. A missing bias is -0 and a missing gate 1:
+    // bf16(y + -0) = y and bf16(1 * y) = y exactly, so the arithmetic below needs no
+    // per-element tests.
+    float bias8[8], gate8[8];
     if (ep.vec && col + 8 <= n) {
-      if (ep.bias != nullptr) bias_w = *reinterpret_cast<const u32x4*>(ep.bias + col);
-      if (ep.gate != nullptr) gate_w = *reinterpret_cast<const u32x4*>(ep.gate + col);
+      u32x4 bw = {0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+      u32x4 gw = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+      if (ep.bias != nullptr) bw = *reinterpret_cast<const u32x4*>(ep.bias + col);
+      if (ep.gate != nullptr) gw = *reinterpret_cast<const u32x4*>(ep.gate + col);
+      unpack8(bw, bias8);
+      unpack8(gw, gate8);
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const bool in = col + e < n;
-        const uint32_t bb = ep.bias != nullptr && in ? ep.bias[col + e] : 0u;
-        const uint32_t gg = ep.gate != nullptr && in ? ep.gate[col + e] : 0x3f80u;
-        bias_w[e / 2] |= bb << (16 * (e & 1));
-        gate_w[e / 2] = (gate_w[e / 2] & ~(0xffffu << (16 * (e & 1)))) | (gg << (16 * (e & 1)));
+        bias8[e] = ep.bias != nullptr && in ? bf16_bits_to_f32(ep.bias[col + e]) : -0.f;
+        gate8[e] = ep.gate != nullptr && in ? bf16_bits_to_f32(ep.gate[col + e]) : 1.f;
       }
     }
-    auto word_elem = [](const u32x4& w, int e) __attribute__((always_inline)) {
-      return bf16_bits_to_f32(static_cast<uint16_t>(w[e / 2] >> (16 * (e & 1))));
-    };
     const int64_t chunk128 = (n0 + wn * 128) >> 7;
+    // The residual rows of row group mt+1 are loaded while group mt is finished, so their
+    // latency is paid once per tile rather than once per group.
+    const int64_t rows0 = m0 + wm * 128 + c_lo;   // + 16 mt + 4 pass
+    u32x4 res_next[4];
+    auto load_residual = [&](int mt, u32x4 (&r)[4]) __attribute__((always_inline)) {
+      if (col >= n) return;
+#pragma unroll
+      for (int pass = 0; pass < 4; ++pass) {
+        const int64_t row = rows0 + mt * 16 + pass * 4;
+        if (row < out_rows)
+          r[pass] = *reinterpret_cast<const u32x4*>(ep.residual + row * ep.ld_res + col);
+      }
+    };
+    if constexpr (kMode == 1) load_residual(0, res_next);
     // A rolled loop over the 8 row groups keeps one copy of the store code; the
     // accumulators (registers) are picked by a uniform branch chain, not indexed.
 #pragma nounroll
     for (int mt = 0; mt < TM; ++mt) {
+      u32x4 res_cur[4];
+      if constexpr (kMode == 1) {
+#pragma unroll
+        for (int pass = 0; pass < 4; ++pass) res_cur[pass] = res_next[pass];
+        if (mt + 1 < TM) load_residual(mt + 1, res_next);
+      }
       // lane l holds columns nt * 16 + 4 (l / 16) .. +3 of strip row l % 16
 #pragma unroll
       for (int m = 0; m < TM; ++m) {
         if (m != mt) continue;
 #pragma unroll
         for (int nt = 0; nt < TN; ++nt) {
+          f32x4 v = acc[m][nt];
+          // the copy is opaque: the rounding below stays in this branch instead of being
+          // hoisted (for all 256 accumulators at once) out of the loop
+          asm volatile("" : "+v"(v));
           u32x2 packed;
-          packed[0] = pack_bf16x2(round_bf16(acc[m][nt][0]), round_bf16(acc[m][nt][1]));
-          packed[1] = pack_bf16x2(round_bf16(acc[m][nt][2]), round_bf16(acc[m][nt][3]));
+          packed[0] = pack_bf16x2(round_bf16(v[0]), round_bf16(v[1]));
+          packed[1] = pack_bf16x2(round_bf16(v[2]), round_bf16(v[3]));
           *reinterpret_cast<u32x2*>(stage + frag_row * kPStageStride + nt * 32 + c_lo * 8) = packed;
         }
       }
-      const int64_t row0 = m0 + wm * 128 + mt * 16 + c_lo;   // + 4 pass
+      const int64_t row0 = rows0 + mt * 16;   // + 4 pass
       u32x4 yv[4];
 #pragma unroll
       for (int pass = 0; pass < 4; ++pass)
         yv[pass] = *reinterpret_cast<const u32x4*>(stage + (pass * 4 + c_lo) * kPStageStride +
                                                    chunk * 16);
-      if constexpr (kProducer) {
+      if constexpr (kMode == 2) {
         // the 16 lanes of a row hold its 128-column chunk in order: quantize_store8's layout
         const bool chunk_in = chunk128 < (ep.kp_out >> 7);
 #pragma unroll
@@ -671,7 +687,7 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
           for (int e = 0; e < 8; ++e) {
             float v = 0.f;
             if (row < out_rows && col + e < n) {
-              v = ep.bias != nullptr ? round_bf16(y[e] + word_elem(bias_w, e)) : y[e];
+              v = round_bf16(y[e] + bias8[e]);
               if (ep.act == 1) v = round_bf16(gelu_tanh(v));
               bad = bad || !(fabsf(v) < INFINITY);
             }
@@ -680,41 +696,28 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
           quantize_store8(y, chunk, row, chunk128, ep.kp_out, ep.q_out, ep.s_out);
         }
       } else if (col < n) {
-        // two rows per batch: both rows' addend/residual loads are issued before either
-        // row's arithmetic
 #pragma unroll
-        for (int p0 = 0; p0 < 4; p0 += 2) {
-          u32x4 av[2], rv[2];
+        for (int pass = 0; pass < 4; ++pass) {
+          const int64_t row = row0 + pass * 4;
+          if (row >= out_rows) continue;
+          float y[8];
+          unpack8(yv[pass], y);
+          float r[8];
+          if constexpr (kMode == 1) unpack8(res_cur[pass], r);
+          u32x4 packed;
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const int64_t row = row0 + (p0 + j) * 4;
-            if (row < out_rows) {
-              if (ep.addend != nullptr)
-                av[j] = *reinterpret_cast<const u32x4*>(ep.addend + row * ep.ld_add + col);
-              if (ep.residual != nullptr)
-                rv[j] = *reinterpret_cast<const u32x4*>(ep.residual + row * ep.ld_res + col);
+          for (int e = 0; e < 8; e += 2) {
+            float yy[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              float v = round_bf16(y[e + h] + bias8[e + h]);
+              if constexpr (kMode == 1) v = round_bf16(r[e + h] + round_bf16(gate8[e + h] * v));
+              yy[h] = v;
             }
+            bad = bad || !(fabsf(yy[0]) < INFINITY) || !(fabsf(yy[1]) < INFINITY);
+            packed[e / 2] = pack_bf16x2(yy[0], yy[1]);
           }
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const int64_t row = row0 + (p0 + j) * 4;
-            if (row >= out_rows) continue;
-            u32x4 packed;
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-              float yy[2];
-#pragma unroll
-              for (int h = 0; h < 2; ++h) {
-                const float a = ep.addend != nullptr ? word_elem(av[j], e + h) : 0.f;
-                const float rs = ep.residual != nullptr ? word_elem(rv[j], e + h) : 0.f;
-                yy[h] = epilogue_value(word_elem(yv[p0 + j], e + h), word_elem(bias_w, e + h), a,
-                                       rs, word_elem(gate_w, e + h), ep);
-              }
-              bad = bad || !(fabsf(yy[0]) < INFINITY) || !(fabsf(yy[1]) < INFINITY);
-              packed[e / 2] = pack_bf16x2(yy[0], yy[1]);
-            }
-            *reinterpret_cast<u32x4*>(ep.out + row * ep.ldc + col) = packed;
-          }
+          *reinterpret_cast<u32x4*>(ep.out + row * ep.ldc + col) = packed;
         }
       }
     }
@@ -838,14 +841,16 @@ int launch_persistent(const uint8_t* a, const uint8_t* as, int64_t mp, const uin
     return set_error(kUnsupported, "vdn_mxfp8_gemm: problem too large for 32-bit tile offsets");
   const int64_t tiles = tiles_m * tiles_n;
   const int grid = static_cast<int>(tiles < cu_count() ? tiles : cu_count());
+  const int tm = static_cast<int>(tiles_m), tn = static_cast<int>(tiles_n);
   if (ep.q_out != nullptr)
-    hipLaunchKernelGGL((mxfp8_gemm_persistent_kernel<VDN_GEMM_HEAD, true>), dim3(grid), dim3(256),
-                       0, stream, a, as, w, ws, mp, np, kp, ep, out_rows, n,
-                       static_cast<int>(tiles_m), static_cast<int>(tiles_n), 8);
+    hipLaunchKernelGGL((mxfp8_gemm_persistent_kernel<VDN_GEMM_HEAD, 2>), dim3(grid), dim3(256),
+                       0, stream, a, as, w, ws, mp, np, kp, ep, out_rows, n, tm, tn, 8);
+  else if (ep.residual != nullptr)
+    hipLaunchKernelGGL((mxfp8_gemm_persistent_kernel<VDN_GEMM_HEAD, 1>), dim3(grid), dim3(256),
+                       0, stream, a, as, w, ws, mp, np, kp, ep, out_rows, n, tm, tn, 8);
   else
-    hipLaunchKernelGGL((mxfp8_gemm_persistent_kernel<VDN_GEMM_HEAD, false>), dim3(grid), dim3(256),
-                       0, stream, a, as, w, ws, mp, np, kp, ep, out_rows, n,
-                       static_cast<int>(tiles_m), static_cast<int>(tiles_n), 8);
+    hipLaunchKernelGGL((mxfp8_gemm_persistent_kernel<VDN_GEMM_HEAD, 0>), dim3(grid), dim3(256),
+                       0, stream, a, as, w, ws, mp, np, kp, ep, out_rows, n, tm, tn, 8);
   return check_launch("vdn_mxfp8_gemm");
 }
 
@@ -911,7 +916,8 @@ VDN_API int vdn_mxfp8_gemm(const void* a, const void* a_scales, int64_t mp, cons
                     static_cast<const uint16_t*>(gate), static_cast<uint16_t*>(out), ldc,
                     nonfinite, vec ? 1 : 0, nullptr, nullptr, 0, 0};
   if (mp >= 1024 && np >= 1024) {
-    if (vec) return launch_persistent(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
+    if (vec && addend == nullptr)
+      return launch_persistent(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
     return launch_gemm<256, 256, 2, 2>(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
   }
   return launch_gemm<128, 128, 2, 2>(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
