@@ -44,15 +44,21 @@ __device__ __forceinline__ u32x2 e4m3x8(const float* v) {
 }
 
 
-// torch's GELU(approximate='tanh') evaluated in fp32, one rounding per operation.
+// torch's GELU(approximate='tanh') in fp32, rounded to bf16 by the caller:
+//   0.5 x (1 + tanh(u)) = x / (1 + exp(-2u)),  u = sqrt(2/pi) (x + 0.044715 x^3).
+// The second form (1 + tanh(u) = 2 sigmoid(2u)) has no cancellation in the negative tail
+// and costs one hardware exp2 and one reciprocal instead of a libm tanh. Its fp32 result
+// is within a few ulp of the first, so the bf16 value agrees except where the exact value
+// lies within those few ulp of a bf16 rounding boundary.
 #pragma clang fp contract(off)
 __device__ __forceinline__ float gelu_tanh(float x) {
-  // torch's approximate="tanh" GELU, evaluated in fp32 and rounded once by the caller.
-  const float kBeta = 0.7978845608028654f;  // sqrt(2/pi)
+  const float kBeta = 0.7978845608028654f;        // sqrt(2/pi)
   const float kKappa = 0.044715f;
+  const float kMinus2Log2e = -2.8853900817779268f;  // -2 / ln 2
   const float cube = x * x * x;
   const float inner = kBeta * (x + kKappa * cube);
-  return 0.5f * x * (1.f + tanhf(inner));
+  const float e = __builtin_amdgcn_exp2f(inner * kMinus2Log2e);   // exp(-2u)
+  return x * __builtin_amdgcn_rcpf(1.f + e);
 }
 #pragma clang fp contract(on)
 
