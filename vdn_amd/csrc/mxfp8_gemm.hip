@@ -605,6 +605,7 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
   // ---- epilogue of one tile: per wave, 16 rows at a time through its LDS strip ----
   uint8_t* stage = lds + 2 * kPStep + wave * kPStageBytes;
   bool bad = false;
+  u16x2 mag_max = {0, 0};   // bf16 output modes: largest magnitude bit pattern stored
   auto epilogue = [&](int64_t m0, int64_t n0) __attribute__((always_inline)) {
     const int chunk = lane & 15;                       // 8 columns of the wave's 128
     const int64_t col = n0 + wn * 128 + chunk * 8;
@@ -662,9 +663,9 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
           // the copy is opaque: the rounding below stays in this branch instead of being
           // hoisted (for all 256 accumulators at once) out of the loop
           asm volatile("" : "+v"(v));
-          u32x2 packed;
-          packed[0] = pack_bf16x2(round_bf16(v[0]), round_bf16(v[1]));
-          packed[1] = pack_bf16x2(round_bf16(v[2]), round_bf16(v[3]));
+          u32x2 packed;   // RNE to bf16 in the conversion itself
+          packed[0] = pack_bf16x2(v[0], v[1]);
+          packed[1] = pack_bf16x2(v[2], v[3]);
           *reinterpret_cast<u32x2*>(stage + frag_row * kPStageStride + nt * 32 + c_lo * 8) = packed;
         }
       }
@@ -707,17 +708,23 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
           u32x4 packed;
 #pragma unroll
           for (int e = 0; e < 8; e += 2) {
+            // the last rounding of each value is the one of the packing conversion
             float yy[2];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-              float v = round_bf16(y[e + h] + bias8[e + h]);
-              if constexpr (kMode == 1) v = round_bf16(r[e + h] + round_bf16(gate8[e + h] * v));
+              float v = y[e + h] + bias8[e + h];
+              if constexpr (kMode == 1) v = r[e + h] + round_bf16(gate8[e + h] * round_bf16(v));
               yy[h] = v;
             }
-            bad = bad || !(fabsf(yy[0]) < INFINITY) || !(fabsf(yy[1]) < INFINITY);
             packed[e / 2] = pack_bf16x2(yy[0], yy[1]);
           }
           *reinterpret_cast<u32x4*>(ep.out + row * ep.ldc + col) = packed;
+          // nonfinite outputs: bf16 exponent all ones, tested on the packed words with a
+          // running 16-bit max of the magnitudes (checked once at the end)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            mag_max = __builtin_elementwise_max(
+                mag_max, __builtin_bit_cast(u16x2, packed[i] & 0x7fff7fffu));
         }
       }
     }
@@ -813,6 +820,7 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
   }
   // the DMAs issued past the last step must land before the workgroup's LDS is released
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  bad = bad || mag_max[0] >= 0x7f80 || mag_max[1] >= 0x7f80;
   if (ep.nonfinite != nullptr && __ballot(bad) != 0 && lane == 0) atomicOr(ep.nonfinite, 1u);
 }
 
