@@ -14,7 +14,7 @@
 //                         exactly the B-operand K layout of the 16-key MFMA (slots 0-3 = keys
 //                         4g.., 4-7 = keys 8+4g..; measured), so P never leaves registers;
 //                         Vᵀ fragments come from the token-major V tile via ds_read_tr16_b64.
-// K/V tiles stream global -> LDS with global_load_lds_dwordx4, double-buffered; 16-byte
+// K/V tiles stream global -> LDS with buffer_load_dwordx4 ... lds, double-buffered; 16-byte
 // chunk c of tile row r is stored at c ^ (r & 15) (K: row reads) or c ^ 2 (r & 7) (V: the
 // 4-row transpose reads), which keeps both read patterns free of bank conflicts.
 #include "common.h"
@@ -39,8 +39,17 @@ typedef const __attribute__((address_space(1))) void global_void_t;
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
 
-__device__ __forceinline__ void load_to_lds16(const void* src, void* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)lds_wave_base, 16, 0, 0);
+// Tile rows go global -> LDS through a buffer resource (buffer_load_dwordx4 ... lds): lane l's
+// 16 bytes at voffset + soffset land at lds_wave_base + 16 l. Unlike the flat/global form,
+// the compiler counts these on vmcnt only, so the fragment reads of the current tile keep
+// exact lgkmcnt waits instead of waiting for every outstanding LDS read before each MFMA.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
+__device__ __forceinline__ void load_to_lds16(__amdgpu_buffer_rsrc_t r, uint32_t voffset,
+                                              uint32_t soffset, void* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds_wave_base, 16, voffset, soffset, 0, 0);
 }
 
 __device__ __forceinline__ bf16x4_t lds_read_tr(const uint16_t* p) {
@@ -123,15 +132,17 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
   }
   const char* k_head = reinterpret_cast<const char*>(in.k + h * in.k_sh);
   const char* v_head = reinterpret_cast<const char*>(in.v + h * in.v_sh);
+  // Buffer resources based at the tile's first key row (wave-uniform); the per-lane offsets
+  // stay below 128 rows x stride (the host bounds the strides).
   auto issue_tile = [&](int a, int b, uint16_t* dk, uint16_t* dv) __attribute__((always_inline)) {
-    const char* kb = k_head + static_cast<int64_t>(a) * in.k_st * 2;
-    const char* vb = v_head + static_cast<int64_t>(a) * in.v_st * 2;
+    const __amdgpu_buffer_rsrc_t k_rsrc = tile_rsrc(k_head + static_cast<int64_t>(a) * in.k_st * 2);
+    const __amdgpu_buffer_rsrc_t v_rsrc = tile_rsrc(v_head + static_cast<int64_t>(a) * in.v_st * 2);
     if (b - a == kBN) {
 #pragma unroll
       for (int j = 0; j < kSegs; ++j) {
         const int seg = j * kWaves + wave;
-        load_to_lds16(kb + koff[j], dk + seg * 4 * kD);
-        load_to_lds16(vb + voff[j], dv + seg * 4 * kD);
+        load_to_lds16(k_rsrc, koff[j], 0, dk + seg * 4 * kD);
+        load_to_lds16(v_rsrc, voff[j], 0, dv + seg * 4 * kD);
       }
     } else {  // tail tile: rows past the interval end repeat its last key
 #pragma unroll
@@ -141,8 +152,8 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
         const int r = min(row, b - a - 1);
         const uint32_t ko = static_cast<uint32_t>(r * in.k_st * 2 + 16 * (phys ^ swz_k(row)));
         const uint32_t vo = static_cast<uint32_t>(r * in.v_st * 2 + 16 * (phys ^ swz_v(row)));
-        load_to_lds16(kb + ko, dk + seg * 4 * kD);
-        load_to_lds16(vb + vo, dv + seg * 4 * kD);
+        load_to_lds16(k_rsrc, ko, 0, dk + seg * 4 * kD);
+        load_to_lds16(v_rsrc, vo, 0, dv + seg * 4 * kD);
       }
     }
   };
@@ -340,8 +351,8 @@ VDN_API int vdn_window_attention(const void* q, int64_t q_st, int64_t q_sh, cons
       q_sh % 8 || k_st % 8 || k_sh % 8 || v_st % 8 || v_sh % 8 || o_st % 8 || o_sh % 8)
     return set_error(kInvalidArgument, "%s: rows need 16-byte alignment", name);
   if (!(scale > 0.f) || !isfinite(scale)) return set_error(kInvalidArgument, "%s: bad scale", name);
-  if (k_st <= 0 || v_st <= 0 || k_st > (1 << 24) || v_st > (1 << 24))
-    return set_error(kUnsupported, "%s: K/V token strides must be in (0, 2^24] elements", name);
+  if (k_st <= 0 || v_st <= 0 || k_st > (1 << 22) || v_st > (1 << 22))
+    return set_error(kUnsupported, "%s: K/V token strides must be in (0, 2^22] elements", name);
   if (nblocks == 0) return kOk;
   const Layout in{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                   static_cast<const uint16_t*>(v), q_st, q_sh, k_st, k_sh, v_st, v_sh};
