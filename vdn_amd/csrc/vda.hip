@@ -39,7 +39,12 @@ __device__ __forceinline__ bf16x4_t lds_read_tr(const uint16_t* lds_elem_ptr) {
       (lds_bf16x4_t*)((__attribute__((address_space(3))) char*)(lds_elem_ptr)));
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+// SiLU(x) = x / (1 + exp(-x)) with the hardware exp2 and reciprocal: a few fp32 ulp from
+// the libm form, far below the bf16 rounding that follows every use.
+__device__ __forceinline__ float silu(float x) {
+  constexpr float kMinusLog2e = -1.4426950408889634f;
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * kMinusLog2e));
+}
 
 // Sum over the 16 lanes of a 16-lane group (xor butterfly).
 __device__ __forceinline__ float sum16(float v) {
@@ -76,7 +81,7 @@ __device__ __forceinline__ void activate8(float* v, bool l2) {
   }
   if (l2) {
     ss = sum16(ss);
-    const float inv = 1.0f / sqrtf(fmaxf(ss, 1e-12f));
+    const float inv = __builtin_amdgcn_rsqf(fmaxf(ss, 1e-12f));
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] *= inv;
   }
@@ -123,7 +128,7 @@ vda_prepare_kernel(const void* __restrict__ x, int64_t n, int heads, int64_t sn,
   }
   if (l2) {
     ss = sum16(ss);
-    const float inv = 1.0f / sqrtf(fmaxf(ss, 1e-12f));
+    const float inv = __builtin_amdgcn_rsqf(fmaxf(ss, 1e-12f));
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] *= inv;
   }
@@ -159,27 +164,31 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
   const int c8 = lane16 * 8;
   const int steps = (spatial + kTS - 1) / kTS;
 
-  // loader: thread handles tokens (tid/16) and (tid/16 + 16) of the step, channels c8..c8+7
-  u32x4 kraw[2], vraw[2];
-  float braw[2];
-  auto load_step = [&](int step) {
+  // loader: thread handles tokens (tid/16) and (tid/16 + 16) of the step, channels c8..c8+7.
+  // Two steps of raw rows are in registers: `kraw` etc. (the next step, stored to LDS at the
+  // end of this one) and `kraw_n` etc. (the step after, loading meanwhile), so every global
+  // load has a whole step to arrive.
+  u32x4 kraw[2], vraw[2], kraw_n[2], vraw_n[2];
+  float braw[2], braw_n[2];
+  auto load_step = [&](int step, u32x4 (&kr)[2], u32x4 (&vr)[2], float (&br)[2])
+      __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int s = step * kTS + (tid >> 4) + 16 * j;
       if (s < spatial) {
-        kraw[j] = *reinterpret_cast<const u32x4*>(kv.at(f, h, s) + c8);
-        vraw[j] = *reinterpret_cast<const u32x4*>(vv.at(f, h, s) + c8);
+        kr[j] = *reinterpret_cast<const u32x4*>(kv.at(f, h, s) + c8);
+        vr[j] = *reinterpret_cast<const u32x4*>(vv.at(f, h, s) + c8);
         const int64_t bo = f * b_sf + h * b_sh + s * b_ss;
-        braw[j] = beta_f32 ? static_cast<const float*>(beta)[bo]
-                           : bf16_bits_to_f32(static_cast<const uint16_t*>(beta)[bo]);
+        br[j] = beta_f32 ? static_cast<const float*>(beta)[bo]
+                         : bf16_bits_to_f32(static_cast<const uint16_t*>(beta)[bo]);
       } else {
-        kraw[j] = u32x4{0, 0, 0, 0};
-        vraw[j] = u32x4{0, 0, 0, 0};
-        braw[j] = 0.f;
+        kr[j] = u32x4{0, 0, 0, 0};
+        vr[j] = u32x4{0, 0, 0, 0};
+        br[j] = 0.f;
       }
     }
   };
-  auto store_step = [&](int buf) {
+  auto store_step = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int r = (tid >> 4) + 16 * j;
@@ -238,13 +247,14 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
     return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   };
 
-  load_step(0);
+  load_step(0, kraw, vraw, braw);
   store_step(0);
+  if (steps > 1) load_step(1, kraw, vraw, braw);
   __syncthreads();
   for (int step = 0; step < steps; ++step) {
     const int buf = step & 1;
     const bool more = step + 1 < steps;
-    if (more) load_step(step + 1);
+    if (step + 2 < steps) load_step(step + 2, kraw_n, vraw_n, braw_n);
     const uint16_t* tk = lds[buf][0];
     const uint16_t* tv = lds[buf][1 + kSplit];
     bf16x8 kn[4];  // K fragments for this wave's column blocks (B' operand B)
@@ -265,6 +275,12 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
       }
     }
     if (more) store_step(buf ^ 1);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      kraw[j] = kraw_n[j];
+      vraw[j] = vraw_n[j];
+      braw[j] = braw_n[j];
+    }
     __syncthreads();
   }
 
