@@ -30,7 +30,8 @@ D = 128
 
 GEMMS = ("vdn_mxfp8_gemm", "vdn_mxfp8_gemm_act_quantize")
 VDA_ENTRIES = ("vdn_vda_statistics", "vdn_vda_factors", "vdn_vda_compose", "vdn_vda_scan",
-               "vdn_vda_log_prefix", "vdn_vda_gather", "vdn_vda_readout")
+               "vdn_vda_log_prefix", "vdn_vda_gather", "vdn_vda_readout", "vdn_vda_readout_mxfp8")
+ATTENTION = ("vdn_window_attention", "vdn_window_attention_mxfp8")
 
 
 def log(msg):
@@ -68,7 +69,7 @@ def work(name, a, plans):
         operands = 1 if flags & 8 else 2
         tables = 0 if a[13] is None else 2 * tokens * rot * (4 if flags & 4 else 2)
         return 0.0, operands * tokens * heads * hd * 4 + tables
-    if name == "vdn_window_attention":
+    if name in ("vdn_window_attention", "vdn_window_attention_mxfp8"):
         heads = a[13]
         pairs = plans.get(a[11], 0)
         return 4.0 * D * heads * pairs, 0.0
@@ -94,6 +95,10 @@ def work(name, a, plans):
     if name == "vdn_vda_readout":
         f, h, s = a[17], a[18], a[19]
         return 2.0 * f * s * h * D * D, 3 * f * s * h * D * 2 + f * h * D * D * 2
+    if name == "vdn_vda_readout_mxfp8":   # q, gate read (bf16); codes + scales written
+        f, h, s = a[17], a[18], a[19]
+        return (2.0 * f * s * h * D * D,
+                2 * f * s * h * D * 2 + f * s * h * D * (1 + 1 / 32) + f * h * D * D * 2)
     return 0.0, 0.0
 
 
@@ -311,9 +316,9 @@ def main():
     for name, (count, t, flop, nbytes) in sorted(per.items(), key=lambda kv: -kv[1][1]):
         row = dict(ms_per_step=round(t / args.steps, 3), launches_per_step=count // args.steps,
                    avg_launch_ms=round(t / count, 4))
-        if flop and name in GEMMS + ("vdn_window_attention",):
+        if flop and name in GEMMS + ATTENTION:
             row["tflops"] = round(flop / (t * 1e-3) / 1e12, 1)
-        if nbytes and name not in GEMMS + ("vdn_window_attention",):
+        if nbytes and name not in GEMMS + ATTENTION:
             row["gbs"] = round(nbytes / (t * 1e-3) / 1e9, 1)
         breakdown[name] = row
     g = [sum(per[nm][i] for nm in GEMMS if nm in per) for i in range(4)]
@@ -321,7 +326,7 @@ def main():
     vda_t = sum(per[n][1] for n in VDA_ENTRIES if n in per)
     vda_bytes = sum(per[n][3] for n in VDA_ENTRIES if n in per)
     vda_gbs = vda_bytes / (vda_t * 1e-3) / 1e9
-    w = per["vdn_window_attention"]
+    w = [sum(per[nm][i] for nm in ATTENTION if nm in per) for i in range(4)]
     traffic = traffic_per_launch()
 
     result = {

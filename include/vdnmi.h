@@ -186,6 +186,19 @@ int vdn_vda_readout(const void* q, int64_t q_sf, int64_t q_sh, int64_t q_ss, int
                     int64_t o_sf, int64_t o_sh, int64_t o_ss, int frames, int heads, int spatial,
                     void* stream);
 
+/* vdn_vda_readout with the output quantized in the epilogue instead of stored as bf16: token
+ * row f * spatial + s, head h -> MXFP8 codes[row, 128 (chunk0 + h) .. +128) of a [rows, kp]
+ * code matrix and that chunk's four E8M0 scales in its SWIZZLE_32_4_4 scale array; the same
+ * bytes vdn_mxfp8_quantize writes for the bf16 output.
+ * Replaces: the readout of paper_readout (src/models/linear_attention/paper_stack.py:317-318,
+ * paper_sglang.py:377-437) followed by quantize_activation (src/models/ops/mxfp8_quant.py:77-90).
+ */
+int vdn_vda_readout_mxfp8(const void* q, int64_t q_sf, int64_t q_sh, int64_t q_ss,
+                          int activate_q, const void* state, const void* weight, int weight_f32,
+                          float eps, const void* gate, int64_t g_sf, int64_t g_sh, int64_t g_ss,
+                          void* codes, void* scales, int64_t kp, int chunk0, int frames,
+                          int heads, int spatial, void* stream);
+
 /*
  * RMSNorm(128) * weight * gate of a frame-major readout [frames, heads, spatial, 128] bf16.
  * Replaces: vdn_linear_epilogue (src/models/linear_attention/paper_sglang.py:406-437).
@@ -232,6 +245,21 @@ int vdn_window_attention(const void* q, int64_t q_st, int64_t q_sh, const void* 
                          int heads, float scale, const void* gate, int64_t g_st, int64_t g_sh,
                          void* out, int64_t o_st, int64_t o_sh, float* lse, int64_t l_st,
                          int64_t l_sh, void* stream);
+
+/* vdn_window_attention with the output quantized in the epilogue instead of stored as bf16:
+ * query row q, head h -> MXFP8 codes[q, 128 (chunk0 + h) .. +128) of a [rows, kp] code
+ * matrix and the four E8M0 scales of that chunk in its SWIZZLE_32_4_4 scale array; the same
+ * bytes vdn_mxfp8_quantize writes for the bf16 output. Rows without a query are not written.
+ * codes 16-byte aligned, kp a multiple of 128 with (chunk0 + heads) * 128 <= kp.
+ * Replaces: paper_window_attention (src/models/softmax_attention/paper_window.py:182-243)
+ * followed by quantize_activation (src/models/ops/mxfp8_quant.py:77-90) of its output.
+ */
+int vdn_window_attention_mxfp8(const void* q, int64_t q_st, int64_t q_sh, const void* k,
+                               int64_t k_st, int64_t k_sh, const void* v, int64_t v_st,
+                               int64_t v_sh, const int* blocks, int nblocks, const int* grp_kv,
+                               const int* grp_n, int heads, float scale, const void* gate,
+                               int64_t g_st, int64_t g_sh, void* codes, void* scales, int64_t kp,
+                               int chunk0, void* stream);
 
 #ifdef __cplusplus
 }

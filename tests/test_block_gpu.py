@@ -122,6 +122,22 @@ def test_block_is_deterministic_and_leaves_its_input_alone():
     assert torch.isfinite(a.float()).all()
 
 
+def test_fused_mxfp8_epilogues_give_the_unfused_block():
+    """The block's default path quantizes the attention, VDA and cross-attention outputs in
+    their kernels; return_parts keeps them in bf16 and quantizes them separately. Both feed
+    the same bytes to the output projections, so the outputs are identical."""
+    cfg = WIDE
+    w = BlockWeights.random(cfg, 5, device="cuda")
+    block = HybridDiTBlock(cfg, w)
+    hidden, temb, ctx, layout, rope = make_inputs(cfg, 3, 4, 8, 6, device="cuda")
+    plan = vw.prepare_paper_window_plan(layout, vw.window_bounds(3, 1), device="cuda")
+    cplan = cross_attention_plan(hidden.shape[0], ctx.shape[0], "cuda")
+    with torch.no_grad():
+        fused = block(hidden, temb, ctx, layout, rope, plan, cplan)
+        unfused, _ = block(hidden, temb, ctx, layout, rope, plan, cplan, return_parts=True)
+    assert torch.equal(fused, unfused)
+
+
 def test_rope_tables_match_the_oracle_restatement():
     cos, sin = vw.rope_tables_3d(3, 5, 7, device="cuda", dtype=torch.float32)
     oc, os_ = ow.rope_tables_3d(3, 5, 7)

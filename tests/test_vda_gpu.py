@@ -222,3 +222,30 @@ def test_c3_full_shape_sampled_heads(device):
                              frames, spatial, w, 1e-6)
     got = out.view(n, h, 128)[:, heads].reshape(n, -1)
     close_rel(got, ref, 0.004)
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("chunk0", [0, 2])
+def test_readout_mxfp8_equals_quantized_bf16_readout(device, chunk0):
+    """The quantizing readout epilogue writes exactly the bytes quantize_activation writes for
+    the bf16 readout, into chunks chunk0 .. chunk0+H-1; padding rows read as zero."""
+    from vdn_amd import mxfp8 as vm
+    frames, spatial, h = 3, 50, 3
+    g = torch.Generator().manual_seed(21)
+    n = frames * spatial
+    q = torch.randn(n, h, 128, generator=g).bfloat16().to(device)
+    state = (torch.randn(frames, h, 128, 128, generator=g) * 0.1).bfloat16().to(device)
+    gate = torch.rand(n, h, 128, generator=g).bfloat16().to(device)
+    w = (torch.rand(128, generator=g) + 0.5).to(device)
+    ref = vv.linear_readout(q, state, w, gate, 1e-6, frames, spatial)
+    width = (chunk0 + h) * 128
+    wide = torch.zeros(n, width, device=device, dtype=torch.bfloat16)
+    wide[:, chunk0 * 128:] = ref
+    rq, rs = vm.launch_quantize(wide)
+    codes, scales = vm.empty_activation(n, width, device)
+    codes.zero_()
+    scales.copy_(rs)
+    assert vv.linear_readout(q, state, w, gate, 1e-6, frames, spatial,
+                             out_mxfp8=(codes, scales, chunk0)) is None
+    assert torch.equal(codes, rq)
+    assert torch.equal(scales, rs)

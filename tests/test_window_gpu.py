@@ -207,3 +207,48 @@ def test_rope_3d_tables_c4_geometry(device):
     expected = ow.qk_rope(q, w, 1e-6, cos.cpu(), sin.cpu())
     torch.testing.assert_close(out.cpu(), expected, atol=.032, rtol=.02)
     assert ((out.cpu().float() - expected.float()).norm() / expected.float().norm()) < 2e-3
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("rows,chunk0,gated", [(1200, 0, True), (1000, 3, False)])
+def test_mxfp8_output_equals_quantized_bf16_output(device, rows, chunk0, gated):
+    """The quantizing epilogue writes exactly the bytes quantize_activation writes for the bf16
+    output, into chunks chunk0 .. chunk0+H-1 of a wider operand; padding rows stay zero."""
+    from vdn_amd import mxfp8 as vm
+    torch.manual_seed(5)
+    frames = 4
+    layout = vw.SequenceLayout(rows, 0, frames, rows // frames)
+    plan = vw.prepare_paper_window_plan(layout, vw.window_bounds(frames, 1), device=device)
+    h = 5
+    q, k, v = [torch.randn(rows, h, 128, device=device, dtype=torch.bfloat16) for _ in range(3)]
+    gate = torch.rand(rows, h, 1, device=device, dtype=torch.bfloat16) if gated else None
+    ref = vw.paper_window_attention(q, k, v, plan, enabled=True, gate=gate)
+    width = (chunk0 + h + 1) * 128
+    wide = torch.zeros(rows, width, device=device, dtype=torch.bfloat16)
+    wide[:, chunk0 * 128:(chunk0 + h) * 128] = ref.reshape(rows, -1)
+    rq, rs = vm.launch_quantize(wide)
+    codes, scales = vm.empty_activation(rows, width, device)
+    # chunks outside the attention's range hold what the reference buffer holds there (zero)
+    codes.zero_()
+    scales.copy_(rs)
+    assert vw.paper_window_attention(q, k, v, plan, enabled=True, gate=gate,
+                                     out_mxfp8=(codes, scales, chunk0)) is None
+    assert torch.equal(codes, rq)
+    assert torch.equal(scales, rs)
+
+
+@torch.no_grad()
+def test_mxfp8_output_rejects_bad_destinations(device):
+    from vdn_amd import mxfp8 as vm
+    layout = vw.SequenceLayout(256, 0, 2, 128)
+    plan = vw.prepare_paper_window_plan(layout, vw.window_bounds(2, 1), device=device)
+    q = torch.randn(256, 4, 128, device=device, dtype=torch.bfloat16)
+    codes, scales = vm.empty_activation(256, 4 * 128, device)
+    with pytest.raises(ValueError, match="chunk0"):
+        vw.paper_window_attention(q, q, q, plan, enabled=True, out_mxfp8=(codes, scales, 1))
+    with pytest.raises(ValueError, match="padded"):
+        vw.paper_window_attention(q, q, q, plan, enabled=True,
+                                  out_mxfp8=(codes[:, :384].contiguous(), scales, 0))
+    with pytest.raises(ValueError, match="excludes"):
+        vw.paper_window_attention(q, q, q, plan, enabled=True, return_lse=True,
+                                  out_mxfp8=(codes, scales, 0))

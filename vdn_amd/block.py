@@ -175,7 +175,6 @@ class HybridDiTBlock(nn.Module):
         dev = hidden.device
         shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = self.adaln_tables(temb)
         idx = torch.zeros(T, dtype=torch.long, device=dev)
-        h = hidden.clone()
         parts = {} if return_parts else None
 
         def snap(name, t):
@@ -183,8 +182,8 @@ class HybridDiTBlock(nn.Module):
                 parts[name] = t.clone() if isinstance(t, torch.Tensor) else t
 
         # ---- hybrid self-attention ----
-        x1, q1, s1, _ = mx.launch_prenorm_quantize(h, k["norm1"], cfg.eps, scale_msa, shift_msa,
-                                                   idx, write_bf16=True)
+        x1, q1, s1, _ = mx.launch_prenorm_quantize(hidden, k["norm1"], cfg.eps, scale_msa,
+                                                   shift_msa, idx, write_bf16=True)
         qkv = self.qkv.forward_quantized(q1, s1, rows=T)
         snap("tables", (shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp))
         snap("x1", x1)
@@ -201,21 +200,35 @@ class HybridDiTBlock(nn.Module):
         cos, sin = rope
         q, kk = vw.paper_qk_rmsnorm_rope(raw_q, raw_k, k["norm_q"], k["norm_k"], cfg.eps, cos, sin,
                                          enabled=True)
-        # the two branch outputs land side by side in one [T, 2H] buffer
-        both = torch.empty((T, 2 * hd), dtype=torch.bfloat16, device=dev)
-        vw.paper_window_attention(q, kk, value, window_plan, d ** -0.5, enabled=True,
-                                  gate=soft_gate, out=both[:, :hd].view(T, heads, d))
-        del q, kk
+        # The two branch outputs are the two halves of the [O | O_lin] operand. The kernels
+        # quantize them in their epilogues straight into the MXFP8 operand (chunks 0..H-1 for
+        # the softmax branch, H.. for VDA); with return_parts they are kept in bf16 for the
+        # snapshots and quantized afterwards, which gives the same bytes.
         bounds = window_plan.bounds
-        vv.vda_forward(raw_q, raw_k, value, beta, lin_gate.view(T, heads, d), alpha, bounds,
-                       frames, spatial, k["vda_norm"], cfg.eps, chunk_size=cfg.vda_chunk,
-                       out=both[:, hd:])
+        if parts is None:
+            qb, sb = mx.empty_activation(T, 2 * hd, dev)
+            vw.paper_window_attention(q, kk, value, window_plan, d ** -0.5, enabled=True,
+                                      gate=soft_gate, out_mxfp8=(qb, sb, 0))
+            del q, kk
+            vv.vda_forward(raw_q, raw_k, value, beta, lin_gate.view(T, heads, d), alpha, bounds,
+                           frames, spatial, k["vda_norm"], cfg.eps, chunk_size=cfg.vda_chunk,
+                           out_mxfp8=(qb, sb, heads))
+        else:
+            both = torch.empty((T, 2 * hd), dtype=torch.bfloat16, device=dev)
+            vw.paper_window_attention(q, kk, value, window_plan, d ** -0.5, enabled=True,
+                                      gate=soft_gate, out=both[:, :hd].view(T, heads, d))
+            del q, kk
+            vv.vda_forward(raw_q, raw_k, value, beta, lin_gate.view(T, heads, d), alpha, bounds,
+                           frames, spatial, k["vda_norm"], cfg.eps, chunk_size=cfg.vda_chunk,
+                           out=both[:, hd:])
+            snap("soft", both[:, :hd])
+            snap("far", both[:, hd:])
+            qb, sb = mx.launch_quantize(both)
+            del both
         del qkv, raw_q, raw_k, value, lin_gate
-        snap("soft", both[:, :hd])
-        snap("far", both[:, hd:])
-        qb, sb = mx.launch_quantize(both)
-        del both
-        self.o_cat.forward_quantized(qb, sb, rows=T, out=h, residual=h, gate=gate_msa)
+        # the first residual update writes a fresh tensor (no copy of the input)
+        h = torch.empty_like(hidden)
+        self.o_cat.forward_quantized(qb, sb, rows=T, out=h, residual=hidden, gate=gate_msa)
         snap("h1", h)
         del qb, sb
 
@@ -230,11 +243,15 @@ class HybridDiTBlock(nn.Module):
         cv = self.cv.forward_quantized(cx, csx, rows=L).view(L, heads, d)
         cq = vw.qk_rmsnorm(cq, k["norm_qc"], cfg.eps)
         ck = vw.qk_rmsnorm(ck, k["norm_kc"], cfg.eps)
-        co = cross_attention(cq, ck, cv, cross_plan, d ** -0.5)
+        if parts is None:
+            qo, so = mx.empty_activation(T, hd, dev)
+            cross_attention(cq, ck, cv, cross_plan, d ** -0.5, out_mxfp8=(qo, so, 0))
+        else:
+            co = cross_attention(cq, ck, cv, cross_plan, d ** -0.5)
+            snap("co", co.view(T, hd))
+            qo, so = mx.launch_quantize(co.view(T, hd))
+            del co
         del cq, ck, cv
-        snap("co", co.view(T, hd))
-        qo, so = mx.launch_quantize(co.view(T, hd))
-        del co
         self.co.forward_quantized(qo, so, rows=T, out=h, residual=h)
         del qo, so
         snap("h2", h)
@@ -253,10 +270,20 @@ def cross_attention_plan(num_queries: int, num_keys: int, device) -> vw.DevicePl
     return vw._device_plan([(((0, num_queries),), ((0, num_keys),))], torch.device(device))
 
 
-def cross_attention(q, k, v, plan: vw.DevicePlan, scale):
-    """Unmasked attention of q [T, H, D] over context k, v [L, H, D] on the window kernel."""
+def cross_attention(q, k, v, plan: vw.DevicePlan, scale, out_mxfp8=None):
+    """Unmasked attention of q [T, H, D] over context k, v [L, H, D] on the window kernel.
+    `out_mxfp8` = (codes, scales, chunk0): quantize the output in the kernel (head h -> chunk
+    chunk0 + h) instead of returning bf16 [T, H, D]."""
     from . import _lib
     T, h, d = q.shape
+    if out_mxfp8 is not None:
+        codes, scales, chunk0 = mx.mxfp8_destination(out_mxfp8, T, h, q.device)
+        _lib.call("vdn_window_attention_mxfp8", q.data_ptr(), q.stride(0), q.stride(1),
+                  k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
+                  plan.blocks.data_ptr(), plan.nblocks, plan.intervals.data_ptr(),
+                  plan.counts.data_ptr(), h, float(scale), None, 0, 0, codes.data_ptr(),
+                  scales.data_ptr(), codes.shape[1], chunk0, _lib.stream(q.device))
+        return None
     out = torch.empty_like(q)
     _lib.call("vdn_window_attention", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
               k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),

@@ -22,7 +22,7 @@
 //     M[r0 .. r0+3][c0 + l] (measured on gfx950);
 //   * the scans keep a 16-row block of the 128x128 fp32 state per workgroup (rows evolve
 //     independently) and use fp32 MFMA for state @ T.
-#include "common.h"
+#include "mxfp8_common.h"
 
 #include <math.h>
 
@@ -622,8 +622,18 @@ vda_gather_kernel(const float* __restrict__ prefix, const float* __restrict__ su
 // ------------------------------------------------------------ readout + norm ----
 // RMSNorm(d)·w·gate of 8 channels held by one lane of a 16-lane token group
 // (paper_sglang.py:398-403): y * (1 / sqrt(mean(y^2) + eps)) * w * g, fp32, one rounding.
-__device__ __forceinline__ void norm_gate_store8(float* y, const float* w, const uint16_t* gsrc,
-                                                 uint16_t* dst, float eps) {
+// MXFP8 destination of the readout (instead of bf16 rows): token row n = f * S + s, head h
+// fills 128-column chunk chunk0 + h of codes [rows, kp] and its SWIZZLE_32_4_4 scales.
+struct MxDst {
+  uint8_t* codes;
+  uint8_t* scales;
+  int64_t kp;
+  int chunk0;
+};
+
+// RMSNorm(y)·w·gate of one lane's 8 values, rounded to bf16 (as stored by the bf16 form).
+__device__ __forceinline__ void norm_gate8(const float* y, const float* w, const uint16_t* gsrc,
+                                           float eps, float* o) {
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) ss += y[i] * y[i];
@@ -631,9 +641,14 @@ __device__ __forceinline__ void norm_gate_store8(float* y, const float* w, const
   const float inv = 1.0f / sqrtf(ss / static_cast<float>(kD) + eps);
   float gv[8];
   unpack8(*reinterpret_cast<const u32x4*>(gsrc), gv);
-  float o[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = y[i] * inv * w[i] * gv[i];
+  for (int i = 0; i < 8; ++i) o[i] = round_bf16(y[i] * inv * w[i] * gv[i]);
+}
+
+__device__ __forceinline__ void norm_gate_store8(float* y, const float* w, const uint16_t* gsrc,
+                                                 uint16_t* dst, float eps) {
+  float o[8];
+  norm_gate8(y, w, gsrc, eps, o);
   *reinterpret_cast<u32x4*>(dst) = pack8(o);
 }
 
@@ -642,11 +657,12 @@ __device__ __forceinline__ void norm_gate_store8(float* y, const float* w, const
 constexpr int kQT = 64;
 constexpr int kQRow = 136;  // padded bf16 row (272 bytes)
 
+template <bool kMx>
 __global__ void __launch_bounds__(256, 2)
 vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
                    const void* __restrict__ weight, int weight_f32, float eps, View gv,
                    uint16_t* __restrict__ out, int64_t o_sf, int64_t o_sh, int64_t o_ss,
-                   int spatial, int heads, int tiles) {
+                   int spatial, int heads, int tiles, MxDst mx) {
   __shared__ __attribute__((aligned(16))) uint16_t sState[kD * kQRow];  // [v][k]
   __shared__ __attribute__((aligned(16))) uint16_t sQ[kQT * kQRow];     // [token][k], then y
   const int tile = blockIdx.x % tiles;
@@ -708,8 +724,15 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
     if (s >= spatial) continue;  // uniform per 16-lane group
     float y[8];
     unpack8(*reinterpret_cast<const u32x4*>(&sQ[r * kQRow + lane16 * 8]), y);
-    norm_gate_store8(y, w, gv.at(f, h, s) + lane16 * 8,
-                     out + f * o_sf + h * o_sh + s * o_ss + lane16 * 8, eps);
+    if constexpr (kMx) {
+      float o[8];
+      norm_gate8(y, w, gv.at(f, h, s) + lane16 * 8, eps, o);
+      quantize_store8(o, lane16, static_cast<int64_t>(f) * spatial + s, mx.chunk0 + h, mx.kp,
+                      mx.codes, mx.scales);
+    } else {
+      norm_gate_store8(y, w, gv.at(f, h, s) + lane16 * 8,
+                       out + f * o_sf + h * o_sh + s * o_ss + lane16 * 8, eps);
+    }
   }
 }
 
@@ -880,28 +903,78 @@ VDN_API int vdn_vda_gather(const float* prefix, const float* suffix, const float
 // the q activation of paper_prepare applied in registers when activate_q = 1.
 // q: (f, h, s, c) at q + f*q_sf + h*q_sh + s*q_ss + c; gate likewise; out likewise.
 // state: bf16 [F, H, 128, 128] ([v][k]); weight [128] bf16 or fp32.
+namespace vdn {
+namespace {
+
+int launch_readout(const char* name, const void* q, int64_t q_sf, int64_t q_sh, int64_t q_ss,
+                   int activate_q, const void* state, const void* weight, int weight_f32,
+                   float eps, const void* gate, int64_t g_sf, int64_t g_sh, int64_t g_ss,
+                   void* out, int64_t o_sf, int64_t o_sh, int64_t o_ss, const MxDst* mx,
+                   int frames, int heads, int spatial, void* stream) {
+  if (q == nullptr || state == nullptr || weight == nullptr || gate == nullptr ||
+      (mx == nullptr && out == nullptr))
+    return set_error(kInvalidArgument, "%s: null pointer", name);
+  if (frames <= 0 || heads <= 0 || spatial <= 0)
+    return set_error(kInvalidArgument, "%s: bad geometry", name);
+  if (!aligned16(q) || !aligned16(gate) || !aligned16(state) || !stride8(q_sf) ||
+      !stride8(q_sh) || !stride8(q_ss) || !stride8(g_sf) || !stride8(g_sh) || !stride8(g_ss) ||
+      (mx == nullptr && (!aligned16(out) || !stride8(o_sf) || !stride8(o_sh) || !stride8(o_ss))))
+    return set_error(kInvalidArgument, "%s: operands need 16-byte aligned rows", name);
+  if (mx != nullptr) {
+    if (mx->codes == nullptr || mx->scales == nullptr)
+      return set_error(kInvalidArgument, "%s: null pointer", name);
+    if (!aligned16(mx->codes) || (reinterpret_cast<uintptr_t>(mx->scales) & 3) != 0 ||
+        mx->kp <= 0 || mx->kp % 128 != 0 || mx->chunk0 < 0 ||
+        static_cast<int64_t>(mx->chunk0 + heads) * 128 > mx->kp)
+      return set_error(kInvalidArgument,
+                       "%s: codes need 16-byte alignment, a multiple-of-128 row length holding "
+                       "chunks [chunk0, chunk0 + heads), scales 4-byte alignment", name);
+  }
+  const int tiles = (spatial + kQT - 1) / kQT;
+  const View qv{static_cast<const uint16_t*>(q), q_sf, q_sh, q_ss};
+  const View gv{static_cast<const uint16_t*>(gate), g_sf, g_sh, g_ss};
+  const dim3 grid(frames * heads * tiles), block(256);
+  const auto st = static_cast<hipStream_t>(stream);
+  if (mx != nullptr)
+    hipLaunchKernelGGL(vda_readout_kernel<true>, grid, block, 0, st, qv, activate_q,
+                       static_cast<const uint16_t*>(state), weight, weight_f32, eps, gv, nullptr,
+                       0, 0, 0, spatial, heads, tiles, *mx);
+  else
+    hipLaunchKernelGGL(vda_readout_kernel<false>, grid, block, 0, st, qv, activate_q,
+                       static_cast<const uint16_t*>(state), weight, weight_f32, eps, gv,
+                       static_cast<uint16_t*>(out), o_sf, o_sh, o_ss, spatial, heads, tiles,
+                       MxDst{nullptr, nullptr, 0, 0});
+  return check_launch(name);
+}
+
+}  // namespace
+}  // namespace vdn
+
 VDN_API int vdn_vda_readout(const void* q, int64_t q_sf, int64_t q_sh, int64_t q_ss,
                             int activate_q, const void* state, const void* weight, int weight_f32,
                             float eps, const void* gate, int64_t g_sf, int64_t g_sh, int64_t g_ss,
                             void* out, int64_t o_sf, int64_t o_sh, int64_t o_ss, int frames,
                             int heads, int spatial, void* stream) {
-  const char* name = "vdn_vda_readout";
-  if (q == nullptr || state == nullptr || weight == nullptr || gate == nullptr || out == nullptr)
-    return set_error(kInvalidArgument, "%s: null pointer", name);
-  if (frames <= 0 || heads <= 0 || spatial <= 0)
-    return set_error(kInvalidArgument, "%s: bad geometry", name);
-  if (!aligned16(q) || !aligned16(gate) || !aligned16(out) || !aligned16(state) ||
-      !stride8(q_sf) || !stride8(q_sh) || !stride8(q_ss) || !stride8(g_sf) || !stride8(g_sh) ||
-      !stride8(g_ss) || !stride8(o_sf) || !stride8(o_sh) || !stride8(o_ss))
-    return set_error(kInvalidArgument, "%s: operands need 16-byte aligned rows", name);
-  const int tiles = (spatial + kQT - 1) / kQT;
-  const View qv{static_cast<const uint16_t*>(q), q_sf, q_sh, q_ss};
-  const View gv{static_cast<const uint16_t*>(gate), g_sf, g_sh, g_ss};
-  hipLaunchKernelGGL(vda_readout_kernel, dim3(frames * heads * tiles), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), qv, activate_q,
-                     static_cast<const uint16_t*>(state), weight, weight_f32, eps, gv,
-                     static_cast<uint16_t*>(out), o_sf, o_sh, o_ss, spatial, heads, tiles);
-  return check_launch(name);
+  return launch_readout("vdn_vda_readout", q, q_sf, q_sh, q_ss, activate_q, state, weight,
+                        weight_f32, eps, gate, g_sf, g_sh, g_ss, out, o_sf, o_sh, o_ss, nullptr,
+                        frames, heads, spatial, stream);
+}
+
+// The same readout with the output quantized in the epilogue: token row f * S + s, head h ->
+// MXFP8 codes[row, 128 (chunk0 + h) ..] (row length kp) and the swizzled scales of its four
+// 32-blocks, bit-identical to vdn_mxfp8_quantize of the bf16 output. Reference: the
+// projection's producer, quantize_activation (src/models/ops/mxfp8_quant.py:77-90), applied
+// to the readout of paper_readout (src/models/linear_attention/paper_stack.py:266-318).
+VDN_API int vdn_vda_readout_mxfp8(const void* q, int64_t q_sf, int64_t q_sh, int64_t q_ss,
+                                  int activate_q, const void* state, const void* weight,
+                                  int weight_f32, float eps, const void* gate, int64_t g_sf,
+                                  int64_t g_sh, int64_t g_ss, void* codes, void* scales,
+                                  int64_t kp, int chunk0, int frames, int heads, int spatial,
+                                  void* stream) {
+  const MxDst mx{static_cast<uint8_t*>(codes), static_cast<uint8_t*>(scales), kp, chunk0};
+  return launch_readout("vdn_vda_readout_mxfp8", q, q_sf, q_sh, q_ss, activate_q, state,
+                        weight, weight_f32, eps, gate, g_sf, g_sh, g_ss, nullptr, 0, 0, 0, &mx,
+                        frames, heads, spatial, stream);
 }
 
 // Reference: paper_sglang.py:377-437 (_linear_epilogue_kernel / vdn_linear_epilogue):

@@ -17,7 +17,7 @@
 // K/V tiles stream global -> LDS with buffer_load_dwordx4 ... lds, double-buffered; 16-byte
 // chunk c of tile row r is stored at c ^ (r & 15) (K: row reads) or c ^ 2 (r & 7) (V: the
 // 4-row transpose reads), which keeps both read patterns free of bank conflicts.
-#include "common.h"
+#include "mxfp8_common.h"
 
 #include <math.h>
 
@@ -60,6 +60,16 @@ __device__ __forceinline__ bf16x4_t lds_read_tr(const uint16_t* p) {
 __device__ __forceinline__ int swz_k(int row) { return row & 15; }
 __device__ __forceinline__ int swz_v(int row) { return 2 * (row & 7); }
 
+// MXFP8 destination of the output (instead of bf16 rows): codes [rows, kp] and
+// SWIZZLE_32_4_4 scales; head h of query row q fills 128-column chunk chunk0 + h, exactly
+// what the MXFP8 producer writes for that bf16 row.
+struct MxDst {
+  uint8_t* codes;
+  uint8_t* scales;
+  int64_t kp;
+  int chunk0;
+};
+
 struct Layout {
   const uint16_t* q;
   const uint16_t* k;
@@ -69,13 +79,13 @@ struct Layout {
 
 // kWaves waves of 32 queries each: a workgroup owns kBM = 32 kWaves queries, and every K/V
 // tile it loads serves all of them.
-template <int kWaves>
+template <int kWaves, bool kMx>
 __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restrict__ grp_kv,
                    const int* __restrict__ grp_n, int nblocks, int heads, float scale_log2,
                    const uint16_t* __restrict__ gate, int64_t g_st, int64_t g_sh,
                    uint16_t* __restrict__ out, int64_t o_st, int64_t o_sh,
-                   float* __restrict__ lse, int64_t l_st, int64_t l_sh) {
+                   float* __restrict__ lse, int64_t l_st, int64_t l_sh, MxDst mx) {
   // Separate arrays per buffer: with distinct LDS objects the compiler can tell a tile
   // prefetch into one buffer from reads of the other and does not wait on the prefetch.
   __shared__ __attribute__((aligned(1024))) uint16_t sK0[kBN * kD];
@@ -309,14 +319,24 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
   if (lse != nullptr && q_live && g == 0)
     lse[static_cast<int64_t>(my_q) * l_st + h * l_sh] = (m + log2f(l)) * kLn2;
   __syncthreads();
-  // 16 lanes write one query row (256 bytes)
+  // 16 lanes write one query row (256 bytes, or its 128 MXFP8 codes and 4 scales)
   for (int r = tid >> 4; r < kBM; r += kThreads / 16) {
     const int q = q0 + r;
-    if (q >= q1) continue;
+    if (q >= q1) continue;  // uniform per 16-lane group
     const int c8 = (tid & 15) * 8;
     const uint16_t* src = stage_rows(r);
-    *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(q) * o_st + h * o_sh + c8) =
-        *reinterpret_cast<const u32x4*>(&src[(r % kBN) * kD + c8]);
+    const u32x4 row8 = *reinterpret_cast<const u32x4*>(&src[(r % kBN) * kD + c8]);
+    if constexpr (kMx) {
+      float y[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        y[2 * i] = bf16_bits_to_f32(static_cast<uint16_t>(row8[i] & 0xffff));
+        y[2 * i + 1] = bf16_bits_to_f32(static_cast<uint16_t>(row8[i] >> 16));
+      }
+      quantize_store8(y, tid & 15, q, mx.chunk0 + h, mx.kp, mx.codes, mx.scales);
+    } else {
+      *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(q) * o_st + h * o_sh + c8) = row8;
+    }
   }
 }
 
@@ -326,6 +346,62 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 }  // namespace vdn
 
 using namespace vdn;
+
+namespace vdn {
+namespace {
+
+// Shared validation and launch of both entry points (out / lse for the bf16 form, mx for
+// the MXFP8 form).
+int launch_window(const char* name, const void* q, int64_t q_st, int64_t q_sh, const void* k,
+                  int64_t k_st, int64_t k_sh, const void* v, int64_t v_st, int64_t v_sh,
+                  const int* blocks, int nblocks, const int* grp_kv, const int* grp_n, int heads,
+                  float scale, const void* gate, int64_t g_st, int64_t g_sh, void* out,
+                  int64_t o_st, int64_t o_sh, float* lse, int64_t l_st, int64_t l_sh,
+                  const MxDst* mx, void* stream) {
+  if (q == nullptr || k == nullptr || v == nullptr || blocks == nullptr || grp_kv == nullptr ||
+      grp_n == nullptr || (mx == nullptr && out == nullptr))
+    return set_error(kInvalidArgument, "%s: null pointer", name);
+  if (heads <= 0 || nblocks < 0) return set_error(kInvalidArgument, "%s: bad geometry", name);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || q_st % 8 || q_sh % 8 || k_st % 8 ||
+      k_sh % 8 || v_st % 8 || v_sh % 8 ||
+      (mx == nullptr && (!aligned16(out) || o_st % 8 || o_sh % 8)))
+    return set_error(kInvalidArgument, "%s: rows need 16-byte alignment", name);
+  if (mx != nullptr) {
+    if (mx->codes == nullptr || mx->scales == nullptr)
+      return set_error(kInvalidArgument, "%s: null pointer", name);
+    if (!aligned16(mx->codes) || (reinterpret_cast<uintptr_t>(mx->scales) & 3) != 0 ||
+        mx->kp <= 0 || mx->kp % 128 != 0 || mx->chunk0 < 0 ||
+        static_cast<int64_t>(mx->chunk0 + heads) * 128 > mx->kp)
+      return set_error(kInvalidArgument,
+                       "%s: codes need 16-byte alignment, a multiple-of-128 row length holding "
+                       "chunks [chunk0, chunk0 + heads), scales 4-byte alignment", name);
+  }
+  if (!(scale > 0.f) || !isfinite(scale)) return set_error(kInvalidArgument, "%s: bad scale", name);
+  if (k_st <= 0 || v_st <= 0 || k_st > (1 << 22) || v_st > (1 << 22))
+    return set_error(kUnsupported, "%s: K/V token strides must be in (0, 2^22] elements", name);
+  if (nblocks == 0) return kOk;
+  const Layout in{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                  static_cast<const uint16_t*>(v), q_st, q_sh, k_st, k_sh, v_st, v_sh};
+  const int64_t total = static_cast<int64_t>(nblocks) * heads;
+  if (total > (1ll << 31) - 1) return set_error(kUnsupported, "%s: too many blocks", name);
+  const dim3 grid(static_cast<unsigned>(total)), block(kBlockWaves * 64);
+  const auto st = static_cast<hipStream_t>(stream);
+  if (mx != nullptr)
+    hipLaunchKernelGGL((window_attn_kernel<kBlockWaves, true>), grid, block, 0, st, in, blocks,
+                       grp_kv, grp_n, nblocks, heads, scale * kLog2e,
+                       static_cast<const uint16_t*>(gate), g_st, g_sh, nullptr, 0, 0, nullptr,
+                       0, 0, *mx);
+  else
+    hipLaunchKernelGGL((window_attn_kernel<kBlockWaves, false>), grid, block, 0, st, in, blocks,
+                       grp_kv, grp_n, nblocks, heads, scale * kLog2e,
+                       static_cast<const uint16_t*>(gate), g_st, g_sh,
+                       static_cast<uint16_t*>(out), o_st, o_sh, lse, l_st, l_sh,
+                       MxDst{nullptr, nullptr, 0, 0});
+  return check_launch(name);
+}
+
+}  // namespace
+}  // namespace vdn
 
 // Reference: paper_window_attention (src/models/softmax_attention/paper_window.py:182-243),
 // window_softmax_reference (window.py:56-111), apply_softmax_gate (kernels.py:51-67).
@@ -342,26 +418,25 @@ VDN_API int vdn_window_attention(const void* q, int64_t q_st, int64_t q_sh, cons
                                  int64_t g_st, int64_t g_sh, void* out, int64_t o_st,
                                  int64_t o_sh, float* lse, int64_t l_st, int64_t l_sh,
                                  void* stream) {
-  const char* name = "vdn_window_attention";
-  if (q == nullptr || k == nullptr || v == nullptr || blocks == nullptr || grp_kv == nullptr ||
-      grp_n == nullptr || out == nullptr)
-    return set_error(kInvalidArgument, "%s: null pointer", name);
-  if (heads <= 0 || nblocks < 0) return set_error(kInvalidArgument, "%s: bad geometry", name);
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || q_st % 8 ||
-      q_sh % 8 || k_st % 8 || k_sh % 8 || v_st % 8 || v_sh % 8 || o_st % 8 || o_sh % 8)
-    return set_error(kInvalidArgument, "%s: rows need 16-byte alignment", name);
-  if (!(scale > 0.f) || !isfinite(scale)) return set_error(kInvalidArgument, "%s: bad scale", name);
-  if (k_st <= 0 || v_st <= 0 || k_st > (1 << 22) || v_st > (1 << 22))
-    return set_error(kUnsupported, "%s: K/V token strides must be in (0, 2^22] elements", name);
-  if (nblocks == 0) return kOk;
-  const Layout in{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                  static_cast<const uint16_t*>(v), q_st, q_sh, k_st, k_sh, v_st, v_sh};
-  const int64_t total = static_cast<int64_t>(nblocks) * heads;
-  if (total > (1ll << 31) - 1) return set_error(kUnsupported, "%s: too many blocks", name);
-  hipLaunchKernelGGL(window_attn_kernel<kBlockWaves>, dim3(static_cast<unsigned>(total)),
-                     dim3(kBlockWaves * 64), 0,
-                     static_cast<hipStream_t>(stream), in, blocks, grp_kv, grp_n, nblocks, heads,
-                     scale * kLog2e, static_cast<const uint16_t*>(gate), g_st, g_sh,
-                     static_cast<uint16_t*>(out), o_st, o_sh, lse, l_st, l_sh);
-  return check_launch(name);
+  return launch_window("vdn_window_attention", q, q_st, q_sh, k, k_st, k_sh, v, v_st, v_sh,
+                       blocks, nblocks, grp_kv, grp_n, heads, scale, gate, g_st, g_sh, out, o_st,
+                       o_sh, lse, l_st, l_sh, nullptr, stream);
+}
+
+// The same attention with the output quantized in the epilogue: query row q, head h ->
+// MXFP8 codes[q, 128 (chunk0 + h) ..] (row length kp) and the swizzled scales of those four
+// 32-blocks, bit-identical to vdn_mxfp8_quantize of the bf16 output. Rows with no query
+// are not written. Reference: the output projection's producer, quantize_activation
+// (src/models/ops/mxfp8_quant.py:77-90), applied to paper_window_attention's output.
+VDN_API int vdn_window_attention_mxfp8(const void* q, int64_t q_st, int64_t q_sh, const void* k,
+                                       int64_t k_st, int64_t k_sh, const void* v, int64_t v_st,
+                                       int64_t v_sh, const int* blocks, int nblocks,
+                                       const int* grp_kv, const int* grp_n, int heads,
+                                       float scale, const void* gate, int64_t g_st, int64_t g_sh,
+                                       void* codes, void* scales, int64_t kp, int chunk0,
+                                       void* stream) {
+  const MxDst mx{static_cast<uint8_t*>(codes), static_cast<uint8_t*>(scales), kp, chunk0};
+  return launch_window("vdn_window_attention_mxfp8", q, q_st, q_sh, k, k_st, k_sh, v, v_st,
+                       v_sh, blocks, nblocks, grp_kv, grp_n, heads, scale, gate, g_st, g_sh,
+                       nullptr, 0, 0, nullptr, 0, 0, &mx, stream);
 }

@@ -133,6 +133,40 @@ def _new_outputs(x: torch.Tensor, rows: int, k: int):
     return q, s, flag
 
 
+def empty_activation(rows: int, k: int, device):
+    """Codes [RP, KP] and flat swizzled scales for an MXFP8 activation that fused producers
+    (vdn_window_attention_mxfp8, vdn_vda_readout_mxfp8) fill chunk by chunk. The padding rows
+    rows .. RP-1 are zeroed here (codes 0, scale bytes 0), as the quantize producer leaves
+    them; every real row must then be written by the producers."""
+    rp, kp = padded_shape(rows, k)
+    q = torch.empty((rp, kp), dtype=torch.uint8, device=device)
+    s = torch.empty(scale_numel(rows, k), dtype=torch.uint8, device=device)
+    if rp > rows:
+        q[rows:].zero_()
+        # the scales of a 128-row block are one contiguous run of KP/128 x 512 bytes
+        s[(rows // 128) * (kp // 128) * 512:].zero_()
+    return q, s
+
+
+def mxfp8_destination(dest, rows: int, heads: int, device):
+    """Validates (codes, scales, chunk0) for a producer writing chunks chunk0 .. chunk0+heads-1
+    of rows [0, rows)."""
+    codes, scales, chunk0 = dest
+    if (codes.dtype != torch.uint8 or scales.dtype != torch.uint8 or codes.ndim != 2
+            or not codes.is_contiguous() or not scales.is_contiguous()
+            or codes.device != device or scales.device != device):
+        raise ValueError("MXFP8 destination must be contiguous uint8 codes [RP, KP] and scales "
+                         "on the producer's device")
+    rp, kp = codes.shape
+    if rp % 128 or kp % 128 or rp < rows or scales.numel() != rp * kp // 32:
+        raise ValueError("MXFP8 destination must be padded to 128 rows/columns with "
+                         "RP * KP / 32 scale bytes")
+    if isinstance(chunk0, bool) or not isinstance(chunk0, int) or chunk0 < 0 \
+            or (chunk0 + heads) * 128 > kp:
+        raise ValueError("chunk0 must leave room for one 128-column chunk per head")
+    return codes, scales, chunk0
+
+
 def launch_quantize(x: torch.Tensor):
     """bf16 [R,K] -> (codes u8 [RP,KP], flat swizzled scales u8). No finite check."""
     q, s, _ = _quantize(x)

@@ -19,6 +19,7 @@ from functools import lru_cache
 import torch
 
 from . import _lib
+from .mxfp8 import mxfp8_destination
 
 HEAD_DIM = 128
 
@@ -325,12 +326,15 @@ def vdn_linear_epilogue(readout, norm_weight, gate, eps):
 
 
 def linear_readout(q, state, norm_weight, gate, eps, frames, spatial, *, activate_q=True,
-                   out=None):
+                   out=None, out_mxfp8=None):
     """Fused q activation + readout + epilogue.
 
     q: raw [F*S, H, D] bf16 (any row/head stride; prepared q with activate_q=False);
     state: [F, H, D, D] bf16 from paper_gather; gate [F*S, H, D] bf16.
     Returns (or writes into `out`) [F*S, H*D] bf16 = RMSNorm(bf16(q'·stateᵀ))·w·gate.
+    `out_mxfp8` = (codes, scales, chunk0) instead quantizes the result in the kernel: head h of
+    row r becomes chunk chunk0 + h of row r of an MXFP8 activation (empty_activation),
+    byte-identical to quantize_activation of the bf16 result; returns None then.
     """
     _cuda(q, "q", torch.bfloat16)
     _cuda(state, "state", torch.bfloat16)
@@ -341,12 +345,21 @@ def linear_readout(q, state, norm_weight, gate, eps, frames, spatial, *, activat
         raise ValueError("readout geometry mismatch")
     state = state.contiguous()
     w = norm_weight.to(device=q.device).contiguous()
+    qs = (spatial * q.stride(0), q.stride(1), q.stride(0))
+    gs = (spatial * gate.stride(0), gate.stride(1), gate.stride(0))
+    if out_mxfp8 is not None:
+        if out is not None:
+            raise ValueError("out_mxfp8 excludes out")
+        codes, scales, chunk0 = mxfp8_destination(out_mxfp8, n, h, q.device)
+        _lib.call("vdn_vda_readout_mxfp8", q.data_ptr(), *qs, int(bool(activate_q)),
+                  state.data_ptr(), w.data_ptr(), _weight_flag(w), float(eps), gate.data_ptr(),
+                  *gs, codes.data_ptr(), scales.data_ptr(), codes.shape[1], chunk0, frames, h,
+                  spatial, _stream(q))
+        return None
     if out is None:
         out = torch.empty((n, h * d), dtype=torch.bfloat16, device=q.device)
     elif out.shape != (n, h * d) or out.stride(-1) != 1 or out.dtype != torch.bfloat16:
         raise ValueError("out must be bf16 [F*S, H*D]")
-    qs = (spatial * q.stride(0), q.stride(1), q.stride(0))
-    gs = (spatial * gate.stride(0), gate.stride(1), gate.stride(0))
     os_ = (spatial * out.stride(0), d, out.stride(0))
     _lib.call("vdn_vda_readout", q.data_ptr(), *qs, int(bool(activate_q)), state.data_ptr(),
               w.data_ptr(), _weight_flag(w), float(eps), gate.data_ptr(), *gs, out.data_ptr(),
@@ -357,12 +370,14 @@ def linear_readout(q, state, norm_weight, gate, eps, frames, spatial, *, activat
 # ---------------------------------------------------------------- orchestration ----
 
 def vda_forward(q_raw, k_raw, v_raw, beta, gate, alpha, bounds, num_frames, tokens_per_frame,
-                norm_weight, eps, *, chunk_size=8, bridge=True, text=None, out=None):
+                norm_weight, eps, *, chunk_size=8, bridge=True, text=None, out=None,
+                out_mxfp8=None):
     """The paper VDA branch body on raw projections (paper_stack.py:266-318).
 
     q_raw/k_raw/v_raw: [F*S, H, 128] bf16 raw projections; beta [F*S, H]; gate [F*S, H, 128];
     alpha [F, H, 128] fp32. `text` = (tk_raw, tv_raw, text_beta) adds the prompt's virtual
-    frame (its factors share the batch; half its injection seeds both scans).
+    frame (its factors share the batch; half its injection seeds both scans). `out` /
+    `out_mxfp8` as in linear_readout.
     """
     f, s = num_frames, tokens_per_frame
     h = q_raw.shape[1]
@@ -388,7 +403,8 @@ def vda_forward(q_raw, k_raw, v_raw, beta, gate, alpha, bounds, num_frames, toke
     del transitions, injections
     state = paper_gather(bank, alpha, plan, seed, torch.bfloat16, bridge)
     del bank
-    return linear_readout(q_raw, state, norm_weight, gate, eps, f, s, out=out)
+    return linear_readout(q_raw, state, norm_weight, gate, eps, f, s, out=out,
+                          out_mxfp8=out_mxfp8)
 
 
 def paper_readout(branch, xv, num_frames, tokens_per_frame, bounds, qkv_raw, frame_size=None,

@@ -17,6 +17,7 @@ from numbers import Real
 import torch
 
 from . import _lib
+from .mxfp8 import mxfp8_destination
 
 BLOCK_M = 256
 MAX_INTERVALS = 8
@@ -244,12 +245,16 @@ def prepare_paper_window_plan(layout: SequenceLayout, bounds, anchor_frames="non
 # ---------------------------------------------------------------------- attention ----
 
 def paper_window_attention(query, key, value, plan: PaperWindowPlan, scale=None, *,
-                           enabled=False, return_lse=False, nvtx=True, gate=None, out=None):
+                           enabled=False, return_lse=False, nvtx=True, gate=None, out=None,
+                           out_mxfp8=None):
     """[used+padding, H, D] -> fresh output of the same shape; padding rows are zero
     (paper_window.py:182-243). LSE (fp32 [rows, H], natural log) is -inf on padding.
     `gate` ([rows, H] or [rows, H, 1]) fuses apply_softmax_gate: out = bf16(bf16(o) * gate).
     `out` (optional bf16 [rows, H, D] view with unit channel stride) receives the result
-    instead of a fresh tensor, e.g. a column slice of a wider buffer."""
+    instead of a fresh tensor, e.g. a column slice of a wider buffer.
+    `out_mxfp8` = (codes, scales, chunk0) instead quantizes the output in the kernel: head h of
+    used row r becomes chunk chunk0 + h of row r of an MXFP8 activation (empty_activation),
+    byte-identical to quantize_activation of the bf16 output; returns None then."""
     if not enabled:
         raise RuntimeError("paper window attention is disabled; retain the existing caller path "
                            "or explicitly enable")
@@ -272,6 +277,22 @@ def paper_window_attention(query, key, value, plan: PaperWindowPlan, scale=None,
     if not math.isfinite(scale):
         raise ValueError("scale must be finite")
     rows, h, d = query.shape
+    if out_mxfp8 is not None:
+        if out is not None or return_lse:
+            raise ValueError("out_mxfp8 excludes out and return_lse")
+        codes, scales, chunk0 = mxfp8_destination(out_mxfp8, plan.layout.seq_len, h,
+                                                  query.device)
+        if gate is not None:
+            gate = _gate_rows(gate, plan.layout.seq_len, h)
+        dp = plan.device_plan
+        _lib.call("vdn_window_attention_mxfp8", query.data_ptr(), query.stride(0),
+                  query.stride(1), key.data_ptr(), key.stride(0), key.stride(1),
+                  value.data_ptr(), value.stride(0), value.stride(1), dp.blocks.data_ptr(),
+                  dp.nblocks, dp.intervals.data_ptr(), dp.counts.data_ptr(), h, scale,
+                  _lib.ptr(gate), 0 if gate is None else gate.stride(0),
+                  0 if gate is None else gate.stride(1), codes.data_ptr(), scales.data_ptr(),
+                  codes.shape[1], chunk0, _lib.stream(query.device))
+        return None
     if out is None:
         out = torch.empty((rows, h, d), dtype=query.dtype, device=query.device)
     elif (out.shape != (rows, h, d) or out.dtype != query.dtype or out.device != query.device
@@ -284,11 +305,7 @@ def paper_window_attention(query, key, value, plan: PaperWindowPlan, scale=None,
         if lse is not None:
             lse[used:].fill_(-float("inf"))
     if gate is not None:
-        if gate.shape[0] < used or gate.numel() != gate.shape[0] * h:
-            raise ValueError("gate must be [rows, H] or [rows, H, 1] covering the used rows")
-        gate = gate.reshape(gate.shape[0], h)
-        if gate.dtype != torch.bfloat16:
-            gate = gate.to(torch.bfloat16)
+        gate = _gate_rows(gate, used, h)
     dp = plan.device_plan
     _lib.call("vdn_window_attention", query.data_ptr(), query.stride(0), query.stride(1),
               key.data_ptr(), key.stride(0), key.stride(1), value.data_ptr(), value.stride(0),
@@ -299,6 +316,13 @@ def paper_window_attention(query, key, value, plan: PaperWindowPlan, scale=None,
               0 if lse is None else lse.stride(0), 0 if lse is None else lse.stride(1),
               _lib.stream(query.device))
     return (out, lse) if return_lse else out
+
+
+def _gate_rows(gate, used, h):
+    if gate.shape[0] < used or gate.numel() != gate.shape[0] * h:
+        raise ValueError("gate must be [rows, H] or [rows, H, 1] covering the used rows")
+    gate = gate.reshape(gate.shape[0], h)
+    return gate if gate.dtype == torch.bfloat16 else gate.to(torch.bfloat16)
 
 
 def apply_softmax_gate(softmax_out, gate, inference=False):
