@@ -138,6 +138,14 @@ __device__ __forceinline__ void load_table8(const void* __restrict__ t, int f32,
   }
 }
 
+__device__ __forceinline__ void unpack_bf16x8(const u32x4 w, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffff));
+    f[2 * i + 1] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
+  }
+}
+
 // Sixteen padded rows per workgroup (one per wave, kS 8-column slices per lane). When the
 // rows share one AdaLN table row (the usual case: one timestep for a whole clip) the weight,
 // scale and shift rows are staged once in LDS as fp32, so they are read from L2 once per 16
@@ -194,27 +202,35 @@ prenorm_quantize_rows_kernel(const uint16_t* __restrict__ x, int64_t rows, int64
     if (r >= rp) return;  // whole wave (no barrier follows)
     const bool in_row = r < rows;
     const int64_t table_row = in_row ? indices[r] : 0;
-    float v[kS][8];
-    bool bad = false;
+    // the row stays in registers as packed bf16 (kS x 4 VGPRs) and is unpacked where used
+    u32x4 raw[kS];
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < kS; ++j) {
-      const int64_t sl = lane + 64 * j;
-      load_row8<true>(x, sl < slices ? r : rows, sl * 8, rows, k, stride, v[j], bad);
+      const int64_t c0 = (lane + 64 * j) * 8;
+      raw[j] = u32x4{0u, 0u, 0u, 0u};
+      if (in_row && c0 < k) raw[j] = *reinterpret_cast<const u32x4*>(x + r * stride + c0);
+      float f[8];
+      unpack_bf16x8(raw[j], f);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ss += v[j][i] * v[j][i];
+      for (int i = 0; i < 8; ++i) ss += f[i] * f[i];
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
     const float ms = ss / static_cast<float>(k) + eps;
     const float inv_rms = static_cast<float>(1.0 / sqrt(static_cast<double>(ms)));
+    // A nonfinite input makes its row's sum of squares nonfinite and so some output of the
+    // row nonfinite: testing the outputs covers the inputs.
+    bool bad = false;
 #pragma unroll
     for (int j = 0; j < kS; ++j) {
       const int64_t sl = lane + 64 * j;
       if (sl >= slices) break;  // slices beyond KP: none of this lane's later ones exist
       const int64_t c0 = sl * 8;
+      float v[8];
       if (in_row && c0 < k) {
-        float w[8], sc[8], sh[8];
+        float xv[8], w[8], sc[8], sh[8];
+        unpack_bf16x8(raw[j], xv);
         if (shared_row) {
 #pragma unroll
           for (int i = 0; i < 8; i += 4) {
@@ -235,22 +251,22 @@ prenorm_quantize_rows_kernel(const uint16_t* __restrict__ x, int64_t rows, int64
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float t = (v[j][i] * inv_rms) * w[i];
+          const float t = (xv[i] * inv_rms) * w[i];
           const float u = 1.0f + sc[i];
-          v[j][i] = round_bf16(t * u + sh[i]);
-          bad |= !(fabsf(v[j][i]) < INFINITY);
+          v[i] = round_bf16(t * u + sh[i]);
+          bad |= !(fabsf(v[i]) < INFINITY);
         }
         if (y != nullptr) {
           u32x4 packed;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) packed[i] = pack_bf16x2(v[j][2 * i], v[j][2 * i + 1]);
+          for (int i = 0; i < 4; ++i) packed[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
           *reinterpret_cast<u32x4*>(y + r * k + c0) = packed;
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[j][i] = 0.f;
+        for (int i = 0; i < 8; ++i) v[i] = 0.f;
       }
-      quantize_store8(v[j], lane & 15, r, sl >> 4, kp, q, s);
+      quantize_store8(v, lane & 15, r, sl >> 4, kp, q, s);
     }
     const bool any_bad = __ballot(bad) != 0;
     if (lane == 0) finite[r] = any_bad ? 0 : 1;
