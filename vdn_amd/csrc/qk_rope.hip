@@ -7,7 +7,8 @@
 //       r_i = -n_{i+R/2} (i < R/2), n_{i-R/2} (R/2 <= i < R); c, s = table values in bf16
 //   channels i >= R pass n through.
 // A row is held by D/8 lanes (8 channels each); the rotate partner is exchanged through a
-// per-row LDS line, which keeps arbitrary even R <= D exact.
+// per-row LDS line, which keeps arbitrary even R <= D exact (qk_rope_kernel), or, for the
+// common D = R = 128, through a DPP lane rotation (qk_rope_row128_kernel).
 #include "common.h"
 
 #include <math.h>
@@ -140,6 +141,68 @@ qk_rope_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float eps,
   }
 }
 
+// Fast form for 128-channel heads rotated over the full width (R = 128) or not rotated
+// (R = 0), with unit channel strides and 16-byte rows: the rotate-half partner of a lane's 8
+// channels is 8 lanes away in the same 16-lane row, so a DPP row rotation by 8 exchanges it
+// (no LDS line, no barrier), and a workgroup walks kGroups groups of 16 rows. Arithmetic and
+// rounding are those of qk_rope_kernel.
+constexpr int kRopeGroups = 8;
+
+__device__ __forceinline__ float row_ror8(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                               0x128, 0xf, 0xf, false));
+}
+
+__global__ void __launch_bounds__(256)
+qk_rope_row128_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float eps,
+                      const void* __restrict__ cos_t, const void* __restrict__ sin_t,
+                      int64_t c_st, int64_t s_st, int table_f32, int rot) {
+#pragma clang fp contract(off)
+  constexpr int kD = 128;
+  const int sub = threadIdx.x & 15;
+  const RopeArgs& a = blockIdx.y == 0 ? q : k;
+  const int64_t rows = tokens * heads;
+  float wv[8];
+  load8(a.w, a.w_f32, sub * 8, false, wv);
+  for (int it = 0; it < kRopeGroups; ++it) {
+    const int64_t row =
+        (static_cast<int64_t>(blockIdx.x) * kRopeGroups + it) * 16 + (threadIdx.x >> 4);
+    if (row >= rows) break;  // uniform per 16-lane row group; nothing below synchronizes more
+    const int64_t t = row / heads;
+    const int h = static_cast<int>(row - t * heads);
+    float v[8];
+    load8(a.x + t * a.st + h * a.sh, 0, sub * 8, false, v);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) ss += __shfl_xor(ss, off, 16);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(kD) + eps);
+    float n[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) n[i] = round_bf16((v[i] * inv) * wv[i]);
+    float o[8];
+    if (rot == kD) {
+      float cvv[8], svv[8];
+      load8(cos_t, table_f32, t * c_st + sub * 8, true, cvv);
+      load8(sin_t, table_f32, t * s_st + sub * 8, true, svv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float partner = row_ror8(n[i]);   // channel c + 64 (lanes 0-7) or c - 64
+        const float other = sub < 8 ? -partner : partner;
+        o[i] = round_bf16(round_bf16(n[i] * cvv[i]) + round_bf16(other * svv[i]));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = n[i];
+    }
+    u32x4 packed;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) packed[i] = pack_bf16x2(o[2 * i], o[2 * i + 1]);
+    *reinterpret_cast<u32x4*>(a.out + row * kD + sub * 8) = packed;
+  }
+}
+
 }  // namespace
 }  // namespace vdn
 
@@ -193,7 +256,14 @@ VDN_API int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64
                           q_only ? 1 : 2),                                                      \
                      dim3(256), 0, st, qa, ka, tokens, heads, eps, cos_t, sin_t, c_st, c_sd,    \
                      s_st, s_sd, tf, r);
-  if (head_dim == 64) {
+  if (head_dim == 128 && vec && (r == 0 || r == 128)) {
+    const int64_t per_block = 16 * kRopeGroups;
+    hipLaunchKernelGGL(qk_rope_row128_kernel,
+                       dim3(static_cast<unsigned>((rows + per_block - 1) / per_block),
+                            q_only ? 1 : 2),
+                       dim3(256), 0, st, qa, ka, tokens, heads, eps, cos_t, sin_t, c_st, s_st,
+                       tf, r);
+  } else if (head_dim == 64) {
     VDN_ROPE(64)
   } else if (head_dim == 128) {
     VDN_ROPE(128)
