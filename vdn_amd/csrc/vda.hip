@@ -632,7 +632,7 @@ struct MxDst {
 };
 
 // RMSNorm(y)·w·gate of one lane's 8 values, rounded to bf16 (as stored by the bf16 form).
-__device__ __forceinline__ void norm_gate8(const float* y, const float* w, const uint16_t* gsrc,
+__device__ __forceinline__ void norm_gate8(const float* y, const float* w, const u32x4 graw,
                                            float eps, float* o) {
   float ss = 0.f;
 #pragma unroll
@@ -640,7 +640,7 @@ __device__ __forceinline__ void norm_gate8(const float* y, const float* w, const
   ss = sum16(ss);
   const float inv = 1.0f / sqrtf(ss / static_cast<float>(kD) + eps);
   float gv[8];
-  unpack8(*reinterpret_cast<const u32x4*>(gsrc), gv);
+  unpack8(graw, gv);
 #pragma unroll
   for (int i = 0; i < 8; ++i) o[i] = round_bf16(y[i] * inv * w[i] * gv[i]);
 }
@@ -648,17 +648,21 @@ __device__ __forceinline__ void norm_gate8(const float* y, const float* w, const
 __device__ __forceinline__ void norm_gate_store8(float* y, const float* w, const uint16_t* gsrc,
                                                  uint16_t* dst, float eps) {
   float o[8];
-  norm_gate8(y, w, gsrc, eps, o);
+  norm_gate8(y, w, *reinterpret_cast<const u32x4*>(gsrc), eps, o);
   *reinterpret_cast<u32x4*>(dst) = pack8(o);
 }
 
-// Fused readout: per (frame, head, 64-token tile): q' = bf16(L2(SiLU(q_raw))) (optional),
+// Fused readout: per (frame, head, kQT-token tile): q' = bf16(L2(SiLU(q_raw))) (optional),
 // y = bf16(q' · stateᵀ) on bf16 MFMA, then RMSNorm·w·gate into out[f*S + s, h*D + c].
-constexpr int kQT = 64;
+// A workgroup of kRoWaves waves reads out kQT = 16 kRoWaves tokens of one (frame, head): the
+// 32 KB state is staged once per kQT tokens.
+constexpr int kRoWaves = 8;
+constexpr int kQT = 16 * kRoWaves;
+constexpr int kRoThreads = 64 * kRoWaves;
 constexpr int kQRow = 136;  // padded bf16 row (272 bytes)
 
 template <bool kMx>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(kRoThreads)
 vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
                    const void* __restrict__ weight, int weight_f32, float eps, View gv,
                    uint16_t* __restrict__ out, int64_t o_sf, int64_t o_sh, int64_t o_ss,
@@ -670,14 +674,23 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
   const int f = fh / heads, h = fh % heads;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lane16 = tid & 15;
   const int s0 = tile * kQT;
+  constexpr int kPasses = kQT / (kRoThreads / 16);
+  // the gate rows of the epilogue are loaded first, so they arrive during the matmul
+  u32x4 gate_raw[kPasses];
+#pragma unroll
+  for (int pass = 0; pass < kPasses; ++pass) {
+    const int s = s0 + pass * (kRoThreads / 16) + (tid >> 4);
+    gate_raw[pass] = s < spatial ? *reinterpret_cast<const u32x4*>(gv.at(f, h, s) + lane16 * 8)
+                                 : u32x4{0u, 0u, 0u, 0u};
+  }
   const uint16_t* st = state + static_cast<int64_t>(fh) * kD * kD;
-  for (int idx = tid * 8; idx < kD * kD; idx += 256 * 8)
+  for (int idx = tid * 8; idx < kD * kD; idx += kRoThreads * 8)
     *reinterpret_cast<u32x4*>(&sState[(idx >> 7) * kQRow + (idx & 127)]) =
         *reinterpret_cast<const u32x4*>(st + idx);
-  // q tile: 16 tokens per pass (one 16-lane group per token)
+  // q tile: kRoThreads / 16 tokens per pass (one 16-lane group per token)
 #pragma unroll
-  for (int pass = 0; pass < kQT / 16; ++pass) {
-    const int r = pass * 16 + (tid >> 4);
+  for (int pass = 0; pass < kQT / (kRoThreads / 16); ++pass) {
+    const int r = pass * (kRoThreads / 16) + (tid >> 4);
     const int s = s0 + r;
     float v[8];
     if (s < spatial) {
@@ -718,20 +731,19 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
     w[i] = weight_f32 ? static_cast<const float*>(weight)[lane16 * 8 + i]
                       : bf16_bits_to_f32(static_cast<const uint16_t*>(weight)[lane16 * 8 + i]);
 #pragma unroll
-  for (int pass = 0; pass < kQT / 16; ++pass) {
-    const int r = pass * 16 + (tid >> 4);
+  for (int pass = 0; pass < kQT / (kRoThreads / 16); ++pass) {
+    const int r = pass * (kRoThreads / 16) + (tid >> 4);
     const int s = s0 + r;
     if (s >= spatial) continue;  // uniform per 16-lane group
     float y[8];
     unpack8(*reinterpret_cast<const u32x4*>(&sQ[r * kQRow + lane16 * 8]), y);
+    float o[8];
+    norm_gate8(y, w, gate_raw[pass], eps, o);
     if constexpr (kMx) {
-      float o[8];
-      norm_gate8(y, w, gv.at(f, h, s) + lane16 * 8, eps, o);
       quantize_store8(o, lane16, static_cast<int64_t>(f) * spatial + s, mx.chunk0 + h, mx.kp,
                       mx.codes, mx.scales);
     } else {
-      norm_gate_store8(y, w, gv.at(f, h, s) + lane16 * 8,
-                       out + f * o_sf + h * o_sh + s * o_ss + lane16 * 8, eps);
+      *reinterpret_cast<u32x4*>(out + f * o_sf + h * o_sh + s * o_ss + lane16 * 8) = pack8(o);
     }
   }
 }
@@ -933,7 +945,7 @@ int launch_readout(const char* name, const void* q, int64_t q_sf, int64_t q_sh, 
   const int tiles = (spatial + kQT - 1) / kQT;
   const View qv{static_cast<const uint16_t*>(q), q_sf, q_sh, q_ss};
   const View gv{static_cast<const uint16_t*>(gate), g_sf, g_sh, g_ss};
-  const dim3 grid(frames * heads * tiles), block(256);
+  const dim3 grid(frames * heads * tiles), block(kRoThreads);
   const auto st = static_cast<hipStream_t>(stream);
   if (mx != nullptr)
     hipLaunchKernelGGL(vda_readout_kernel<true>, grid, block, 0, st, qv, activate_q,
