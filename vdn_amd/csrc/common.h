@@ -37,6 +37,31 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
+// Lane exchanges inside 16-lane DPP rows (VALU, no LDS traffic). kCtrl is the DPP control:
+// quad_perm 0xB1 = lane ^ 1, 0x4E = lane ^ 2; 0x141 = half-row mirror (i <- 7 - i within 8);
+// 0x140 = row mirror (i <- 15 - i); 0x100 + n = row_shl n (i <- i + n, lanes past the row's
+// end read 0); 0x120 + n = row rotate right by n.
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xf, 0xf, false));
+}
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, dpp_u32<kCtrl>(__builtin_bit_cast(uint32_t, v)));
+}
+
+// Sum over a 16-lane DPP row. Bit-identical to the xor butterfly over lanes ^1, ^2, ^4, ^8:
+// after the two quad steps every lane of quad k holds its total q_k, the half-row mirror
+// adds the neighbouring quad (q0 + q1, q2 + q3) and the row mirror the other half.
+__device__ __forceinline__ float sum16(float v) {
+  v += dpp_f32<0xB1>(v);
+  v += dpp_f32<0x4E>(v);
+  v += dpp_f32<0x141>(v);
+  v += dpp_f32<0x140>(v);
+  return v;
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }

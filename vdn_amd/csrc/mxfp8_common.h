@@ -63,15 +63,17 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 #pragma clang fp contract(on)
 
 // Quantizes the 8 values a lane holds (one quarter of a 32-block), stores the 8 codes
-// and, from lane 0 of each 16-lane group, the chunk's 4 scale bytes.
+// and, from lane 0 of each 16-lane group, the chunk's 4 scale bytes. A group is one DPP
+// row (lanes 16k .. 16k + 15) whose lanes are all active: the amax and the scale bytes move
+// between its lanes by DPP.
 __device__ __forceinline__ void quantize_store8(const float* v, int lane16, int64_t r, int64_t chunk,
                                                 int64_t kp, uint8_t* __restrict__ q,
                                                 uint8_t* __restrict__ s) {
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 16));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 16));
+  amax = fmaxf(amax, dpp_f32<0xB1>(amax));  // lane ^ 1
+  amax = fmaxf(amax, dpp_f32<0x4E>(amax));  // lane ^ 2
   float inv;
   const uint32_t scale = e8m0_from_amax(amax, &inv);
   float scaled[8];
@@ -79,9 +81,9 @@ __device__ __forceinline__ void quantize_store8(const float* v, int lane16, int6
   for (int i = 0; i < 8; ++i) scaled[i] = v[i] * inv;
   const u32x2 codes = e4m3x8(scaled);
   *reinterpret_cast<u32x2*>(q + r * kp + chunk * 128 + lane16 * 8) = codes;
-  const uint32_t s1 = __shfl_down(scale, 4, 16);
-  const uint32_t s2 = __shfl_down(scale, 8, 16);
-  const uint32_t s3 = __shfl_down(scale, 12, 16);
+  const uint32_t s1 = dpp_u32<0x104>(scale);  // lane + 4 of the 16-lane row
+  const uint32_t s2 = dpp_u32<0x108>(scale);
+  const uint32_t s3 = dpp_u32<0x10C>(scale);
   if (lane16 == 0) {
     const uint32_t word = scale | (s1 << 8) | (s2 << 16) | (s3 << 24);
     *reinterpret_cast<uint32_t*>(s + swizzled_scale_offset(r, chunk * 4, kp >> 7)) = word;

@@ -148,11 +148,80 @@ __device__ __forceinline__ void unpack_bf16x8(const u32x4 w, float* f) {
 
 // Sixteen padded rows per workgroup (one per wave, kS 8-column slices per lane). When the
 // rows share one AdaLN table row (the usual case: one timestep for a whole clip) the weight,
-// scale and shift rows are staged once in LDS as fp32, so they are read from L2 once per 16
-// rows instead of once per row; otherwise each row reads its own table row. Arithmetic and
-// rounding are those of prenorm_quantize_kernel.
+// 1 + scale and shift rows are staged once in LDS as fp32, so they are read from L2 once per
+// 16 rows instead of once per row; otherwise each row reads its own table row. Arithmetic
+// and rounding are those of prenorm_quantize_kernel. (A wave that walks several rows is
+// slower: its next row's loads wait for the current row's arithmetic, while fresh waves
+// of the next workgroups overlap them.)
 constexpr int kPrenormRows = 16;
 constexpr int kPrenormThreads = 64 * kPrenormRows;
+
+// One row of kCols = 512 kS columns (every slice real) whose weight, 1 + scale and shift
+// rows are staged in `tab`: the arithmetic and rounding of the general path below in
+// straight-line code. The bf16 results stay packed (the rounding conversion is the
+// packing); a bf16 is nonfinite iff its magnitude bits reach 0x7f80, so one packed max per
+// word tests two of them.
+template <int kS>
+__device__ __forceinline__ void prenorm_row_straight(const uint16_t* __restrict__ xrow,
+                                                     const float (*tab)[64 * kS * 8], float eps,
+                                                     int64_t r, int64_t kp,
+                                                     uint16_t* __restrict__ y,
+                                                     uint8_t* __restrict__ q,
+                                                     uint8_t* __restrict__ s,
+                                                     uint8_t* __restrict__ finite) {
+#pragma clang fp contract(off)
+  constexpr int kCols = 64 * kS * 8;
+  const int lane = threadIdx.x & 63;
+  u32x4 raw[kS];
+#pragma unroll
+  for (int j = 0; j < kS; ++j)
+    raw[j] = *reinterpret_cast<const u32x4*>(xrow + (lane + 64 * j) * 8);
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kS; ++j) {
+    float f[8];
+    unpack_bf16x8(raw[j], f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += f[i] * f[i];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+  const float ms = ss / static_cast<float>(kCols) + eps;
+  const float inv_rms = static_cast<float>(1.0 / sqrt(static_cast<double>(ms)));
+  u16x2 mag = {0, 0};
+#pragma unroll
+  for (int j = 0; j < kS; ++j) {
+    const int c0 = (lane + 64 * j) * 8;
+    float xv[8], w[8], u[8], sh[8];
+    unpack_bf16x8(raw[j], xv);
+#pragma unroll
+    for (int i = 0; i < 8; i += 4) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(&tab[0][c0 + i]);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(&tab[1][c0 + i]);
+      const f32x4 c = *reinterpret_cast<const f32x4*>(&tab[2][c0 + i]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        w[i + e] = a[e];
+        u[i + e] = b[e];
+        sh[i + e] = c[e];
+      }
+    }
+    u32x4 packed;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float t0 = (xv[2 * i] * inv_rms) * w[2 * i];
+      const float t1 = (xv[2 * i + 1] * inv_rms) * w[2 * i + 1];
+      packed[i] = pack_bf16x2(t0 * u[2 * i] + sh[2 * i], t1 * u[2 * i + 1] + sh[2 * i + 1]);
+      mag = __builtin_elementwise_max(mag, __builtin_bit_cast(u16x2, packed[i] & 0x7fff7fffu));
+    }
+    if (y != nullptr) *reinterpret_cast<u32x4*>(y + r * kCols + c0) = packed;
+    float v[8];
+    unpack_bf16x8(packed, v);
+    quantize_store8(v, lane & 15, r, 4 * j + (lane >> 4), kp, q, s);
+  }
+  const bool any_bad = __ballot(mag[0] >= 0x7f80 || mag[1] >= 0x7f80) != 0;
+  if (lane == 0) finite[r] = any_bad ? 0 : 1;
+}
 
 template <int kS>
 __global__ void __launch_bounds__(kPrenormThreads)
@@ -191,7 +260,7 @@ prenorm_quantize_rows_kernel(const uint16_t* __restrict__ x, int64_t rows, int64
                           : bf16_bits_to_f32(static_cast<const uint16_t*>(shift)[ho]);
         }
         tab[0][cc] = wv;
-        tab[1][cc] = sv;
+        tab[1][cc] = 1.0f + sv;  // the (1 + scale) factor, formed once per column
         tab[2][cc] = hv;
       }
     }
@@ -201,6 +270,10 @@ prenorm_quantize_rows_kernel(const uint16_t* __restrict__ x, int64_t rows, int64
     const int64_t r = r0 + wave;
     if (r >= rp) return;  // whole wave (no barrier follows)
     const bool in_row = r < rows;
+    if (__builtin_amdgcn_readfirstlane(shared_row && in_row && k == kCols)) {  // wave-uniform
+      prenorm_row_straight<kS>(x + r * stride, tab, eps, r, kp, y, q, s, finite);
+      return;
+    }
     const int64_t table_row = in_row ? indices[r] : 0;
     // the row stays in registers as packed bf16 (kS x 4 VGPRs) and is unpacked where used
     u32x4 raw[kS];
@@ -229,7 +302,7 @@ prenorm_quantize_rows_kernel(const uint16_t* __restrict__ x, int64_t rows, int64
       const int64_t c0 = sl * 8;
       float v[8];
       if (in_row && c0 < k) {
-        float xv[8], w[8], sc[8], sh[8];
+        float xv[8], w[8], u[8], sh[8];
         unpack_bf16x8(raw[j], xv);
         if (shared_row) {
 #pragma unroll
@@ -240,20 +313,21 @@ prenorm_quantize_rows_kernel(const uint16_t* __restrict__ x, int64_t rows, int64
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               w[i + e] = a[e];
-              sc[i + e] = b[e];
+              u[i + e] = b[e];
               sh[i + e] = c[e];
             }
           }
         } else {
           load_table8(weight, weight_f32, c0, w);
-          load_table8(scale, tables_f32, table_row * scale_stride + c0, sc);
+          load_table8(scale, tables_f32, table_row * scale_stride + c0, u);
           load_table8(shift, tables_f32, table_row * shift_stride + c0, sh);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) u[i] = 1.0f + u[i];
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const float t = (xv[i] * inv_rms) * w[i];
-          const float u = 1.0f + sc[i];
-          v[i] = round_bf16(t * u + sh[i]);
+          v[i] = round_bf16(t * u[i] + sh[i]);
           bad |= !(fabsf(v[i]) < INFINITY);
         }
         if (y != nullptr) {

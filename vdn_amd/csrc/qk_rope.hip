@@ -175,8 +175,7 @@ qk_rope_row128_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float e
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) ss += __shfl_xor(ss, off, 16);
+    ss = sum16(ss);
     const float inv = 1.0f / sqrtf(ss / static_cast<float>(kD) + eps);
     float n[8];
 #pragma unroll

@@ -46,15 +46,6 @@ __device__ __forceinline__ float silu(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * kMinusLog2e));
 }
 
-// Sum over the 16 lanes of a 16-lane group (xor butterfly).
-__device__ __forceinline__ float sum16(float v) {
-  v += __shfl_xor(v, 1, 16);
-  v += __shfl_xor(v, 2, 16);
-  v += __shfl_xor(v, 4, 16);
-  v += __shfl_xor(v, 8, 16);
-  return v;
-}
-
 __device__ __forceinline__ void unpack8(const u32x4 w, float* v) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
