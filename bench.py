@@ -30,7 +30,8 @@ D = 128
 
 GEMMS = ("vdn_mxfp8_gemm", "vdn_mxfp8_gemm_act_quantize")
 VDA_ENTRIES = ("vdn_vda_statistics", "vdn_vda_factors", "vdn_vda_compose", "vdn_vda_scan",
-               "vdn_vda_log_prefix", "vdn_vda_gather", "vdn_vda_readout", "vdn_vda_readout_mxfp8")
+               "vdn_vda_log_prefix", "vdn_vda_gather", "vdn_vda_readout", "vdn_vda_readout_mxfp8",
+               "vdn_vda_readout_gated")
 ATTENTION = ("vdn_window_attention", "vdn_window_attention_mxfp8")
 
 
@@ -99,6 +100,11 @@ def work(name, a, plans):
         f, h, s = a[17], a[18], a[19]
         return (2.0 * f * s * h * D * D,
                 2 * f * s * h * D * 2 + f * s * h * D * (1 + 1 / 32) + f * h * D * D * 2)
+    if name == "vdn_vda_readout_gated":   # q and the gate's down rows read; gate formed inside
+        f, h, s, mx = a[21], a[22], a[23], a[17] is not None
+        out = f * s * h * D * ((1 + 1 / 32) if mx else 2)
+        return (4.0 * f * s * h * D * D,
+                f * s * h * D * 2 + f * s * D * 2 + h * D * (D + 1) * 2 + f * h * D * D * 2 + out)
     return 0.0, 0.0
 
 

@@ -199,6 +199,22 @@ int vdn_vda_readout_mxfp8(const void* q, int64_t q_sf, int64_t q_sh, int64_t q_s
                           void* codes, void* scales, int64_t kp, int chunk0, int frames,
                           int heads, int spatial, void* stream);
 
+/* vdn_vda_readout with the linear branch's low-rank output gate formed in the kernel instead
+ * of read: gate[t, h, c] = bf16(sigmoid(bf16(down[t] . up_w[h*128 + c] + up_b[h*128 + c]))),
+ * with down [frames*spatial, 128] bf16 rows at row stride d_st (elements), up_w
+ * [heads*128, 128] bf16, up_b [heads*128] bf16. Exactly one destination: bf16 `out` (strides
+ * as vdn_vda_readout; codes = NULL) or MXFP8 `codes`/`scales`/`kp`/`chunk0` (as
+ * vdn_vda_readout_mxfp8; out = NULL).
+ * Replaces: output_gate(xv) (OutputGate.forward, src/models/attention_gates.py:52-55) +
+ * the readout of paper_readout (src/models/linear_attention/paper_stack.py:315-318).
+ */
+int vdn_vda_readout_gated(const void* q, int64_t q_sf, int64_t q_sh, int64_t q_ss,
+                          int activate_q, const void* state, const void* weight, int weight_f32,
+                          float eps, const void* down, int64_t d_st, const void* up_w,
+                          const void* up_b, void* out, int64_t o_sf, int64_t o_sh, int64_t o_ss,
+                          void* codes, void* scales, int64_t kp, int chunk0, int frames,
+                          int heads, int spatial, void* stream);
+
 /*
  * RMSNorm(128) * weight * gate of a frame-major readout [frames, heads, spatial, 128] bf16.
  * Replaces: vdn_linear_epilogue (src/models/linear_attention/paper_sglang.py:406-437).

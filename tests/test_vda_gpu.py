@@ -249,3 +249,86 @@ def test_readout_mxfp8_equals_quantized_bf16_readout(device, chunk0):
                              out_mxfp8=(codes, scales, chunk0)) is None
     assert torch.equal(codes, rq)
     assert torch.equal(scales, rs)
+
+
+def _gate_operands(n, h, g, device):
+    down = (torch.randn(n, 208, generator=g) * 0.5).bfloat16().to(device)[:, 80:]
+    up_w = (torch.randn(h * 128, 128, generator=g) * 0.1).bfloat16().to(device)
+    up_b = (torch.randn(h * 128, generator=g) * 0.5).bfloat16().to(device)
+    return down, up_w, up_b
+
+
+@torch.no_grad()
+def test_gated_readout_forms_the_output_gate(device):
+    """With q = ones, state = identity and unit weights the readout returns the gate itself
+    (RMSNorm of a constant row is 1 - 5e-7, which bf16 rounding absorbs), so the gate formed
+    in the kernel is compared with OutputGate's torch composition sigmoid(up(down)) on a
+    strided down view: equal but for one-ulp bf16 flips where the two GEMMs' fp32 sums
+    straddle a rounding boundary."""
+    frames, spatial, h = 2, 131, 3
+    n = frames * spatial
+    g = torch.Generator().manual_seed(5)
+    down, up_w, up_b = _gate_operands(n, h, g, device)
+    q = torch.ones(n, h, 128, dtype=torch.bfloat16, device=device)
+    state = torch.eye(128).expand(frames, h, 128, 128).bfloat16().contiguous().to(device)
+    w = torch.ones(128, device=device)
+    out = vv.linear_readout(q, state, w, vv.OutputGateProjection(down, up_w, up_b), 1e-6, frames,
+                            spatial, activate_q=False)
+    ref = torch.sigmoid(F.linear(down, up_w, up_b))
+    diff = (out.float() - ref.float()).abs()
+    ulp = torch.finfo(torch.bfloat16).eps * ref.float().abs()
+    assert bool((diff <= ulp).all()), diff.max().item()
+    assert (diff == 0).float().mean().item() > 0.99
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("chunk0", [0, 3])
+def test_gated_readout_matches_the_read_gate(device, chunk0):
+    """The gated readout against the readout of the torch-formed gate (activated q), in bf16
+    and into MXFP8, where it must equal quantize_activation of its own bf16 result."""
+    from vdn_amd import mxfp8 as vm
+    frames, spatial, h = 3, 70, 3
+    n = frames * spatial
+    g = torch.Generator().manual_seed(8)
+    q = torch.randn(n, h, 128, generator=g).bfloat16().to(device)
+    state = (torch.randn(frames, h, 128, 128, generator=g) * 0.1).bfloat16().to(device)
+    w = (torch.rand(128, generator=g) + 0.5).to(device)
+    down, up_w, up_b = _gate_operands(n, h, g, device)
+    gp = vv.OutputGateProjection(down, up_w, up_b)
+    gate = torch.sigmoid(F.linear(down, up_w, up_b)).view(n, h, 128)
+    ref = vv.linear_readout(q, state, w, gate, 1e-6, frames, spatial)
+    got = vv.linear_readout(q, state, w, gp, 1e-6, frames, spatial)
+    close_rel(got, ref, 2e-3)
+    width = (chunk0 + h) * 128
+    wide = torch.zeros(n, width, device=device, dtype=torch.bfloat16)
+    wide[:, chunk0 * 128:] = got
+    rq, rs = vm.launch_quantize(wide)
+    codes, scales = vm.empty_activation(n, width, device)
+    codes.zero_()
+    scales.copy_(rs)
+    assert vv.linear_readout(q, state, w, gp, 1e-6, frames, spatial,
+                             out_mxfp8=(codes, scales, chunk0)) is None
+    assert torch.equal(codes, rq)
+    assert torch.equal(scales, rs)
+
+
+def test_gated_readout_rejects_bad_operands(device):
+    from vdn_amd import _lib
+    frames, spatial, h = 1, 16, 2
+    n = frames * spatial
+    g = torch.Generator().manual_seed(1)
+    down, up_w, up_b = _gate_operands(n, h, g, device)
+    q = torch.randn(n, h, 128, generator=g).bfloat16().to(device)
+    state = torch.zeros(frames, h, 128, 128, dtype=torch.bfloat16, device=device)
+    w = torch.ones(128, device=device)
+    with pytest.raises(ValueError, match="up_weight"):
+        vv.linear_readout(q, state, w, vv.OutputGateProjection(down, up_w[:128], up_b), 1e-6,
+                          frames, spatial)
+    with pytest.raises(ValueError, match="down"):
+        vv.linear_readout(q, state, w, vv.OutputGateProjection(down[:, :64], up_w, up_b), 1e-6,
+                          frames, spatial)
+    with pytest.raises(RuntimeError, match="exactly one of out and codes"):
+        _lib.call("vdn_vda_readout_gated", q.data_ptr(), spatial * q.stride(0), q.stride(1),
+                  q.stride(0), 1, state.data_ptr(), w.data_ptr(), 1, 1e-6, down.data_ptr(),
+                  down.stride(0), up_w.data_ptr(), up_b.data_ptr(), None, 0, 0, 0, None, None, 0,
+                  0, frames, h, spatial, _lib.stream(q.device))

@@ -56,6 +56,9 @@ SIGNATURES = {
                                    _i64, _i32, _ptr],
     "vdn_vda_readout_mxfp8": [_ptr, _i64, _i64, _i64, _i32, _ptr, _ptr, _i32, _f32, _ptr, _i64,
                               _i64, _i64, _ptr, _ptr, _i64, _i32, _i32, _i32, _i32, _ptr],
+    "vdn_vda_readout_gated": [_ptr, _i64, _i64, _i64, _i32, _ptr, _ptr, _i32, _f32, _ptr, _i64,
+                              _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _ptr, _i64, _i32, _i32,
+                              _i32, _i32, _ptr],
 }
 
 _LOCK = threading.Lock()

@@ -194,7 +194,8 @@ class HybridDiTBlock(nn.Module):
         small = F.linear(x1, self.small_w)
         soft_gate = torch.sigmoid(small[:, :heads] + k["soft_gate_b"])
         beta = torch.sigmoid(small[:, heads:2 * heads])
-        lin_gate = torch.sigmoid(F.linear(small[:, 2 * heads:], k["lgate_up_w"], k["lgate_up_b"]))
+        # the low-rank gate sigmoid(up(down(x1))) is formed inside the VDA readout
+        lin_gate = vv.OutputGateProjection(small[:, 2 * heads:], k["lgate_up_w"], k["lgate_up_b"])
         frame_mean = x1.view(frames, spatial, hd).mean(1, dtype=torch.float32)
         alpha = self.frame_alpha(frame_mean)
         cos, sin = rope
@@ -210,7 +211,7 @@ class HybridDiTBlock(nn.Module):
             vw.paper_window_attention(q, kk, value, window_plan, d ** -0.5, enabled=True,
                                       gate=soft_gate, out_mxfp8=(qb, sb, 0))
             del q, kk
-            vv.vda_forward(raw_q, raw_k, value, beta, lin_gate.view(T, heads, d), alpha, bounds,
+            vv.vda_forward(raw_q, raw_k, value, beta, lin_gate, alpha, bounds,
                            frames, spatial, k["vda_norm"], cfg.eps, chunk_size=cfg.vda_chunk,
                            out_mxfp8=(qb, sb, heads))
         else:
@@ -218,7 +219,7 @@ class HybridDiTBlock(nn.Module):
             vw.paper_window_attention(q, kk, value, window_plan, d ** -0.5, enabled=True,
                                       gate=soft_gate, out=both[:, :hd].view(T, heads, d))
             del q, kk
-            vv.vda_forward(raw_q, raw_k, value, beta, lin_gate.view(T, heads, d), alpha, bounds,
+            vv.vda_forward(raw_q, raw_k, value, beta, lin_gate, alpha, bounds,
                            frames, spatial, k["vda_norm"], cfg.eps, chunk_size=cfg.vda_chunk,
                            out=both[:, hd:])
             snap("soft", both[:, :hd])

@@ -652,13 +652,40 @@ constexpr int kQT = 16 * kRoWaves;
 constexpr int kRoThreads = 64 * kRoWaves;
 constexpr int kQRow = 136;  // padded bf16 row (272 bytes)
 
-template <bool kMx>
+// The low-rank output gate of the linear branch, formed inside the readout instead of read:
+// gate[t, h*128 + c] = bf16(sigmoid(bf16(down[t] . up_w[h*128 + c] + up_b[h*128 + c]))), with
+// down [F*S, 128] bf16 rows (row stride d_st), up_w [H*128, 128] bf16, up_b [H*128] bf16.
+struct GateProj {
+  const uint16_t* down;
+  int64_t d_st;
+  const uint16_t* up_w;
+  const uint16_t* up_b;
+};
+
+// acc[nt] += A rows (tokens 16 wave + lane16) . B rows (16 nt + lane16) over K = 128, both
+// staged [row][k] with row stride kQRow: the readout's 128 x 128 x 128 tile product.
+__device__ __forceinline__ void tile_product(const uint16_t* sa, const uint16_t* sb, int wave,
+                                             int lane, f32x4* acc) {
+  const int lane16 = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int kc = ks * 32 + g * 8;
+    const bf16x8 a = *reinterpret_cast<const bf16x8*>(&sa[(wave * 16 + lane16) * kQRow + kc]);
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(&sb[(nt * 16 + lane16) * kQRow + kc]);
+      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[nt], 0, 0, 0);
+    }
+  }
+}
+
+template <bool kMx, bool kProj>
 __global__ void __launch_bounds__(kRoThreads)
 vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
                    const void* __restrict__ weight, int weight_f32, float eps, View gv,
-                   uint16_t* __restrict__ out, int64_t o_sf, int64_t o_sh, int64_t o_ss,
-                   int spatial, int heads, int tiles, MxDst mx) {
-  __shared__ __attribute__((aligned(16))) uint16_t sState[kD * kQRow];  // [v][k]
+                   GateProj gp, uint16_t* __restrict__ out, int64_t o_sf, int64_t o_sh,
+                   int64_t o_ss, int spatial, int heads, int tiles, MxDst mx) {
+  __shared__ __attribute__((aligned(16))) uint16_t sState[kD * kQRow];  // [v][k], then gate
   __shared__ __attribute__((aligned(16))) uint16_t sQ[kQT * kQRow];     // [token][k], then y
   const int tile = blockIdx.x % tiles;
   const int fh = blockIdx.x / tiles;
@@ -666,13 +693,48 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lane16 = tid & 15;
   const int s0 = tile * kQT;
   constexpr int kPasses = kQT / (kRoThreads / 16);
-  // the gate rows of the epilogue are loaded first, so they arrive during the matmul
+  // a read gate: its rows are loaded first, so they arrive during the matmul
   u32x4 gate_raw[kPasses];
+  // a formed gate: bf16 pairs of the gate tile in the accumulator layout
+  uint32_t gate_pk[8][2];
+  if constexpr (!kProj) {
 #pragma unroll
-  for (int pass = 0; pass < kPasses; ++pass) {
-    const int s = s0 + pass * (kRoThreads / 16) + (tid >> 4);
-    gate_raw[pass] = s < spatial ? *reinterpret_cast<const u32x4*>(gv.at(f, h, s) + lane16 * 8)
-                                 : u32x4{0u, 0u, 0u, 0u};
+    for (int pass = 0; pass < kPasses; ++pass) {
+      const int s = s0 + pass * (kRoThreads / 16) + (tid >> 4);
+      gate_raw[pass] = s < spatial ? *reinterpret_cast<const u32x4*>(gv.at(f, h, s) + lane16 * 8)
+                                   : u32x4{0u, 0u, 0u, 0u};
+    }
+  } else {
+    // down rows of the tile's tokens -> sQ, head h's up rows -> sState
+    for (int idx = tid * 8; idx < kQT * kD; idx += kRoThreads * 8) {
+      const int r = idx >> 7, c = idx & 127, s = s0 + r;
+      *reinterpret_cast<u32x4*>(&sQ[r * kQRow + c]) =
+          s < spatial ? *reinterpret_cast<const u32x4*>(
+                            gp.down + (static_cast<int64_t>(f) * spatial + s) * gp.d_st + c)
+                      : u32x4{0u, 0u, 0u, 0u};
+    }
+    const uint16_t* up = gp.up_w + static_cast<int64_t>(h) * kD * kD;
+    for (int idx = tid * 8; idx < kD * kD; idx += kRoThreads * 8)
+      *reinterpret_cast<u32x4*>(&sState[(idx >> 7) * kQRow + (idx & 127)]) =
+          *reinterpret_cast<const u32x4*>(up + idx);
+    __syncthreads();
+    f32x4 acc[8];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    tile_product(sQ, sState, wave, lane, acc);
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const float b = bf16_bits_to_f32(gp.up_b[h * kD + nt * 16 + lane16]);
+      float gv4[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float z = round_bf16(acc[nt][v] + b);
+        gv4[v] = 1.0f / (1.0f + expf(-z));
+      }
+      gate_pk[nt][0] = pack_bf16x2(gv4[0], gv4[1]);
+      gate_pk[nt][1] = pack_bf16x2(gv4[2], gv4[3]);
+    }
+    __syncthreads();  // every wave is done with the down / up tiles
   }
   const uint16_t* st = state + static_cast<int64_t>(fh) * kD * kD;
   for (int idx = tid * 8; idx < kD * kD; idx += kRoThreads * 8)
@@ -699,22 +761,18 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int g = lane >> 4;
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const int kc = ks * 32 + g * 8;
-    const bf16x8 a = *reinterpret_cast<const bf16x8*>(&sQ[(wave * 16 + lane16) * kQRow + kc]);
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      const bf16x8 b = *reinterpret_cast<const bf16x8*>(&sState[(nt * 16 + lane16) * kQRow + kc]);
-      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[nt], 0, 0, 0);
-    }
-  }
-  __syncthreads();  // every wave is done with sQ as the q tile
+  tile_product(sQ, sState, wave, lane, acc);
+  __syncthreads();  // every wave is done with sQ as the q tile and sState as the state
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
-      sQ[(wave * 16 + g * 4 + v) * kQRow + nt * 16 + lane16] = f32_to_bf16_bits(acc[nt][v]);
+    for (int v = 0; v < 4; ++v) {
+      const int at = (wave * 16 + g * 4 + v) * kQRow + nt * 16 + lane16;
+      sQ[at] = f32_to_bf16_bits(acc[nt][v]);
+      if constexpr (kProj)
+        sState[at] = static_cast<uint16_t>(v & 1 ? gate_pk[nt][v >> 1] >> 16
+                                                 : gate_pk[nt][v >> 1] & 0xffff);
+    }
   __syncthreads();
   float w[8];
 #pragma unroll
@@ -729,7 +787,10 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
     float y[8];
     unpack8(*reinterpret_cast<const u32x4*>(&sQ[r * kQRow + lane16 * 8]), y);
     float o[8];
-    norm_gate8(y, w, gate_raw[pass], eps, o);
+    if constexpr (kProj)
+      norm_gate8(y, w, *reinterpret_cast<const u32x4*>(&sState[r * kQRow + lane16 * 8]), eps, o);
+    else
+      norm_gate8(y, w, gate_raw[pass], eps, o);
     if constexpr (kMx) {
       quantize_store8(o, lane16, static_cast<int64_t>(f) * spatial + s, mx.chunk0 + h, mx.kp,
                       mx.codes, mx.scales);
@@ -912,17 +973,26 @@ namespace {
 int launch_readout(const char* name, const void* q, int64_t q_sf, int64_t q_sh, int64_t q_ss,
                    int activate_q, const void* state, const void* weight, int weight_f32,
                    float eps, const void* gate, int64_t g_sf, int64_t g_sh, int64_t g_ss,
-                   void* out, int64_t o_sf, int64_t o_sh, int64_t o_ss, const MxDst* mx,
-                   int frames, int heads, int spatial, void* stream) {
-  if (q == nullptr || state == nullptr || weight == nullptr || gate == nullptr ||
-      (mx == nullptr && out == nullptr))
+                   const GateProj* gp, void* out, int64_t o_sf, int64_t o_sh, int64_t o_ss,
+                   const MxDst* mx, int frames, int heads, int spatial, void* stream) {
+  if (q == nullptr || state == nullptr || weight == nullptr ||
+      (gp == nullptr && gate == nullptr) || (mx == nullptr && out == nullptr))
     return set_error(kInvalidArgument, "%s: null pointer", name);
   if (frames <= 0 || heads <= 0 || spatial <= 0)
     return set_error(kInvalidArgument, "%s: bad geometry", name);
-  if (!aligned16(q) || !aligned16(gate) || !aligned16(state) || !stride8(q_sf) ||
-      !stride8(q_sh) || !stride8(q_ss) || !stride8(g_sf) || !stride8(g_sh) || !stride8(g_ss) ||
+  if (!aligned16(q) || !aligned16(state) || !stride8(q_sf) || !stride8(q_sh) ||
+      !stride8(q_ss) ||
+      (gp == nullptr &&
+       (!aligned16(gate) || !stride8(g_sf) || !stride8(g_sh) || !stride8(g_ss))) ||
       (mx == nullptr && (!aligned16(out) || !stride8(o_sf) || !stride8(o_sh) || !stride8(o_ss))))
     return set_error(kInvalidArgument, "%s: operands need 16-byte aligned rows", name);
+  if (gp != nullptr) {
+    if (gp->down == nullptr || gp->up_w == nullptr || gp->up_b == nullptr)
+      return set_error(kInvalidArgument, "%s: null pointer", name);
+    if (!aligned16(gp->down) || !aligned16(gp->up_w) || !stride8(gp->d_st) || gp->d_st < kD)
+      return set_error(kInvalidArgument,
+                       "%s: gate down rows and up weights need 16-byte aligned rows of 128", name);
+  }
   if (mx != nullptr) {
     if (mx->codes == nullptr || mx->scales == nullptr)
       return set_error(kInvalidArgument, "%s: null pointer", name);
@@ -936,17 +1006,25 @@ int launch_readout(const char* name, const void* q, int64_t q_sf, int64_t q_sh, 
   const int tiles = (spatial + kQT - 1) / kQT;
   const View qv{static_cast<const uint16_t*>(q), q_sf, q_sh, q_ss};
   const View gv{static_cast<const uint16_t*>(gate), g_sf, g_sh, g_ss};
+  const GateProj g = gp != nullptr ? *gp : GateProj{nullptr, 0, nullptr, nullptr};
+  const MxDst m = mx != nullptr ? *mx : MxDst{nullptr, nullptr, 0, 0};
   const dim3 grid(frames * heads * tiles), block(kRoThreads);
   const auto st = static_cast<hipStream_t>(stream);
-  if (mx != nullptr)
-    hipLaunchKernelGGL(vda_readout_kernel<true>, grid, block, 0, st, qv, activate_q,
-                       static_cast<const uint16_t*>(state), weight, weight_f32, eps, gv, nullptr,
-                       0, 0, 0, spatial, heads, tiles, *mx);
+  const auto* sp = static_cast<const uint16_t*>(state);
+  auto* op = static_cast<uint16_t*>(out);
+#define VDN_READOUT(MX, PROJ)                                                                  \
+  hipLaunchKernelGGL((vda_readout_kernel<MX, PROJ>), grid, block, 0, st, qv, activate_q, sp,   \
+                     weight, weight_f32, eps, gv, g, op, o_sf, o_sh, o_ss, spatial, heads,      \
+                     tiles, m)
+  if (mx != nullptr && gp != nullptr)
+    VDN_READOUT(true, true);
+  else if (mx != nullptr)
+    VDN_READOUT(true, false);
+  else if (gp != nullptr)
+    VDN_READOUT(false, true);
   else
-    hipLaunchKernelGGL(vda_readout_kernel<false>, grid, block, 0, st, qv, activate_q,
-                       static_cast<const uint16_t*>(state), weight, weight_f32, eps, gv,
-                       static_cast<uint16_t*>(out), o_sf, o_sh, o_ss, spatial, heads, tiles,
-                       MxDst{nullptr, nullptr, 0, 0});
+    VDN_READOUT(false, false);
+#undef VDN_READOUT
   return check_launch(name);
 }
 
@@ -959,8 +1037,8 @@ VDN_API int vdn_vda_readout(const void* q, int64_t q_sf, int64_t q_sh, int64_t q
                             void* out, int64_t o_sf, int64_t o_sh, int64_t o_ss, int frames,
                             int heads, int spatial, void* stream) {
   return launch_readout("vdn_vda_readout", q, q_sf, q_sh, q_ss, activate_q, state, weight,
-                        weight_f32, eps, gate, g_sf, g_sh, g_ss, out, o_sf, o_sh, o_ss, nullptr,
-                        frames, heads, spatial, stream);
+                        weight_f32, eps, gate, g_sf, g_sh, g_ss, nullptr, out, o_sf, o_sh, o_ss,
+                        nullptr, frames, heads, spatial, stream);
 }
 
 // The same readout with the output quantized in the epilogue: token row f * S + s, head h ->
@@ -976,8 +1054,33 @@ VDN_API int vdn_vda_readout_mxfp8(const void* q, int64_t q_sf, int64_t q_sh, int
                                   void* stream) {
   const MxDst mx{static_cast<uint8_t*>(codes), static_cast<uint8_t*>(scales), kp, chunk0};
   return launch_readout("vdn_vda_readout_mxfp8", q, q_sf, q_sh, q_ss, activate_q, state,
-                        weight, weight_f32, eps, gate, g_sf, g_sh, g_ss, nullptr, 0, 0, 0, &mx,
-                        frames, heads, spatial, stream);
+                        weight, weight_f32, eps, gate, g_sf, g_sh, g_ss, nullptr, nullptr, 0, 0,
+                        0, &mx, frames, heads, spatial, stream);
+}
+
+// The readout with the linear branch's low-rank output gate formed in the kernel:
+// gate = bf16(sigmoid(bf16(down · up_wᵀ + up_b))) per (token, head, channel), the
+// OutputGate of the linear branch (src/models/attention_gates.py:52-55, up(down(x)) then
+// sigmoid), from down [F*S, 128] bf16 rows (row stride d_st), up_w [H*128, 128] bf16 and
+// up_b [H*128] bf16. Exactly one destination: bf16 `out` (strides as vdn_vda_readout) or,
+// with out = NULL, MXFP8 `codes` / `scales` (as vdn_vda_readout_mxfp8). Replaces the pair
+// output_gate(xv) + paper_readout (src/models/linear_attention/paper_stack.py:315-318).
+VDN_API int vdn_vda_readout_gated(const void* q, int64_t q_sf, int64_t q_sh, int64_t q_ss,
+                                  int activate_q, const void* state, const void* weight,
+                                  int weight_f32, float eps, const void* down, int64_t d_st,
+                                  const void* up_w, const void* up_b, void* out, int64_t o_sf,
+                                  int64_t o_sh, int64_t o_ss, void* codes, void* scales,
+                                  int64_t kp, int chunk0, int frames, int heads, int spatial,
+                                  void* stream) {
+  const GateProj gp{static_cast<const uint16_t*>(down), d_st,
+                    static_cast<const uint16_t*>(up_w), static_cast<const uint16_t*>(up_b)};
+  if ((out == nullptr) == (codes == nullptr))
+    return set_error(kInvalidArgument,
+                     "vdn_vda_readout_gated: give exactly one of out and codes");
+  const MxDst mx{static_cast<uint8_t*>(codes), static_cast<uint8_t*>(scales), kp, chunk0};
+  return launch_readout("vdn_vda_readout_gated", q, q_sf, q_sh, q_ss, activate_q, state,
+                        weight, weight_f32, eps, nullptr, 0, 0, 0, &gp, out, o_sf, o_sh, o_ss,
+                        codes != nullptr ? &mx : nullptr, frames, heads, spatial, stream);
 }
 
 // Reference: paper_sglang.py:377-437 (_linear_epilogue_kernel / vdn_linear_epilogue):

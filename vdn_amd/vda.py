@@ -325,12 +325,40 @@ def vdn_linear_epilogue(readout, norm_weight, gate, eps):
     return out
 
 
+@dataclass(frozen=True)
+class OutputGateProjection:
+    """The linear branch's low-rank output gate as its operands, for the readout to form in
+    its kernel: gate = sigmoid(up(down)) = bf16(sigmoid(bf16(down · up_weightᵀ + up_bias)))
+    (OutputGate.forward, src/models/attention_gates.py:52-55). down [F*S, 128] bf16 (any row
+    stride, unit column stride) is the bottleneck projection down(x); up_weight [H*128, 128]
+    and up_bias [H*128] bf16 are the up Linear's parameters."""
+    down: torch.Tensor
+    up_weight: torch.Tensor
+    up_bias: torch.Tensor
+
+
+def _gate_projection(gp, n, h, device):
+    down, w, b = gp.down, gp.up_weight, gp.up_bias
+    for t, name in ((down, "down"), (w, "up_weight"), (b, "up_bias")):
+        _cuda(t, name, torch.bfloat16)
+        if t.device != device:
+            raise ValueError(f"{name} must be on the q device")
+    if down.shape != (n, HEAD_DIM):
+        raise ValueError("down must be [F*S, 128]")
+    if down.stride(-1) != 1 or down.stride(0) % 8 or down.data_ptr() % 16:
+        down = down.contiguous()  # the kernel reads 16-byte aligned rows
+    if w.shape != (h * HEAD_DIM, HEAD_DIM) or b.shape != (h * HEAD_DIM,):
+        raise ValueError("up_weight must be [H*128, 128] and up_bias [H*128]")
+    return down, w.contiguous(), b.contiguous()
+
+
 def linear_readout(q, state, norm_weight, gate, eps, frames, spatial, *, activate_q=True,
                    out=None, out_mxfp8=None):
     """Fused q activation + readout + epilogue.
 
     q: raw [F*S, H, D] bf16 (any row/head stride; prepared q with activate_q=False);
-    state: [F, H, D, D] bf16 from paper_gather; gate [F*S, H, D] bf16.
+    state: [F, H, D, D] bf16 from paper_gather; gate [F*S, H, D] bf16, or an
+    OutputGateProjection, which the kernel turns into that gate itself.
     Returns (or writes into `out`) [F*S, H*D] bf16 = RMSNorm(bf16(q'·stateᵀ))·w·gate.
     `out_mxfp8` = (codes, scales, chunk0) instead quantizes the result in the kernel: head h of
     row r becomes chunk chunk0 + h of row r of an MXFP8 activation (empty_activation),
@@ -338,10 +366,15 @@ def linear_readout(q, state, norm_weight, gate, eps, frames, spatial, *, activat
     """
     _cuda(q, "q", torch.bfloat16)
     _cuda(state, "state", torch.bfloat16)
-    _cuda(gate, "gate", torch.bfloat16)
     n, h, d = q.shape
     if (d != HEAD_DIM or n != frames * spatial or state.shape != (frames, h, d, d)
-            or gate.shape != (n, h, d) or q.stride(-1) != 1 or gate.stride(-1) != 1):
+            or q.stride(-1) != 1):
+        raise ValueError("readout geometry mismatch")
+    if isinstance(gate, OutputGateProjection):
+        return _gated_readout(q, state, norm_weight, gate, eps, frames, spatial, activate_q,
+                              out, out_mxfp8)
+    _cuda(gate, "gate", torch.bfloat16)
+    if gate.shape != (n, h, d) or gate.stride(-1) != 1:
         raise ValueError("readout geometry mismatch")
     state = state.contiguous()
     w = norm_weight.to(device=q.device).contiguous()
@@ -367,6 +400,31 @@ def linear_readout(q, state, norm_weight, gate, eps, frames, spatial, *, activat
     return out
 
 
+def _gated_readout(q, state, norm_weight, gp, eps, frames, spatial, activate_q, out, out_mxfp8):
+    n, h, d = q.shape
+    down, up_w, up_b = _gate_projection(gp, n, h, q.device)
+    state = state.contiguous()
+    w = norm_weight.to(device=q.device).contiguous()
+    qs = (spatial * q.stride(0), q.stride(1), q.stride(0))
+    common = (q.data_ptr(), *qs, int(bool(activate_q)), state.data_ptr(), w.data_ptr(),
+              _weight_flag(w), float(eps), down.data_ptr(), down.stride(0), up_w.data_ptr(),
+              up_b.data_ptr())
+    if out_mxfp8 is not None:
+        if out is not None:
+            raise ValueError("out_mxfp8 excludes out")
+        codes, scales, chunk0 = mxfp8_destination(out_mxfp8, n, h, q.device)
+        _lib.call("vdn_vda_readout_gated", *common, None, 0, 0, 0, codes.data_ptr(),
+                  scales.data_ptr(), codes.shape[1], chunk0, frames, h, spatial, _stream(q))
+        return None
+    if out is None:
+        out = torch.empty((n, h * d), dtype=torch.bfloat16, device=q.device)
+    elif out.shape != (n, h * d) or out.stride(-1) != 1 or out.dtype != torch.bfloat16:
+        raise ValueError("out must be bf16 [F*S, H*D]")
+    _lib.call("vdn_vda_readout_gated", *common, out.data_ptr(), spatial * out.stride(0), d,
+              out.stride(0), None, None, 0, 0, frames, h, spatial, _stream(q))
+    return out
+
+
 # ---------------------------------------------------------------- orchestration ----
 
 def vda_forward(q_raw, k_raw, v_raw, beta, gate, alpha, bounds, num_frames, tokens_per_frame,
@@ -374,8 +432,8 @@ def vda_forward(q_raw, k_raw, v_raw, beta, gate, alpha, bounds, num_frames, toke
                 out_mxfp8=None):
     """The paper VDA branch body on raw projections (paper_stack.py:266-318).
 
-    q_raw/k_raw/v_raw: [F*S, H, 128] bf16 raw projections; beta [F*S, H]; gate [F*S, H, 128];
-    alpha [F, H, 128] fp32. `text` = (tk_raw, tv_raw, text_beta) adds the prompt's virtual
+    q_raw/k_raw/v_raw: [F*S, H, 128] bf16 raw projections; beta [F*S, H]; gate [F*S, H, 128]
+    or an OutputGateProjection; alpha [F, H, 128] fp32. `text` = (tk_raw, tv_raw, text_beta) adds the prompt's virtual
     frame (its factors share the batch; half its injection seeds both scans). `out` /
     `out_mxfp8` as in linear_readout.
     """
@@ -429,8 +487,23 @@ def paper_readout(branch, xv, num_frames, tokens_per_frame, bounds, qkv_raw, fra
             text_beta = torch.sigmoid(branch.beta_proj(text_x))
         text = (text_qkv_raw[1], text_qkv_raw[2], text_beta.reshape(-1, h))
     if gate is None:
-        gate = branch.output_gate(xv)
-    return vda_forward(q, k, v, beta.reshape(-1, h), gate.reshape(-1, h, HEAD_DIM), alpha, bounds,
+        gate = _output_gate(branch.output_gate, xv, h)
+    else:
+        gate = gate.reshape(-1, h, HEAD_DIM)
+    return vda_forward(q, k, v, beta.reshape(-1, h), gate, alpha, bounds,
                        num_frames, tokens_per_frame, branch.norm.weight, branch.norm.eps,
                        chunk_size=branch.paper_vda_chunk_size, bridge=branch.bridge == "alpha",
                        text=text)
+
+
+def _output_gate(module, xv, heads):
+    """OutputGate(xv) of the linear branch: a bottleneck-128 gate in bf16 goes to the readout
+    kernel as its projection operands (only down(xv) is formed here); any other gate is
+    evaluated by the module itself."""
+    down, up = getattr(module, "down", None), getattr(module, "up", None)
+    if (down is not None and up is not None and down.out_features == HEAD_DIM
+            and up.in_features == HEAD_DIM and up.out_features == heads * HEAD_DIM
+            and up.bias is not None and xv.dtype == torch.bfloat16
+            and all(p.dtype == torch.bfloat16 for p in (down.weight, up.weight, up.bias))):
+        return OutputGateProjection(down(xv), up.weight, up.bias)
+    return module(xv).reshape(-1, heads, HEAD_DIM)
