@@ -18,6 +18,7 @@ import argparse
 import json
 import math
 import os
+import re
 import sys
 import time
 
@@ -175,6 +176,9 @@ def _counter_rows(path, counter):
     return [(d, name, kib) for d, (name, kib) in per.items()]
 
 
+GEMM_KERNEL = re.compile(r"mxfp8_gemm_(persistent_)?kernel")
+
+
 def summarize_traffic(fetch_csv, write_csv):
     """Markdown summary of the HBM traffic per MXFP8 GEMM launch from a FETCH_SIZE pass and a
     WRITE_SIZE pass (each run with --calibrate-copy). Each counter is scaled by the factor
@@ -187,7 +191,7 @@ def summarize_traffic(fetch_csv, write_csv):
         cal = max(((d, kib) for d, name, kib in rows if CALIBRATION_KERNEL in name), default=None)
         if cal is None:
             raise SystemExit(f"{path}: no {CALIBRATION_KERNEL} dispatch (run with --calibrate-copy)")
-        gemm = sorted((d, name, kib) for d, name, kib in rows if "mxfp8_gemm_kernel" in name)
+        gemm = sorted((d, name, kib) for d, name, kib in rows if GEMM_KERNEL.search(name))
         passes[counter] = (CALIBRATION_KIB / cal[1], gemm)
     fetch_factor, fetch = passes["FETCH_SIZE"]
     write_factor, write = passes["WRITE_SIZE"]
@@ -198,8 +202,9 @@ def summarize_traffic(fetch_csv, write_csv):
     for (d, name, fk), (_, _, wk) in zip(fetch, write):
         nbytes = (fk * fetch_factor + wk * write_factor) * 1024
         total += nbytes
+        kname = GEMM_KERNEL.search(name).group(0)
         tile = name[name.index("<"):name.index(">") + 1] if "<" in name else ""
-        lines.append(f"| {len(lines)} | `mxfp8_gemm_kernel{tile}` | {fk * fetch_factor / 2**20:.3f} | "
+        lines.append(f"| {len(lines)} | `{kname}{tile}` | {fk * fetch_factor / 2**20:.3f} | "
                      f"{wk * write_factor / 2**20:.3f} | {nbytes / 1e9:.3f} |")
     per_launch = total / len(fetch)
     out = ["# HBM traffic per MXFP8 GEMM launch, hybrid DiT block at 108,000 tokens", "",
@@ -348,8 +353,9 @@ def main():
                    "tokens": tokens, "hidden": cfg.hidden, "heads": cfg.heads,
                    "head_dim": cfg.head_dim, "ffn": cfg.ffn, "context": ctx.shape[0],
                    "parallelism": "single GPU"},
-        "roofline": {"kernel": "mxfp8_gemm_kernel (all block projections: vdn_mxfp8_gemm and "
-                               "the FFN-up vdn_mxfp8_gemm_act_quantize)", "bound": "mfma",
+        "roofline": {"kernel": "mxfp8_gemm_persistent_kernel / mxfp8_gemm_kernel (all block "
+                               "projections: vdn_mxfp8_gemm and the FFN-up "
+                               "vdn_mxfp8_gemm_act_quantize)", "bound": "mfma",
                      "achieved": round(gemm_tflops, 1), "peak": PEAK_MXFP8_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_MXFP8_TFLOPS, 4),
                      "traffic": traffic,
