@@ -140,6 +140,7 @@ class HybridDiTBlock(nn.Module):
             "lgate_up_w", "lgate_up_b", "alpha_down_w", "alpha_up_w", "a_log", "dt_bias",
             "vda_norm", "norm_qc", "norm_kc")}
         self._zero_table = None
+        self._side = None
 
     # ---------------------------------------------------------------- pieces ----
     def adaln_tables(self, temb):
@@ -154,6 +155,12 @@ class HybridDiTBlock(nn.Module):
                          k["alpha_up_w"].float()) + k["dt_bias"]
         scale = torch.exp(k["a_log"])[:, None]
         return torch.exp(-scale * F.softplus(delta.view(-1, cfg.heads, cfg.head_dim))).contiguous()
+
+    def _side_stream(self, device):
+        """One side stream per device, default priority."""
+        if self._side is None or self._side.device != device:
+            self._side = torch.cuda.Stream(device=device)
+        return self._side
 
     def _zeros(self, device):
         if self._zero_table is None or self._zero_table.device != device:
@@ -199,8 +206,6 @@ class HybridDiTBlock(nn.Module):
         frame_mean = x1.view(frames, spatial, hd).mean(1, dtype=torch.float32)
         alpha = self.frame_alpha(frame_mean)
         cos, sin = rope
-        q, kk = vw.paper_qk_rmsnorm_rope(raw_q, raw_k, k["norm_q"], k["norm_k"], cfg.eps, cos, sin,
-                                         enabled=True)
         # The two branch outputs are the two halves of the [O | O_lin] operand. The kernels
         # quantize them in their epilogues straight into the MXFP8 operand (chunks 0..H-1 for
         # the softmax branch, H.. for VDA); with return_parts they are kept in bf16 for the
@@ -208,13 +213,27 @@ class HybridDiTBlock(nn.Module):
         bounds = window_plan.bounds
         if parts is None:
             qb, sb = mx.empty_activation(T, 2 * hd, dev)
+            # The VDA branch runs on a side stream while RoPE and the window attention run on
+            # the caller's stream (the reference's paper_vda_overlap, tensor_parallel.py:
+            # 202-216): its latency-bound passes fill the attention's gaps.
+            main = torch.cuda.current_stream(dev)
+            side = self._side_stream(dev)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                vv.vda_forward(raw_q, raw_k, value, beta, lin_gate, alpha, bounds,
+                               frames, spatial, k["vda_norm"], cfg.eps, chunk_size=cfg.vda_chunk,
+                               out_mxfp8=(qb, sb, heads))
+            for t in (qkv, small, beta, alpha, qb, sb):
+                t.record_stream(side)
+            q, kk = vw.paper_qk_rmsnorm_rope(raw_q, raw_k, k["norm_q"], k["norm_k"], cfg.eps,
+                                             cos, sin, enabled=True)
             vw.paper_window_attention(q, kk, value, window_plan, d ** -0.5, enabled=True,
                                       gate=soft_gate, out_mxfp8=(qb, sb, 0))
             del q, kk
-            vv.vda_forward(raw_q, raw_k, value, beta, lin_gate, alpha, bounds,
-                           frames, spatial, k["vda_norm"], cfg.eps, chunk_size=cfg.vda_chunk,
-                           out_mxfp8=(qb, sb, heads))
+            main.wait_stream(side)
         else:
+            q, kk = vw.paper_qk_rmsnorm_rope(raw_q, raw_k, k["norm_q"], k["norm_k"], cfg.eps,
+                                             cos, sin, enabled=True)
             both = torch.empty((T, 2 * hd), dtype=torch.bfloat16, device=dev)
             vw.paper_window_attention(q, kk, value, window_plan, d ** -0.5, enabled=True,
                                       gate=soft_gate, out=both[:, :hd].view(T, heads, d))
