@@ -679,8 +679,9 @@ __device__ __forceinline__ void tile_product(const uint16_t* sa, const uint16_t*
   }
 }
 
+// Two workgroups per CU (4 waves per SIMD): the kernel must stay within 128 VGPRs.
 template <bool kMx, bool kProj>
-__global__ void __launch_bounds__(kRoThreads)
+__global__ void __launch_bounds__(kRoThreads) __attribute__((amdgpu_waves_per_eu(4)))
 vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
                    const void* __restrict__ weight, int weight_f32, float eps, View gv,
                    GateProj gp, uint16_t* __restrict__ out, int64_t o_sf, int64_t o_sh,
@@ -697,6 +698,21 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
   u32x4 gate_raw[kPasses];
   // a formed gate: bf16 pairs of the gate tile in the accumulator layout
   uint32_t gate_pk[8][2];
+  // the q rows (kPasses per thread) and the state (kStateLoads 16-byte pieces per thread)
+  constexpr int kStateLoads = kD * kD / (kRoThreads * 8);
+  const uint16_t* st = state + static_cast<int64_t>(fh) * kD * kD;
+  u32x4 q_raw[kPasses], st_raw[kStateLoads];
+  auto load_main = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kStateLoads; ++i)
+      st_raw[i] = *reinterpret_cast<const u32x4*>(st + (tid + i * kRoThreads) * 8);
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) {
+      const int s = s0 + pass * (kRoThreads / 16) + (tid >> 4);
+      q_raw[pass] = s < spatial ? *reinterpret_cast<const u32x4*>(qv.at(f, h, s) + lane16 * 8)
+                                : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
   if constexpr (!kProj) {
 #pragma unroll
     for (int pass = 0; pass < kPasses; ++pass) {
@@ -718,6 +734,7 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
       *reinterpret_cast<u32x4*>(&sState[(idx >> 7) * kQRow + (idx & 127)]) =
           *reinterpret_cast<const u32x4*>(up + idx);
     __syncthreads();
+    load_main();  // the readout's operands arrive while the gate is formed
     f32x4 acc[8];
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -729,29 +746,28 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const float z = round_bf16(acc[nt][v] + b);
-        gv4[v] = 1.0f / (1.0f + expf(-z));
+        // sigmoid by the hardware exp2 and reciprocal: a few fp32 ulp from 1 / (1 + exp(-z)),
+        // below the bf16 rounding that follows
+        gv4[v] = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z * -1.4426950408889634f));
       }
       gate_pk[nt][0] = pack_bf16x2(gv4[0], gv4[1]);
       gate_pk[nt][1] = pack_bf16x2(gv4[2], gv4[3]);
     }
     __syncthreads();  // every wave is done with the down / up tiles
   }
-  const uint16_t* st = state + static_cast<int64_t>(fh) * kD * kD;
-  for (int idx = tid * 8; idx < kD * kD; idx += kRoThreads * 8)
-    *reinterpret_cast<u32x4*>(&sState[(idx >> 7) * kQRow + (idx & 127)]) =
-        *reinterpret_cast<const u32x4*>(st + idx);
-  // q tile: kRoThreads / 16 tokens per pass (one 16-lane group per token)
+  if constexpr (!kProj) load_main();
 #pragma unroll
-  for (int pass = 0; pass < kQT / (kRoThreads / 16); ++pass) {
+  for (int i = 0; i < kStateLoads; ++i) {
+    const int idx = (tid + i * kRoThreads) * 8;
+    *reinterpret_cast<u32x4*>(&sState[(idx >> 7) * kQRow + (idx & 127)]) = st_raw[i];
+  }
+  // q tile: kRoThreads / 16 tokens per pass (one 16-lane group per token); rows past the
+  // frame are zero
+#pragma unroll
+  for (int pass = 0; pass < kPasses; ++pass) {
     const int r = pass * (kRoThreads / 16) + (tid >> 4);
-    const int s = s0 + r;
     float v[8];
-    if (s < spatial) {
-      unpack8(*reinterpret_cast<const u32x4*>(qv.at(f, h, s) + lane16 * 8), v);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = 0.f;
-    }
+    unpack8(q_raw[pass], v);
     if (activate_q) activate8(v, true);
     *reinterpret_cast<u32x4*>(&sQ[r * kQRow + lane16 * 8]) = pack8(v);
   }
