@@ -34,6 +34,10 @@ VDA_ENTRIES = ("vdn_vda_statistics", "vdn_vda_factors", "vdn_vda_compose", "vdn_
                "vdn_vda_log_prefix", "vdn_vda_gather", "vdn_vda_readout", "vdn_vda_readout_mxfp8",
                "vdn_vda_readout_gated")
 ATTENTION = ("vdn_window_attention", "vdn_window_attention_mxfp8")
+# the VDA passes bounded by HBM (the factors and the scan are latency-bound: 128x128
+# eliminations and 30 serial frame steps)
+VDA_HBM_BOUND = ("vdn_vda_statistics", "vdn_vda_gather", "vdn_vda_readout",
+                 "vdn_vda_readout_mxfp8", "vdn_vda_readout_gated")
 
 
 def log(msg):
@@ -107,6 +111,32 @@ def work(name, a, plans):
         return (4.0 * f * s * h * D * D,
                 f * s * h * D * 2 + f * s * D * 2 + h * D * (D + 1) * 2 + f * h * D * D * 2 + out)
     return 0.0, 0.0
+
+
+def aggregate(timer, plans):
+    """name -> [launches, ms, flop, bytes] over the timer's records."""
+    per = {}
+    for name, a, t in timer.durations():
+        flop, nbytes = work(name, a, plans)
+        e = per.setdefault(name, [0, 0.0, 0.0, 0.0])
+        e[0] += 1
+        e[1] += t
+        e[2] += flop
+        e[3] += nbytes
+    return per
+
+
+def breakdown_of(per, steps):
+    out = {}
+    for name, (count, t, flop, nbytes) in sorted(per.items(), key=lambda kv: -kv[1][1]):
+        row = dict(ms_per_step=round(t / steps, 3), launches_per_step=count // steps,
+                   avg_launch_ms=round(t / count, 4))
+        if flop and name in GEMMS + ATTENTION:
+            row["tflops"] = round(flop / (t * 1e-3) / 1e12, 1)
+        if nbytes and name not in GEMMS + ATTENTION:
+            row["gbs"] = round(nbytes / (t * 1e-3) / 1e9, 1)
+        out[name] = row
+    return out
 
 
 def visible_pairs(frames, spatial, radius):
@@ -210,9 +240,9 @@ def summarize_traffic(fetch_csv, write_csv):
     out = ["# HBM traffic per MXFP8 GEMM launch, hybrid DiT block at 108,000 tokens", "",
            "Commands (from the repository root, on one MI355X; one block forward, no warmup):", "",
            "    rocprofv3 --pmc FETCH_SIZE -d gpurun_out/pmc_fetch -o f --output-format csv -- "
-           "python3 bench.py --steps 1 --warmup 0 --no-cpu-baseline --calibrate-copy",
+           "python3 bench.py --steps 1 --warmup 0 --isolated-steps 0 --no-cpu-baseline --calibrate-copy",
            "    rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_write -o w --output-format csv -- "
-           "python3 bench.py --steps 1 --warmup 0 --no-cpu-baseline --calibrate-copy",
+           "python3 bench.py --steps 1 --warmup 0 --isolated-steps 0 --no-cpu-baseline --calibrate-copy",
            "    python3 bench.py --summarize-traffic gpurun_out/pmc_fetch/f_counter_collection.csv "
            "gpurun_out/pmc_write/w_counter_collection.csv", "",
            "Calibration: `torch.neg` over 2^29 bf16 values (1 GiB read, 1 GiB written) reads "
@@ -253,6 +283,9 @@ def main():
     p.add_argument("--frames", type=int, default=30)
     p.add_argument("--cpu-sample-frames", type=int, default=6)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--isolated-steps", type=int, default=2,
+                   help="untimed-for-value steps with the VDA branch after the window attention "
+                        "on one stream, for the branch kernels' own launch times")
     args = p.parse_args()
     if args.summarize_counters:
         summarize_counters(args.summarize_counters)
@@ -315,29 +348,33 @@ def main():
         log("negated 1 GiB into 1 GiB (calibration kernel: 1 GiB read, 1 GiB written)")
         del src, dst
 
-    per = {}
-    for name, a, t in timer.durations():
-        flop, nbytes = work(name, a, plans)
-        e = per.setdefault(name, [0, 0.0, 0.0, 0.0])
-        e[0] += 1
-        e[1] += t
-        e[2] += flop
-        e[3] += nbytes
-    breakdown = {}
-    for name, (count, t, flop, nbytes) in sorted(per.items(), key=lambda kv: -kv[1][1]):
-        row = dict(ms_per_step=round(t / args.steps, 3), launches_per_step=count // args.steps,
-                   avg_launch_ms=round(t / count, 4))
-        if flop and name in GEMMS + ATTENTION:
-            row["tflops"] = round(flop / (t * 1e-3) / 1e12, 1)
-        if nbytes and name not in GEMMS + ATTENTION:
-            row["gbs"] = round(nbytes / (t * 1e-3) / 1e9, 1)
-        breakdown[name] = row
+    per = aggregate(timer, plans)
+    breakdown = breakdown_of(per, args.steps)
     g = [sum(per[nm][i] for nm in GEMMS if nm in per) for i in range(4)]
     gemm_tflops = g[2] / (g[1] * 1e-3) / 1e12
-    vda_t = sum(per[n][1] for n in VDA_ENTRIES if n in per)
-    vda_bytes = sum(per[n][3] for n in VDA_ENTRIES if n in per)
+
+    # The branch kernels again, one stream, no overlap: the VDA passes share the GPU with the
+    # window attention in the timed steps above, so their launch times there are wall times
+    # under contention. These steps give each branch kernel's own launch time.
+    iso_steps = args.isolated_steps
+    if iso_steps > 0:
+        block.overlap_vda = False
+        with _lib.LaunchTimer(set(VDA_ENTRIES) | set(ATTENTION)) as iso_timer:
+            for i in range(iso_steps):
+                step()
+            torch.cuda.synchronize()
+        block.overlap_vda = True
+        iso = aggregate(iso_timer, plans)
+        log(f"isolated branch kernels timed over {iso_steps} steps")
+    else:   # only the overlapped times exist
+        iso, iso_steps = per, args.steps
+    vda_t = sum(iso[n][1] for n in VDA_ENTRIES if n in iso)
+    vda_bytes = sum(iso[n][3] for n in VDA_ENTRIES if n in iso)
     vda_gbs = vda_bytes / (vda_t * 1e-3) / 1e9
-    w = [sum(per[nm][i] for nm in ATTENTION if nm in per) for i in range(4)]
+    hb_t = sum(iso[n][1] for n in VDA_HBM_BOUND if n in iso)
+    hb_bytes = sum(iso[n][3] for n in VDA_HBM_BOUND if n in iso)
+    hb_gbs = hb_bytes / (hb_t * 1e-3) / 1e9
+    w = [sum(iso[nm][i] for nm in ATTENTION if nm in iso) for i in range(4)]
     traffic = traffic_per_launch()
 
     result = {
@@ -363,10 +400,14 @@ def main():
                      "flop_per_launch": g[2] / g[0]},
         "mxfp8_tflops": round(gemm_tflops, 1),
         "vda_gbs": round(vda_gbs, 1), "vda_hbm_frac": round(vda_gbs / PEAK_HBM_GBS, 4),
-        "vda_ms": round(vda_t / args.steps, 3),
+        "vda_ms": round(vda_t / iso_steps, 3),
+        "vda_hbm_bound_passes": {"entries": list(VDA_HBM_BOUND), "gbs": round(hb_gbs, 1),
+                                 "frac": round(hb_gbs / PEAK_HBM_GBS, 4),
+                                 "ms": round(hb_t / iso_steps, 3)},
         "window_attention_tflops": round(w[2] / (w[1] * 1e-3) / 1e12, 1),
         "window_attention_bf16_frac": round(w[2] / (w[1] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "breakdown": breakdown,
+        "breakdown_isolated_branches": breakdown_of(iso, iso_steps),
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

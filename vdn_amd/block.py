@@ -141,6 +141,10 @@ class HybridDiTBlock(nn.Module):
             "vda_norm", "norm_qc", "norm_kc")}
         self._zero_table = None
         self._side = None
+        # The VDA branch runs on a side stream beside RoPE + window attention; False runs it
+        # after them on the caller's stream (same kernels, same outputs), which gives each
+        # branch kernel an unshared launch time.
+        self.overlap_vda = True
 
     # ---------------------------------------------------------------- pieces ----
     def adaln_tables(self, temb):
@@ -213,24 +217,32 @@ class HybridDiTBlock(nn.Module):
         bounds = window_plan.bounds
         if parts is None:
             qb, sb = mx.empty_activation(T, 2 * hd, dev)
+
+            def linear_branch():
+                vv.vda_forward(raw_q, raw_k, value, beta, lin_gate, alpha, bounds,
+                               frames, spatial, k["vda_norm"], cfg.eps, chunk_size=cfg.vda_chunk,
+                               out_mxfp8=(qb, sb, heads))
+
             # The VDA branch runs on a side stream while RoPE and the window attention run on
             # the caller's stream (the reference's paper_vda_overlap, tensor_parallel.py:
             # 202-216): its latency-bound passes fill the attention's gaps.
             main = torch.cuda.current_stream(dev)
-            side = self._side_stream(dev)
-            side.wait_stream(main)
-            with torch.cuda.stream(side):
-                vv.vda_forward(raw_q, raw_k, value, beta, lin_gate, alpha, bounds,
-                               frames, spatial, k["vda_norm"], cfg.eps, chunk_size=cfg.vda_chunk,
-                               out_mxfp8=(qb, sb, heads))
-            for t in (qkv, small, beta, alpha, qb, sb):
-                t.record_stream(side)
+            if self.overlap_vda:
+                side = self._side_stream(dev)
+                side.wait_stream(main)
+                with torch.cuda.stream(side):
+                    linear_branch()
+                for t in (qkv, small, beta, alpha, qb, sb):
+                    t.record_stream(side)
             q, kk = vw.paper_qk_rmsnorm_rope(raw_q, raw_k, k["norm_q"], k["norm_k"], cfg.eps,
                                              cos, sin, enabled=True)
             vw.paper_window_attention(q, kk, value, window_plan, d ** -0.5, enabled=True,
                                       gate=soft_gate, out_mxfp8=(qb, sb, 0))
             del q, kk
-            main.wait_stream(side)
+            if self.overlap_vda:
+                main.wait_stream(side)
+            else:
+                linear_branch()
         else:
             q, kk = vw.paper_qk_rmsnorm_rope(raw_q, raw_k, k["norm_q"], k["norm_k"], cfg.eps,
                                              cos, sin, enabled=True)
