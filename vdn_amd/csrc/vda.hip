@@ -26,6 +26,8 @@
 
 #include <math.h>
 
+#include <algorithm>
+
 namespace vdn {
 namespace {
 
@@ -643,14 +645,20 @@ __device__ __forceinline__ void norm_gate_store8(float* y, const float* w, const
   *reinterpret_cast<u32x4*>(dst) = pack8(o);
 }
 
-// Fused readout: per (frame, head, kQT-token tile): q' = bf16(L2(SiLU(q_raw))) (optional),
-// y = bf16(q' · stateᵀ) on bf16 MFMA, then RMSNorm·w·gate into out[f*S + s, h*D + c].
-// A workgroup of kRoWaves waves reads out kQT = 16 kRoWaves tokens of one (frame, head): the
-// 32 KB state is staged once per kQT tokens.
+// Readout, transposed: Y' = state · q'ᵀ, i.e. Y'[c][t] = y[t][c] = q'[t] · state[c].
+// A workgroup of kRoWaves waves takes one (frame, head) and a range of the frame's 16-token
+// groups. It stages the 128 x 128 state (and, for a formed gate, head h's 128 x 128 up
+// weights) in LDS once; then each wave walks its token groups without barriers.
+// For a group, lane l (t = l % 16, g = l / 16) loads channels 32 ks + 8 g .. +8 (ks = 0..3)
+// of token t, which is exactly its B operand of v_mfma_f32_16x16x32_bf16 (no LDS round
+// trip for q or for the gate's down rows); the A operand is 16 LDS state rows. The
+// accumulators then hold channels c = 16 mt + 4 g + v (mt = 0..7, v = 0..3) of token t, so
+// the SiLU/L2 of q, the gate's bias and sigmoid, RMSNorm·w·gate and the MXFP8 quantization
+// all run in those registers: a per-token sum or a per-32-block max needs only the four
+// lanes t, t + 16, t + 32, t + 48 (two permlane swaps).
 constexpr int kRoWaves = 8;
-constexpr int kQT = 16 * kRoWaves;
 constexpr int kRoThreads = 64 * kRoWaves;
-constexpr int kQRow = 136;  // padded bf16 row (272 bytes)
+constexpr int kQRow = 136;  // padded bf16 row of the LDS matrices (272 bytes)
 
 // The low-rank output gate of the linear branch, formed inside the readout instead of read:
 // gate[t, h*128 + c] = bf16(sigmoid(bf16(down[t] . up_w[h*128 + c] + up_b[h*128 + c]))), with
@@ -662,156 +670,224 @@ struct GateProj {
   const uint16_t* up_b;
 };
 
-// acc[nt] += A rows (tokens 16 wave + lane16) . B rows (16 nt + lane16) over K = 128, both
-// staged [row][k] with row stride kQRow: the readout's 128 x 128 x 128 tile product.
-__device__ __forceinline__ void tile_product(const uint16_t* sa, const uint16_t* sb, int wave,
-                                             int lane, f32x4* acc) {
-  const int lane16 = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const int kc = ks * 32 + g * 8;
-    const bf16x8 a = *reinterpret_cast<const bf16x8*>(&sa[(wave * 16 + lane16) * kQRow + kc]);
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      const bf16x8 b = *reinterpret_cast<const bf16x8*>(&sb[(nt * 16 + lane16) * kQRow + kc]);
-      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[nt], 0, 0, 0);
-    }
-  }
+// Sum / max over the lanes l, l ^ 16, l ^ 32, l ^ 48. Every lane gets the same bits:
+// (x0 + x1) + (x2 + x3) with operand order immaterial (IEEE addition commutes).
+__device__ __forceinline__ float sum_quad_rows(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const uint32_t w = __float_as_uint(s);
+  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// Two workgroups per CU (4 waves per SIMD): the kernel must stay within 128 VGPRs.
+__device__ __forceinline__ float max_quad_rows(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float s = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const uint32_t w = __float_as_uint(s);
+  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// Dispatch id -> logical id such that each XCD (dispatch is round-robin over 8) runs one
+// contiguous range of logical ids.
+__device__ __forceinline__ int xcd_contiguous(int b, int n) {
+  const int xcd = b & 7, local = b >> 3;
+  const int per = n >> 3, rem = n & 7;
+  return xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+}
+
+// acc[mt] += rows 16 mt .. 16 mt + 15 of the LDS matrix m ([row][k], row stride kQRow) times
+// the B operands b[ks] (this lane's token, K = 128 in 4 steps of 32).
+// The A rows are the same for every token group: `base` is made opaque per call, so the
+// compiler reads them from LDS each time instead of keeping all 64 fragments (256 VGPRs)
+// in registers across the group loop.
+__device__ __forceinline__ void rows_times_tokens(const uint16_t* m, const bf16x8 (&b)[4],
+                                                  int t16, int g, f32x4 (&acc)[8]) {
+  int base = t16 * kQRow + g * 8;
+  asm volatile("" : "+v"(base));
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(&m[base + mt * 16 * kQRow + ks * 32]);
+      acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[ks], acc[mt], 0, 0, 0);
+    }
+}
+
+// Fused readout: q' = bf16(L2(SiLU(q_raw))) (optional), y = bf16(q' · stateᵀ), then
+// o = bf16(RMSNorm(y)·w·gate) into bf16 out[f*S + s, h*D + c] or, with kMx, MXFP8 codes and
+// scales (token row f*S + s, chunk chunk0 + h). kProj forms the gate from GateProj; else it
+// is read from gv. Two workgroups per CU (four waves per SIMD): at most 128 VGPRs.
 template <bool kMx, bool kProj>
 __global__ void __launch_bounds__(kRoThreads) __attribute__((amdgpu_waves_per_eu(4)))
 vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
                    const void* __restrict__ weight, int weight_f32, float eps, View gv,
                    GateProj gp, uint16_t* __restrict__ out, int64_t o_sf, int64_t o_sh,
-                   int64_t o_ss, int spatial, int heads, int tiles, MxDst mx) {
-  __shared__ __attribute__((aligned(16))) uint16_t sState[kD * kQRow];  // [v][k], then gate
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[kQT * kQRow];     // [token][k], then y
-  const int tile = blockIdx.x % tiles;
-  const int fh = blockIdx.x / tiles;
-  const int f = fh / heads, h = fh % heads;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lane16 = tid & 15;
-  const int s0 = tile * kQT;
-  constexpr int kPasses = kQT / (kRoThreads / 16);
-  // a read gate: its rows are loaded first, so they arrive during the matmul
-  u32x4 gate_raw[kPasses];
-  // a formed gate: bf16 pairs of the gate tile in the accumulator layout
-  uint32_t gate_pk[8][2];
-  // the q rows (kPasses per thread) and the state (kStateLoads 16-byte pieces per thread)
-  constexpr int kStateLoads = kD * kD / (kRoThreads * 8);
-  const uint16_t* st = state + static_cast<int64_t>(fh) * kD * kD;
-  u32x4 q_raw[kPasses], st_raw[kStateLoads];
-  auto load_main = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < kStateLoads; ++i)
-      st_raw[i] = *reinterpret_cast<const u32x4*>(st + (tid + i * kRoThreads) * 8);
-#pragma unroll
-    for (int pass = 0; pass < kPasses; ++pass) {
-      const int s = s0 + pass * (kRoThreads / 16) + (tid >> 4);
-      q_raw[pass] = s < spatial ? *reinterpret_cast<const u32x4*>(qv.at(f, h, s) + lane16 * 8)
-                                : u32x4{0u, 0u, 0u, 0u};
-    }
-  };
-  if constexpr (!kProj) {
-#pragma unroll
-    for (int pass = 0; pass < kPasses; ++pass) {
-      const int s = s0 + pass * (kRoThreads / 16) + (tid >> 4);
-      gate_raw[pass] = s < spatial ? *reinterpret_cast<const u32x4*>(gv.at(f, h, s) + lane16 * 8)
-                                   : u32x4{0u, 0u, 0u, 0u};
-    }
-  } else {
-    // down rows of the tile's tokens -> sQ, head h's up rows -> sState
-    for (int idx = tid * 8; idx < kQT * kD; idx += kRoThreads * 8) {
-      const int r = idx >> 7, c = idx & 127, s = s0 + r;
-      *reinterpret_cast<u32x4*>(&sQ[r * kQRow + c]) =
-          s < spatial ? *reinterpret_cast<const u32x4*>(
-                            gp.down + (static_cast<int64_t>(f) * spatial + s) * gp.d_st + c)
-                      : u32x4{0u, 0u, 0u, 0u};
-    }
+                   int64_t o_ss, int spatial, int heads, int parts, MxDst mx) {
+  __shared__ __attribute__((aligned(16))) uint16_t sState[kD * kQRow];     // [c][k]
+  __shared__ __attribute__((aligned(16))) uint16_t sUp[kProj ? kD * kQRow : 8];
+  __shared__ __attribute__((aligned(16))) float sW[kD];
+  __shared__ __attribute__((aligned(16))) float sB[kD];
+  const int logical = xcd_contiguous(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int h = logical % heads;
+  const int fp = logical / heads;
+  const int part = fp % parts, f = fp / parts;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int t16 = lane & 15, g = lane >> 4;
+
+  const uint16_t* st = state + (static_cast<int64_t>(f) * heads + h) * kD * kD;
+  for (int idx = tid * 8; idx < kD * kD; idx += kRoThreads * 8)
+    *reinterpret_cast<u32x4*>(&sState[(idx >> 7) * kQRow + (idx & 127)]) =
+        *reinterpret_cast<const u32x4*>(st + idx);
+  if constexpr (kProj) {
     const uint16_t* up = gp.up_w + static_cast<int64_t>(h) * kD * kD;
     for (int idx = tid * 8; idx < kD * kD; idx += kRoThreads * 8)
-      *reinterpret_cast<u32x4*>(&sState[(idx >> 7) * kQRow + (idx & 127)]) =
+      *reinterpret_cast<u32x4*>(&sUp[(idx >> 7) * kQRow + (idx & 127)]) =
           *reinterpret_cast<const u32x4*>(up + idx);
-    __syncthreads();
-    load_main();  // the readout's operands arrive while the gate is formed
-    f32x4 acc[8];
+    if (tid < kD) sB[tid] = bf16_bits_to_f32(gp.up_b[h * kD + tid]);
+  }
+  if (tid < kD)
+    sW[tid] = weight_f32 ? static_cast<const float*>(weight)[tid]
+                         : bf16_bits_to_f32(static_cast<const uint16_t*>(weight)[tid]);
+  __syncthreads();
+
+  const int groups = (spatial + 15) >> 4;
+  const int per = (groups + parts - 1) / parts;
+  const int g_end = min(groups, (part + 1) * per);
+  const int64_t row0 = static_cast<int64_t>(f) * spatial;
+  for (int grp = part * per + wave; grp < g_end; grp += kRoWaves) {
+    const int s = grp * 16 + t16;
+    const bool valid = s < spatial;
+    // ---- q' as B operands ----
+    u32x4 qraw[4];
+    const uint16_t* qrow = qv.at(f, h, s) + g * 8;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    tile_product(sQ, sState, wave, lane, acc);
+    for (int ks = 0; ks < 4; ++ks)
+      qraw[ks] = valid ? *reinterpret_cast<const u32x4*>(qrow + ks * 32) : u32x4{0u, 0u, 0u, 0u};
+    // ---- gate (bf16 pairs in the accumulator layout) ----
+    uint32_t gate_pk[8][2];
+    if constexpr (kProj) {
+      u32x4 draw[4];
+      const uint16_t* drow = gp.down + (row0 + s) * gp.d_st + g * 8;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      const float b = bf16_bits_to_f32(gp.up_b[h * kD + nt * 16 + lane16]);
-      float gv4[4];
+      for (int ks = 0; ks < 4; ++ks)
+        draw[ks] = valid ? *reinterpret_cast<const u32x4*>(drow + ks * 32) : u32x4{0u, 0u, 0u, 0u};
+      bf16x8 db[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) db[ks] = __builtin_bit_cast(bf16x8, draw[ks]);
+      f32x4 ag[8];
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) ag[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      rows_times_tokens(sUp, db, t16, g, ag);
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        const f32x4 b = *reinterpret_cast<const f32x4*>(&sB[mt * 16 + g * 4]);
+        float gv4[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float z = round_bf16(ag[mt][v] + b[v]);
+          // sigmoid by the hardware exp2 and reciprocal: a few fp32 ulp from 1 / (1 + exp(-z)),
+          // below the bf16 rounding that follows
+          gv4[v] = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z * -1.4426950408889634f));
+        }
+        gate_pk[mt][0] = pack_bf16x2(gv4[0], gv4[1]);
+        gate_pk[mt][1] = pack_bf16x2(gv4[2], gv4[3]);
+      }
+    } else {
+      const uint16_t* grow = gv.at(f, h, s) + g * 4;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        const u32x2 w2 = valid ? *reinterpret_cast<const u32x2*>(grow + mt * 16) : u32x2{0u, 0u};
+        gate_pk[mt][0] = w2[0];
+        gate_pk[mt][1] = w2[1];
+      }
+    }
+    bf16x8 qb[4];
+    {
+      float qf[4][8];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) unpack8(qraw[ks], qf[ks]);
+      if (activate_q) {
+        // paper_sglang.py:235-238: y = silu(x); y / sqrt(max(sum y^2, 1e-12))
+        float ss = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            qf[ks][i] = silu(qf[ks][i]);
+            ss += qf[ks][i] * qf[ks][i];
+          }
+        const float inv = __builtin_amdgcn_rsqf(fmaxf(sum_quad_rows(ss), 1e-12f));
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) qf[ks][i] *= inv;
+      }
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) qb[ks] = __builtin_bit_cast(bf16x8, pack8(qf[ks]));
+    }
+    // ---- readout ----
+    f32x4 ay[8];
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) ay[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    rows_times_tokens(sState, qb, t16, g, ay);
+    // ---- RMSNorm(y)·w·gate (paper_sglang.py:398-403), rounded to bf16 ----
+    float ss = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float z = round_bf16(acc[nt][v] + b);
-        // sigmoid by the hardware exp2 and reciprocal: a few fp32 ulp from 1 / (1 + exp(-z)),
-        // below the bf16 rounding that follows
-        gv4[v] = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z * -1.4426950408889634f));
+        ay[mt][v] = round_bf16(ay[mt][v]);
+        ss += ay[mt][v] * ay[mt][v];
       }
-      gate_pk[nt][0] = pack_bf16x2(gv4[0], gv4[1]);
-      gate_pk[nt][1] = pack_bf16x2(gv4[2], gv4[3]);
+    const float inv = 1.0f / sqrtf(sum_quad_rows(ss) / static_cast<float>(kD) + eps);
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+      const f32x4 w = *reinterpret_cast<const f32x4*>(&sW[mt * 16 + g * 4]);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const uint32_t pk = gate_pk[mt][v >> 1];
+        const float gt = __uint_as_float(v & 1 ? pk & 0xffff0000u : pk << 16);
+        ay[mt][v] = round_bf16(ay[mt][v] * inv * w[v] * gt);
+      }
     }
-    __syncthreads();  // every wave is done with the down / up tiles
-  }
-  if constexpr (!kProj) load_main();
-#pragma unroll
-  for (int i = 0; i < kStateLoads; ++i) {
-    const int idx = (tid + i * kRoThreads) * 8;
-    *reinterpret_cast<u32x4*>(&sState[(idx >> 7) * kQRow + (idx & 127)]) = st_raw[i];
-  }
-  // q tile: kRoThreads / 16 tokens per pass (one 16-lane group per token); rows past the
-  // frame are zero
-#pragma unroll
-  for (int pass = 0; pass < kPasses; ++pass) {
-    const int r = pass * (kRoThreads / 16) + (tid >> 4);
-    float v[8];
-    unpack8(q_raw[pass], v);
-    if (activate_q) activate8(v, true);
-    *reinterpret_cast<u32x4*>(&sQ[r * kQRow + lane16 * 8]) = pack8(v);
-  }
-  __syncthreads();
-  // wave w: tokens [16w, 16w+16) x all 128 outputs; K = 128 in 4 steps of 32
-  f32x4 acc[8];
-#pragma unroll
-  for (int nt = 0; nt < 8; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int g = lane >> 4;
-  tile_product(sQ, sState, wave, lane, acc);
-  __syncthreads();  // every wave is done with sQ as the q tile and sState as the state
-#pragma unroll
-  for (int nt = 0; nt < 8; ++nt)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int at = (wave * 16 + g * 4 + v) * kQRow + nt * 16 + lane16;
-      sQ[at] = f32_to_bf16_bits(acc[nt][v]);
-      if constexpr (kProj)
-        sState[at] = static_cast<uint16_t>(v & 1 ? gate_pk[nt][v >> 1] >> 16
-                                                 : gate_pk[nt][v >> 1] & 0xffff);
-    }
-  __syncthreads();
-  float w[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    w[i] = weight_f32 ? static_cast<const float*>(weight)[lane16 * 8 + i]
-                      : bf16_bits_to_f32(static_cast<const uint16_t*>(weight)[lane16 * 8 + i]);
-#pragma unroll
-  for (int pass = 0; pass < kQT / (kRoThreads / 16); ++pass) {
-    const int r = pass * (kRoThreads / 16) + (tid >> 4);
-    const int s = s0 + r;
-    if (s >= spatial) continue;  // uniform per 16-lane group
-    float y[8];
-    unpack8(*reinterpret_cast<const u32x4*>(&sQ[r * kQRow + lane16 * 8]), y);
-    float o[8];
-    if constexpr (kProj)
-      norm_gate8(y, w, *reinterpret_cast<const u32x4*>(&sState[r * kQRow + lane16 * 8]), eps, o);
-    else
-      norm_gate8(y, w, gate_raw[pass], eps, o);
     if constexpr (kMx) {
-      quantize_store8(o, lane16, static_cast<int64_t>(f) * spatial + s, mx.chunk0 + h, mx.kp,
-                      mx.codes, mx.scales);
-    } else {
-      *reinterpret_cast<u32x4*>(out + f * o_sf + h * o_sh + s * o_ss + lane16 * 8) = pack8(o);
+      // 32-block b of the head's 128 channels = accumulator groups mt = 2b, 2b + 1
+      const int64_t row = row0 + s;
+      uint8_t* crow = mx.codes + row * mx.kp + (mx.chunk0 + h) * 128 + g * 4;
+      uint32_t word = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        float amax = 0.f;
+#pragma unroll
+        for (int m = 2 * b; m < 2 * b + 2; ++m)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) amax = fmaxf(amax, fabsf(ay[m][v]));
+        amax = max_quad_rows(amax);
+        float sinv;
+        word |= e8m0_from_amax(amax, &sinv) << (8 * b);
+#pragma unroll
+        for (int m = 2 * b; m < 2 * b + 2; ++m) {
+          int c = 0;
+          c = __builtin_amdgcn_cvt_pk_fp8_f32(ay[m][0] * sinv, ay[m][1] * sinv, c, false);
+          c = __builtin_amdgcn_cvt_pk_fp8_f32(ay[m][2] * sinv, ay[m][3] * sinv, c, true);
+          if (valid) *reinterpret_cast<uint32_t*>(crow + m * 16) = static_cast<uint32_t>(c);
+        }
+      }
+      if (valid && g == 0)
+        *reinterpret_cast<uint32_t*>(
+            mx.scales + swizzled_scale_offset(row, (mx.chunk0 + h) * 4, mx.kp >> 7)) = word;
+    } else if (valid) {
+      uint16_t* orow = out + f * o_sf + h * o_sh + s * o_ss + g * 4;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        u32x2 o2;
+        o2[0] = pack_bf16x2(ay[mt][0], ay[mt][1]);
+        o2[1] = pack_bf16x2(ay[mt][2], ay[mt][3]);
+        *reinterpret_cast<u32x2*>(orow + mt * 16) = o2;
+      }
     }
   }
 }
@@ -1019,19 +1095,25 @@ int launch_readout(const char* name, const void* q, int64_t q_sf, int64_t q_sh, 
                        "%s: codes need 16-byte alignment, a multiple-of-128 row length holding "
                        "chunks [chunk0, chunk0 + heads), scales 4-byte alignment", name);
   }
-  const int tiles = (spatial + kQT - 1) / kQT;
+  // Token-group ranges per (frame, head): enough workgroups to fill the GPU a few times
+  // over, each range at least one group per wave.
+  const int groups = (spatial + 15) / 16;
+  const int64_t fh = static_cast<int64_t>(frames) * heads;
+  int parts = static_cast<int>((4096 + fh - 1) / fh);
+  parts = std::max(1, std::min(parts, groups / kRoWaves));
+  if (fh * parts > (1ll << 31) - 1) return set_error(kUnsupported, "%s: grid too large", name);
   const View qv{static_cast<const uint16_t*>(q), q_sf, q_sh, q_ss};
   const View gv{static_cast<const uint16_t*>(gate), g_sf, g_sh, g_ss};
   const GateProj g = gp != nullptr ? *gp : GateProj{nullptr, 0, nullptr, nullptr};
   const MxDst m = mx != nullptr ? *mx : MxDst{nullptr, nullptr, 0, 0};
-  const dim3 grid(frames * heads * tiles), block(kRoThreads);
+  const dim3 grid(static_cast<unsigned>(fh * parts)), block(kRoThreads);
   const auto st = static_cast<hipStream_t>(stream);
   const auto* sp = static_cast<const uint16_t*>(state);
   auto* op = static_cast<uint16_t*>(out);
 #define VDN_READOUT(MX, PROJ)                                                                  \
   hipLaunchKernelGGL((vda_readout_kernel<MX, PROJ>), grid, block, 0, st, qv, activate_q, sp,   \
                      weight, weight_f32, eps, gv, g, op, o_sf, o_sh, o_ss, spatial, heads,      \
-                     tiles, m)
+                     parts, m)
   if (mx != nullptr && gp != nullptr)
     VDN_READOUT(true, true);
   else if (mx != nullptr)
