@@ -82,6 +82,22 @@ __device__ __forceinline__ void activate8(float* v, bool l2) {
   for (int i = 0; i < 8; ++i) v[i] = round_bf16(v[i]);
 }
 
+// activate8 without the final rounding: the caller rounds through the packing conversion.
+__device__ __forceinline__ void activate8_f32(float* v, bool l2) {
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[i] = silu(v[i]);
+    ss += v[i] * v[i];
+  }
+  if (l2) {
+    ss = sum16(ss);
+    const float inv = __builtin_amdgcn_rsqf(fmaxf(ss, 1e-12f));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] *= inv;
+  }
+}
+
 // Strided 3-D view of a bf16 [frames, heads, tokens, channel] operand; channels contiguous.
 struct View {
   const uint16_t* base;
@@ -139,11 +155,17 @@ vda_prepare_kernel(const void* __restrict__ x, int64_t n, int heads, int64_t sn,
 constexpr int kTS = 32;          // tokens per step
 constexpr int kRow = 144;        // padded LDS row (bf16 elements): 288 bytes
 constexpr int kTile = kTS * kRow;
+constexpr int kStWaves = 8;
+constexpr int kStThreads = 64 * kStWaves;
 
-// One workgroup per (frame, head); 4 waves, wave (wm, wn) owns the 64x64 quadrant
-// rows [64 wm, +64) x cols [64 wn, +64) of both A' = Kᵀ P and B' = Vbᵀ K.
+// One workgroup per (frame, head); 8 waves, wave w owns rows [64 (w / 4), +64) x columns
+// [32 (w % 4), +32) of both A' = Kᵀ P and B' = Vbᵀ K. Each step thread t loads token t / 16
+// of the step's 32, channels 8 (t % 16) .. +8, applies the activation and writes k', the
+// split products and vb to the step's LDS tiles. With bf16 beta (kSplit = 2) two
+// workgroups share a CU (16 waves): at most 128 VGPRs.
 template <int kSplit>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kStThreads)
+__attribute__((amdgpu_waves_per_eu(kSplit == 2 ? 4 : 2)))
 vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b_sf,
                       int64_t b_sh, int64_t b_ss, int beta_f32, int spatial, int heads,
                       int activate, float* __restrict__ A, float* __restrict__ B) {
@@ -152,78 +174,78 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
   const int fh = blockIdx.x;
   const int f = fh / heads, h = fh % heads;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
   const int lane16 = tid & 15;
   const int c8 = lane16 * 8;
+  const int r = tid >> 4;
   const int steps = (spatial + kTS - 1) / kTS;
 
-  // loader: thread handles tokens (tid/16) and (tid/16 + 16) of the step, channels c8..c8+7.
-  // Two steps of raw rows are in registers: `kraw` etc. (the next step, stored to LDS at the
-  // end of this one) and `kraw_n` etc. (the step after, loading meanwhile), so every global
-  // load has a whole step to arrive.
-  u32x4 kraw[2], vraw[2], kraw_n[2], vraw_n[2];
-  float braw[2], braw_n[2];
-  auto load_step = [&](int step, u32x4 (&kr)[2], u32x4 (&vr)[2], float (&br)[2])
-      __attribute__((always_inline)) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int s = step * kTS + (tid >> 4) + 16 * j;
-      if (s < spatial) {
-        kr[j] = *reinterpret_cast<const u32x4*>(kv.at(f, h, s) + c8);
-        vr[j] = *reinterpret_cast<const u32x4*>(vv.at(f, h, s) + c8);
-        const int64_t bo = f * b_sf + h * b_sh + s * b_ss;
-        br[j] = beta_f32 ? static_cast<const float*>(beta)[bo]
-                         : bf16_bits_to_f32(static_cast<const uint16_t*>(beta)[bo]);
-      } else {
-        kr[j] = u32x4{0, 0, 0, 0};
-        vr[j] = u32x4{0, 0, 0, 0};
-        br[j] = 0.f;
-      }
+  // The next step's raw rows load while this step's MFMAs run; they are activated and
+  // stored to the other LDS buffer at the step's end.
+  u32x4 kraw, vraw;
+  float braw;
+  auto load_step = [&](int step, u32x4& kr, u32x4& vr, float& br) __attribute__((always_inline)) {
+    const int s = step * kTS + r;
+    if (s < spatial) {
+      kr = *reinterpret_cast<const u32x4*>(kv.at(f, h, s) + c8);
+      vr = *reinterpret_cast<const u32x4*>(vv.at(f, h, s) + c8);
+      const int64_t bo = f * b_sf + h * b_sh + s * b_ss;
+      br = beta_f32 ? static_cast<const float*>(beta)[bo]
+                    : bf16_bits_to_f32(static_cast<const uint16_t*>(beta)[bo]);
+    } else {
+      kr = u32x4{0, 0, 0, 0};
+      vr = u32x4{0, 0, 0, 0};
+      br = 0.f;
     }
   };
+  // Each rounding to bf16 is the packing conversion (RNE); the packed words are the LDS
+  // tiles and, unpacked, the exact bf16 values the next step of the arithmetic uses.
   auto store_step = [&](int buf) __attribute__((always_inline)) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int r = (tid >> 4) + 16 * j;
-      float kf[8], vf[8];
-      unpack8(kraw[j], kf);
-      unpack8(vraw[j], vf);
-      if (activate) {
-        activate8(kf, true);
-        activate8(vf, false);
-      }
-      const float b = braw[j];
-      const float b16 = round_bf16(b);
-      float p[3][8], vb[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float prod = b * kf[i];  // exact for bf16 beta
-        const float hi = round_bf16(prod);
-        const float rem = prod - hi;  // exact
-        p[0][i] = hi;
-        if (kSplit == 2) {
-          p[1][i] = rem;  // representable in bf16 for bf16 beta
-        } else {
-          const float mid = round_bf16(rem);
-          p[1][i] = mid;
-          p[2][i] = rem - mid;
-        }
-        vb[i] = round_bf16(vf[i] * b16);
-      }
-      uint16_t* row0 = &lds[buf][0][r * kRow + c8];
-      *reinterpret_cast<u32x4*>(row0) = pack8(kf);
-#pragma unroll
-      for (int t = 0; t < kSplit; ++t)
-        *reinterpret_cast<u32x4*>(&lds[buf][1 + t][r * kRow + c8]) = pack8(p[t]);
-      *reinterpret_cast<u32x4*>(&lds[buf][1 + kSplit][r * kRow + c8]) = pack8(vb);
+    float kf[8], vf[8];
+    unpack8(kraw, kf);
+    unpack8(vraw, vf);
+    if (activate) {
+      activate8_f32(kf, true);
+      activate8_f32(vf, false);
     }
+    const u32x4 kw = pack8(kf);  // k' (bf16)
+    unpack8(kw, kf);
+    const float b = braw;
+    const float b16 = round_bf16(b);
+    float prod[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) prod[i] = b * kf[i];  // exact for bf16 beta
+    const u32x4 hw = pack8(prod);                       // hi = bf16(prod)
+    float hi[8];
+    unpack8(hw, hi);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) prod[i] -= hi[i];       // remainder, exact
+    uint16_t* row = &lds[buf][0][r * kRow + c8];
+    *reinterpret_cast<u32x4*>(row) = kw;
+    *reinterpret_cast<u32x4*>(row + kTile) = hw;
+    if constexpr (kSplit == 2) {
+      *reinterpret_cast<u32x4*>(row + 2 * kTile) = pack8(prod);  // representable for bf16 beta
+    } else {
+      const u32x4 mw = pack8(prod);
+      float mid[8];
+      unpack8(mw, mid);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) prod[i] -= mid[i];
+      *reinterpret_cast<u32x4*>(row + 2 * kTile) = mw;
+      *reinterpret_cast<u32x4*>(row + 3 * kTile) = pack8(prod);
+    }
+    const u32x4 vw = pack8(vf);  // v' (bf16)
+    unpack8(vw, vf);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vf[i] *= b16;
+    *reinterpret_cast<u32x4*>(row + (1 + kSplit) * kTile) = pack8(vf);  // bf16(v'·bf16(beta))
   };
 
-  f32x4 accA[4][4], accB[4][4];
+  f32x4 accA[4][2], accB[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
       accA[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
       accB[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -242,38 +264,33 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
 
   load_step(0, kraw, vraw, braw);
   store_step(0);
-  if (steps > 1) load_step(1, kraw, vraw, braw);
   __syncthreads();
   for (int step = 0; step < steps; ++step) {
     const int buf = step & 1;
     const bool more = step + 1 < steps;
-    if (step + 2 < steps) load_step(step + 2, kraw_n, vraw_n, braw_n);
+    if (more) load_step(step + 1, kraw, vraw, braw);
     const uint16_t* tk = lds[buf][0];
     const uint16_t* tv = lds[buf][1 + kSplit];
-    bf16x8 kn[4];  // K fragments for this wave's column blocks (B' operand B)
+    bf16x8 kn[2], pn[kSplit][2];
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) kn[nt] = frag(tk, wn * 64 + nt * 16);
+    for (int nt = 0; nt < 2; ++nt) {
+      kn[nt] = frag(tk, wn * 32 + nt * 16);
+#pragma unroll
+      for (int t = 0; t < kSplit; ++t) pn[t][nt] = frag(lds[buf][1 + t], wn * 32 + nt * 16);
+    }
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const bf16x8 km = frag(tk, wm * 64 + mt * 16);
       const bf16x8 vm = frag(tv, wm * 64 + mt * 16);
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
+      for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
-        for (int t = 0; t < kSplit; ++t) {
-          const bf16x8 pn = frag(lds[buf][1 + t], wn * 64 + nt * 16);
-          accA[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(km, pn, accA[mt][nt], 0, 0, 0);
-        }
+        for (int t = 0; t < kSplit; ++t)
+          accA[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(km, pn[t][nt], accA[mt][nt], 0, 0, 0);
         accB[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vm, kn[nt], accB[mt][nt], 0, 0, 0);
       }
     }
     if (more) store_step(buf ^ 1);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      kraw[j] = kraw_n[j];
-      vraw[j] = vraw_n[j];
-      braw[j] = braw_n[j];
-    }
     __syncthreads();
   }
 
@@ -284,16 +301,16 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+    for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int i = wm * 64 + mt * 16 + row_base + v;
-        const int j = wn * 64 + nt * 16 + lane16;
+        const int j = wn * 32 + nt * 16 + lane16;
         sA[i * kLd + j] = accA[mt][nt][v];
       }
   __syncthreads();
   float* An = A + static_cast<int64_t>(fh) * kD * kD;
-  for (int idx = tid; idx < kD * kD; idx += 256) {
+  for (int idx = tid; idx < kD * kD; idx += kStThreads) {
     const int i = idx >> 7, j = idx & 127;
     An[idx] = (sA[i * kLd + j] + sA[j * kLd + i]) * 0.5f;
   }
@@ -301,16 +318,16 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+    for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int i = wm * 64 + mt * 16 + row_base + v;
-        const int j = wn * 64 + nt * 16 + lane16;
+        const int j = wn * 32 + nt * 16 + lane16;
         sA[i * kLd + j] = round_bf16(accB[mt][nt][v]);
       }
   __syncthreads();
   float* Bn = B + static_cast<int64_t>(fh) * kD * kD;
-  for (int idx = tid; idx < kD * kD; idx += 256) Bn[idx] = sA[(idx >> 7) * kLd + (idx & 127)];
+  for (int idx = tid; idx < kD * kD; idx += kStThreads) Bn[idx] = sA[(idx >> 7) * kLd + (idx & 127)];
 }
 
 // ------------------------------------------------------------------- factors ----
@@ -967,10 +984,10 @@ VDN_API int vdn_vda_statistics(const void* k, int64_t k_sf, int64_t k_sh, int64_
   const View vv{static_cast<const uint16_t*>(v), v_sf, v_sh, v_ss};
   const dim3 grid(frames * heads);
   if (beta_f32)
-    hipLaunchKernelGGL(vda_statistics_kernel<3>, grid, dim3(256), 0, st, kv, vv, beta, b_sf, b_sh,
+    hipLaunchKernelGGL(vda_statistics_kernel<3>, grid, dim3(kStThreads), 0, st, kv, vv, beta, b_sf, b_sh,
                        b_ss, 1, spatial, heads, activate, A, B);
   else
-    hipLaunchKernelGGL(vda_statistics_kernel<2>, grid, dim3(256), 0, st, kv, vv, beta, b_sf, b_sh,
+    hipLaunchKernelGGL(vda_statistics_kernel<2>, grid, dim3(kStThreads), 0, st, kv, vv, beta, b_sf, b_sh,
                        b_ss, 0, spatial, heads, activate, A, B);
   return check_launch(name);
 }
