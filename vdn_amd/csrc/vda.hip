@@ -98,6 +98,14 @@ __device__ __forceinline__ void activate8_f32(float* v, bool l2) {
   }
 }
 
+// Dispatch id -> logical id such that each XCD (dispatch is round-robin over 8) runs one
+// contiguous range of logical ids.
+__device__ __forceinline__ int xcd_contiguous(int b, int n) {
+  const int xcd = b & 7, local = b >> 3;
+  const int per = n >> 3, rem = n & 7;
+  return xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+}
+
 // Strided 3-D view of a bf16 [frames, heads, tokens, channel] operand; channels contiguous.
 struct View {
   const uint16_t* base;
@@ -334,7 +342,9 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
 // One workgroup per matrix. Thread (ti, tj) = (tid / 16, tid % 16) keeps the 8x8 block
 // rows 8ti.., cols 8tj.. of M = I + A in registers; Gauss-Jordan without pivoting (I + A is
 // SPD, every pivot is >= 1), one pivot per step, pivot row/column broadcast through a
-// double-buffered LDS line so each step needs a single barrier.
+// double-buffered LDS line so each step needs a single barrier (a thread writes the line
+// of step k + 1 only after the barrier of step k, by which time every thread has read the
+// line of step k - 1 that it overwrites).
 __global__ void __launch_bounds__(256, 2)
 vda_factors_kernel(const float* __restrict__ A, const float* __restrict__ B,
                    const float* __restrict__ alpha, float* __restrict__ T,
@@ -360,41 +370,46 @@ vda_factors_kernel(const float* __restrict__ A, const float* __restrict__ B,
 #pragma unroll
     for (int r = 0; r < 8; ++r) m[r][r] += 1.0f;
   }
+  // Pivot k = 8 kb + kr: kb is the runtime loop, kr is unrolled, so the pivot row / column
+  // inside a thread's 8 x 8 block are compile-time rows / columns and only those 8 + 8
+  // elements need a select; the rest is one fma each.
 #pragma unroll 1
-  for (int k = 0; k < kD; ++k) {
-    const int buf = k & 1, kb = k >> 3, kr = k & 7;
-    if (ti == kb) {
+  for (int kb = 0; kb < kD / 8; ++kb) {
+    const bool row_owner = ti == kb, col_owner = tj == kb;
 #pragma unroll
-      for (int r = 0; r < 8; ++r)
-        if (r == kr) {
+    for (int kr = 0; kr < 8; ++kr) {
+      const int k = kb * 8 + kr;
+      const int buf = kr & 1;
+      if (row_owner) {
 #pragma unroll
-          for (int c = 0; c < 8; ++c) prow[buf][j0 + c] = m[r][c];
+        for (int c = 0; c < 8; ++c) prow[buf][j0 + c] = m[kr][c];
+      }
+      if (col_owner) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) pcol[buf][i0 + r] = m[r][kr];
+      }
+      __syncthreads();
+      const float rp = 1.0f / prow[buf][k];
+      float pr[8], pc[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) pr[c] = prow[buf][j0 + c] * rp;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) pc[r] = pcol[buf][i0 + r];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const float upd = m[r][c] - pc[r] * pr[c];
+          if (r == kr && c == kr) {
+            m[r][c] = row_owner && col_owner ? rp : (row_owner ? pr[c] : (col_owner ? -pc[r] * rp : upd));
+          } else if (r == kr) {
+            m[r][c] = row_owner ? pr[c] : upd;
+          } else if (c == kr) {
+            m[r][c] = col_owner ? -pc[r] * rp : upd;
+          } else {
+            m[r][c] = upd;
+          }
         }
-    }
-    if (tj == kb) {
-#pragma unroll
-      for (int c = 0; c < 8; ++c)
-        if (c == kr) {
-#pragma unroll
-          for (int r = 0; r < 8; ++r) pcol[buf][i0 + r] = m[r][c];
-        }
-    }
-    __syncthreads();
-    const float rp = 1.0f / prow[buf][k];
-    float pr[8], pc[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) pr[c] = prow[buf][j0 + c] * rp;
-#pragma unroll
-    for (int r = 0; r < 8; ++r) pc[r] = pcol[buf][i0 + r];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const bool pivot_row = (i0 + r) == k;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const bool pivot_col = (j0 + c) == k;
-        const float upd = m[r][c] - pc[r] * pr[c];
-        const float col = -pc[r] * rp;
-        m[r][c] = pivot_row ? (pivot_col ? rp : pr[c]) : (pivot_col ? col : upd);
       }
     }
   }
@@ -460,30 +475,43 @@ vda_factors_kernel(const float* __restrict__ A, const float* __restrict__ B,
 
 // --------------------------------------------------------- affine recurrence ----
 // state[16 x 128] <- state @ T + J over a sequence of frames. Workgroup = (row block of 16
-// state rows, head, direction[, chunk]); 4 waves, wave w owns output columns [32w, 32w+32).
+// state rows, head, direction[, chunk]); 8 waves, wave w owns output columns [16w, 16w+16).
 // state @ T runs on v_mfma_f32_16x16x4_f32: lane l feeds A = state[l%16][4k + l/16] and
-// B = T[4k + l/16][n0 + l%16]; the accumulator holds rows (l/16)*4 + v, column l%16.
+// B = T[4k + l/16][n0 + l%16]; the accumulator holds rows (l/16)*4 + v, column n0 + l%16.
+// The B operands of a step (the wave's 128 x 16 slice of T, 32 values per lane) and the
+// lane's 4 injection values are loaded straight into registers one step ahead: T and J do
+// not depend on the state, so only the MFMA chain and the state exchange through LDS are
+// serial. With 8 KB of LDS and at most 96 VGPRs, five waves share a SIMD and every row
+// block, head and direction of a 40-head launch runs at once.
 enum RecurMode : int { kScan = 0, kCompose = 1 };
 
+constexpr int kRecWaves = 8;
+constexpr int kRecThreads = 64 * kRecWaves;
+
 template <int kMode>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kRecThreads) __attribute__((amdgpu_waves_per_eu(5)))
 vda_recur_kernel(const float* __restrict__ Tm, const float* __restrict__ Jm, int heads,
                  const int* __restrict__ starts, const int* __restrict__ ends, int chunks,
                  const float* __restrict__ seed, int per_direction, float* __restrict__ out0,
                  float* __restrict__ out1) {
-  __shared__ __attribute__((aligned(16))) float sT[kD * kD];      // 64 KB
   // state rows; compose keeps a second state (the accumulated injection b)
   __shared__ __attribute__((aligned(16))) float sS[kMode == kCompose ? 2 : 1][16 * 132];
-  const int rb = blockIdx.x;  // 16-row block
-  const int dir = blockIdx.z;
+  // 1-D grid of (row block, head[, chunk], direction), row block fastest: the 8 row blocks
+  // that read one T run on one XCD, so its L2 fetches each T once per step.
+  const int logical = xcd_contiguous(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int rb = logical % (kD / 16);  // 16-row block
+  const int ys = logical / (kD / 16);
+  const int ny = kMode == kScan ? heads : static_cast<int>(gridDim.x) / (kD / 16) / 2;
+  const int by = ys % ny;
+  const int dir = ys / ny;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r0 = rb * 16;
   int h, c = 0;
   if (kMode == kScan) {
-    h = blockIdx.y;
+    h = by;
   } else {
-    h = blockIdx.y % heads;
-    c = blockIdx.y / heads;
+    h = by % heads;
+    c = by / heads;
   }
   const int64_t mat = kD * kD;
   // number of frames in the sequence and the frame index of step t
@@ -509,7 +537,7 @@ vda_recur_kernel(const float* __restrict__ Tm, const float* __restrict__ Jm, int
     return (static_cast<int64_t>(dir) * chunks + x) * heads + h;
   };
   // initial state: scan -> seed or zero; compose -> m = I (sS[0]), b = 0 (sS[1])
-  for (int idx = tid; idx < 16 * kD; idx += 256) {
+  for (int idx = tid; idx < 16 * kD; idx += kRecThreads) {
     const int i = idx >> 7, j = idx & 127;
     float s0;
     if (kMode == kScan) {
@@ -520,55 +548,67 @@ vda_recur_kernel(const float* __restrict__ Tm, const float* __restrict__ Jm, int
     }
     sS[0][i * 132 + j] = s0;
   }
-  const int n0 = wave * 32;
+  const int n0 = wave * 16;
   const int frow = lane & 15, fk = lane >> 4;
+  const int row_base = (lane >> 4) * 4;
+  constexpr int kStates = kMode == kCompose ? 2 : 1;
+  const int inj = kMode == kCompose ? 1 : 0;  // the state that receives the injection
+  float tcur[32], tnext[32], jcur[4], jnext[4];
+  // Buffer loads: the lane's offset is one VGPR, the matrix base and the row step are
+  // uniform (SGPRs), so the 36 loads of a step need no 64-bit address registers.
+  const int t_off = (fk * kD + n0 + frow) * 4;
+  const int j_off = ((r0 + row_base) * kD + n0 + frow) * 4;
+  auto load_step = [&](int t, float (&tb)[32], float (&jb)[4]) __attribute__((always_inline)) {
+    const int64_t m = in_index(frame_of(t)) * mat;
+    const __amdgpu_buffer_rsrc_t tr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Tm + m), 0, kD * kD * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t jr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Jm + m), 0, kD * kD * 4, 0x00020000);
+#pragma unroll
+    for (int kk = 0; kk < kD / 4; ++kk)
+      tb[kk] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(tr, t_off, kk * 4 * kD * 4, 0));
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      jb[v] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(jr, j_off, v * kD * 4, 0));
+  };
+  if (n_steps > 0) load_step(0, tcur, jcur);
+  __syncthreads();  // initial state written
   for (int t = 0; t < n_steps; ++t) {
     const int x = frame_of(t);
-    const float* Tx = Tm + in_index(x) * mat;
-    const float* Jx = Jm + in_index(x) * mat;
-    __syncthreads();  // previous step finished reading sT / writing sS
-    for (int idx = tid * 4; idx < kD * kD; idx += 256 * 4)
-      *reinterpret_cast<f32x4*>(&sT[idx]) = *reinterpret_cast<const f32x4*>(Tx + idx);
-    __syncthreads();
-    f32x4 acc[2][2];  // [state m / b][n tile]
+    if (t + 1 < n_steps) load_step(t + 1, tnext, jnext);
+    f32x4 acc[2];  // [state m / b]
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < 2; ++a) acc[a] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) acc[a][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    constexpr int kStates = kMode == kCompose ? 2 : 1;
-#pragma unroll 8
     for (int kk = 0; kk < kD / 4; ++kk) {
       const int krow = 4 * kk + fk;
-      const float b0 = sT[krow * kD + n0 + frow];
-      const float b1 = sT[krow * kD + n0 + 16 + frow];
 #pragma unroll
-      for (int a = 0; a < kStates; ++a) {
-        const float av = sS[a][frow * 132 + krow];
-        acc[a][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b0, acc[a][0], 0, 0, 0);
-        acc[a][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b1, acc[a][1], 0, 0, 0);
-      }
+      for (int a = 0; a < kStates; ++a)
+        acc[a] = __builtin_amdgcn_mfma_f32_16x16x4f32(sS[a][frow * 132 + krow], tcur[kk], acc[a],
+                                                      0, 0, 0);
     }
     __syncthreads();  // all waves done reading sS before it is overwritten
-    // the injection is added to the b state (compose) or the only state (scan)
-    const int inj = kMode == kCompose ? 1 : 0;
 #pragma unroll
     for (int a = 0; a < kStates; ++a)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+      for (int v = 0; v < 4; ++v) {
+        const int i = row_base + v;
+        const int j = n0 + frow;
+        float y = acc[a][v];
+        if (a == inj) y += jcur[v];
+        sS[a][i * 132 + j] = y;
+        if (kMode == kScan) out0[out_index(x) * mat + (r0 + i) * kD + j] = y;
+      }
+    __syncthreads();  // the new state is complete
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int i = (lane >> 4) * 4 + v;
-          const int j = n0 + nt * 16 + frow;
-          float y = acc[a][nt][v];
-          if (a == inj) y += Jx[(r0 + i) * kD + j];
-          sS[a][i * 132 + j] = y;
-          if (kMode == kScan) out0[out_index(x) * mat + (r0 + i) * kD + j] = y;
-        }
+    for (int kk = 0; kk < kD / 4; ++kk) tcur[kk] = tnext[kk];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) jcur[v] = jnext[v];
   }
   if (kMode == kCompose) {
     __syncthreads();
     const int64_t o = ((static_cast<int64_t>(dir) * chunks + c) * heads + h) * mat;
-    for (int idx = tid; idx < 16 * kD; idx += 256) {
+    for (int idx = tid; idx < 16 * kD; idx += kRecThreads) {
       const int i = idx >> 7, j = idx & 127;
       out0[o + (r0 + i) * kD + j] = sS[0][i * 132 + j];
       out1[o + (r0 + i) * kD + j] = sS[1][i * 132 + j];
@@ -705,14 +745,6 @@ __device__ __forceinline__ float max_quad_rows(float x) {
   const uint32_t w = __float_as_uint(s);
   const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-
-// Dispatch id -> logical id such that each XCD (dispatch is round-robin over 8) runs one
-// contiguous range of logical ids.
-__device__ __forceinline__ int xcd_contiguous(int b, int n) {
-  const int xcd = b & 7, local = b >> 3;
-  const int per = n >> 3, rem = n & 7;
-  return xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
 }
 
 // acc[mt] += rows 16 mt .. 16 mt + 15 of the LDS matrix m ([row][k], row stride kQRow) times
@@ -1018,7 +1050,10 @@ VDN_API int vdn_vda_compose(const float* T, const float* J, int heads, const int
       CI == nullptr)
     return set_error(kInvalidArgument, "%s: null pointer", name);
   if (heads <= 0 || chunks <= 0) return set_error(kInvalidArgument, "%s: bad geometry", name);
-  hipLaunchKernelGGL(vda_recur_kernel<kCompose>, dim3(kD / 16, heads * chunks, 2), dim3(256), 0,
+  if (static_cast<int64_t>(heads) * chunks * (kD / 16) * 2 > (1ll << 31) - 1)
+    return set_error(kUnsupported, "%s: grid too large", name);
+  const dim3 grid(kD / 16 * heads * chunks * 2);
+  hipLaunchKernelGGL(vda_recur_kernel<kCompose>, grid, dim3(kRecThreads), 0,
                      static_cast<hipStream_t>(stream), T, J, heads, starts, ends, chunks,
                      nullptr, 0, CT, CI);
   return check_launch(name);
@@ -1034,7 +1069,10 @@ VDN_API int vdn_vda_scan(const float* CT, const float* CI, const float* seed, in
   if (CT == nullptr || CI == nullptr || bank == nullptr)
     return set_error(kInvalidArgument, "%s: null pointer", name);
   if (heads <= 0 || chunks <= 0) return set_error(kInvalidArgument, "%s: bad geometry", name);
-  hipLaunchKernelGGL(vda_recur_kernel<kScan>, dim3(kD / 16, heads, 2), dim3(256), 0,
+  if (static_cast<int64_t>(heads) * (kD / 16) * 2 > (1ll << 31) - 1)
+    return set_error(kUnsupported, "%s: grid too large", name);
+  const dim3 grid(kD / 16 * heads * 2);
+  hipLaunchKernelGGL(vda_recur_kernel<kScan>, grid, dim3(kRecThreads), 0,
                      static_cast<hipStream_t>(stream), CT, CI, heads, nullptr, nullptr, chunks,
                      seed, per_direction, bank, nullptr);
   return check_launch(name);
