@@ -47,20 +47,17 @@ __device__ __forceinline__ u32x2 e4m3x8(const float* v) {
 // torch's GELU(approximate='tanh') in fp32, rounded to bf16 by the caller:
 //   0.5 x (1 + tanh(u)) = x / (1 + exp(-2u)),  u = sqrt(2/pi) (x + 0.044715 x^3).
 // The second form (1 + tanh(u) = 2 sigmoid(2u)) has no cancellation in the negative tail
-// and costs one hardware exp2 and one reciprocal instead of a libm tanh. Its fp32 result
-// is within a few ulp of the first, so the bf16 value agrees except where the exact value
-// lies within those few ulp of a bf16 rounding boundary.
-#pragma clang fp contract(off)
+// and costs one hardware exp2 and one reciprocal instead of a libm tanh. The exponent
+// -2u log2(e) = x (B + A x^2) is one multiply, one fma and one multiply, with
+// A = 0.044715 B and B = -2 sqrt(2/pi) / ln 2. The fp32 result is within a few ulp of the
+// first form, so the bf16 value agrees except where the exact value lies within those
+// few ulp of a bf16 rounding boundary.
 __device__ __forceinline__ float gelu_tanh(float x) {
-  const float kBeta = 0.7978845608028654f;        // sqrt(2/pi)
-  const float kKappa = 0.044715f;
-  const float kMinus2Log2e = -2.8853900817779268f;  // -2 / ln 2
-  const float cube = x * x * x;
-  const float inner = kBeta * (x + kKappa * cube);
-  const float e = __builtin_amdgcn_exp2f(inner * kMinus2Log2e);   // exp(-2u)
-  return x * __builtin_amdgcn_rcpf(1.f + e);
+  constexpr float kB = -2.302208198144325f;    // -2 sqrt(2/pi) / ln 2
+  constexpr float kA = -0.1029432395800235f;   // 0.044715 kB
+  const float z = x * __builtin_fmaf(x * x, kA, kB);
+  return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(z));
 }
-#pragma clang fp contract(on)
 
 // Quantizes the 8 values a lane holds (one quarter of a 32-block), stores the 8 codes
 // and, from lane 0 of each 16-lane group, the chunk's 4 scale bytes. A group is one DPP

@@ -84,6 +84,14 @@ __device__ __forceinline__ float epilogue_value(float y, float b, float addend, 
   return y;
 }
 
+__device__ __forceinline__ void unpack4(const u32x2 w, float* f) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
 __device__ __forceinline__ void unpack8(const u32x4 w, float* f) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -429,7 +437,7 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
 //         step s+1 is read into the same registers; step s+2's tiles are DMA'd into buffer
 //         s % 2 between the MFMA groups.
 // So the next step starts with its B fragments and first A fragment already in registers,
-// and a tile's epilogue (accumulators staged through a per-wave LDS strip, 16-byte stores)
+// and a tile's epilogue (straight from the accumulators: 8-byte bf16 or 4-byte MXFP8 stores)
 // runs while the next tile's first steps are in flight.
 // Tiles are fetched with buffer_load ... lds through buffer resources (rows past the padded
 // end read as zero) issued from inline asm (see buffer_to_lds16).
@@ -506,7 +514,7 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
                              int64_t n, int tiles_m, int tiles_n, int group_m) {
   constexpr int TM = 8, TN = 8;
   static_assert(kHead >= 1 && kHead < TM, "head groups");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kPStep + 4 * kPStageBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kPStep + (kMode == 2 ? 0 : 4 * kPStageBytes)];
 
   const int num_wg = tiles_m * tiles_n;
   const int grid = gridDim.x;
@@ -602,11 +610,101 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
 
   f32x4 acc[TM][TN];
 
-  // ---- epilogue of one tile: per wave, 16 rows at a time through its LDS strip ----
-  uint8_t* stage = lds + 2 * kPStep + wave * kPStageBytes;
   bool bad = false;
   u16x2 mag_max = {0, 0};   // bf16 output modes: largest magnitude bit pattern stored
-  auto epilogue = [&](int64_t m0, int64_t n0) __attribute__((always_inline)) {
+
+  // ---- producer epilogue of one tile (kMode 2), straight from the accumulators ----
+  // acc[mt][nt][v] is C[m0 + 128 wm + 16 mt + r][n0 + 128 wn + 16 nt + 4 g + v] with r = lane % 16
+  // and g = lane / 16: each lane holds 4 consecutive columns of one row, so their 4 codes
+  // leave as one 4-byte store, with no LDS staging. A 32-column block is nt = 2b, 2b + 1 of
+  // the four lanes g of a row (two permlane swaps give its amax), and the wave's 128 columns
+  // are one MXFP8 chunk, whose 4 scale bytes are one dword of the swizzled layout.
+  auto epilogue_direct = [&](int64_t m0, int64_t n0) __attribute__((always_inline)) {
+    const int64_t col0 = n0 + wn * 128 + c_lo * 4;       // + 16 nt
+    const int64_t rows0 = m0 + wm * 128 + frag_row;      // + 16 mt
+    // bias of the lane's 32 columns; a missing bias is -0: bf16(y + -0) = y exactly
+    float bias4[TN][4];
+#pragma unroll
+    for (int nt = 0; nt < TN; ++nt) {
+      const int64_t col = col0 + nt * 16;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) bias4[nt][v] = -0.f;
+      if (ep.bias == nullptr) continue;
+      if (ep.vec && col < n) {   // n % 8 == 0: the lane's 4 columns are all inside
+        unpack4(*reinterpret_cast<const u32x2*>(ep.bias + col), bias4[nt]);
+      } else if (!ep.vec) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (col + v < n) bias4[nt][v] = bf16_bits_to_f32(ep.bias[col + v]);
+      }
+    }
+    const int64_t chunk128 = (n0 + wn * 128) >> 7;
+    const bool chunk_in = chunk128 < (ep.kp_out >> 7);
+    // A rolled loop over the 8 row groups keeps one copy of the code; the accumulators
+    // (registers) are picked by a uniform branch chain, not indexed.
+#pragma nounroll
+    for (int mt = 0; mt < TM; ++mt) {
+      // y = bf16(acc)
+      float y[TN][4];
+#pragma unroll
+      for (int m = 0; m < TM; ++m) {
+        if (m != mt) continue;
+#pragma unroll
+        for (int nt = 0; nt < TN; ++nt) {
+          f32x4 a = acc[m][nt];
+          // the copy is opaque: the rounding below stays in this branch instead of being
+          // hoisted (for all 256 accumulators at once) out of the loop
+          asm volatile("" : "+v"(a));
+          u32x2 p;
+          p[0] = pack_bf16x2(a[0], a[1]);
+          p[1] = pack_bf16x2(a[2], a[3]);
+          unpack4(p, y[nt]);
+        }
+      }
+      const int64_t row = rows0 + mt * 16;
+      // bias, activation and bf16 rounding; rows >= out_rows and columns >= n are zero
+#pragma unroll
+      for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          float val = round_bf16(y[nt][v] + bias4[nt][v]);
+          if (ep.act == 1) val = round_bf16(gelu_tanh(val));
+          if (ep.nonfinite != nullptr) bad = bad || !(fabsf(val) < INFINITY);
+          const bool in = row < out_rows && col0 + nt * 16 + v < n;
+          y[nt][v] = in ? val : 0.f;
+        }
+      // every lane takes part in the block maxima; only the stores are predicated
+      const bool store = chunk_in && row < mp;
+      uint8_t* qrow = ep.q_out + row * ep.kp_out + chunk128 * 128 + c_lo * 4;
+      uint32_t word = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        float amax = 0.f;
+#pragma unroll
+        for (int nt = 2 * b; nt < 2 * b + 2; ++nt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) amax = fmaxf(amax, fabsf(y[nt][v]));
+        amax = max_quad_rows(amax);
+        float sinv;
+        word |= e8m0_from_amax(amax, &sinv) << (8 * b);
+#pragma unroll
+        for (int nt = 2 * b; nt < 2 * b + 2; ++nt) {
+          int c = 0;
+          c = __builtin_amdgcn_cvt_pk_fp8_f32(y[nt][0] * sinv, y[nt][1] * sinv, c, false);
+          c = __builtin_amdgcn_cvt_pk_fp8_f32(y[nt][2] * sinv, y[nt][3] * sinv, c, true);
+          if (store) *reinterpret_cast<uint32_t*>(qrow + nt * 16) = static_cast<uint32_t>(c);
+        }
+      }
+      if (store && c_lo == 0)
+        *reinterpret_cast<uint32_t*>(
+            ep.s_out + swizzled_scale_offset(row, chunk128 * 4, ep.kp_out >> 7)) = word;
+    }
+  };
+
+  // ---- bf16 epilogue of one tile (kModes 0, 1): per wave, 16 rows at a time through its LDS
+  // strip, so that each lane stores 16 contiguous bytes ----
+  uint8_t* stage = lds + 2 * kPStep + wave * kPStageBytes;
+  auto epilogue_staged = [&](int64_t m0, int64_t n0) __attribute__((always_inline)) {
     const int chunk = lane & 15;                       // 8 columns of the wave's 128
     const int64_t col = n0 + wn * 128 + chunk * 8;
     // Bias and gate of the lane's 8 columns. A missing bias is -0 and a missing gate 1:
@@ -628,7 +726,6 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
         gate8[e] = ep.gate != nullptr && in ? bf16_bits_to_f32(ep.gate[col + e]) : 1.f;
       }
     }
-    const int64_t chunk128 = (n0 + wn * 128) >> 7;
     // The residual rows of row group mt+1 are loaded while group mt is finished, so their
     // latency is paid once per tile rather than once per group.
     const int64_t rows0 = m0 + wm * 128 + c_lo;   // + 16 mt + 4 pass
@@ -675,28 +772,7 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
       for (int pass = 0; pass < 4; ++pass)
         yv[pass] = *reinterpret_cast<const u32x4*>(stage + (pass * 4 + c_lo) * kPStageStride +
                                                    chunk * 16);
-      if constexpr (kMode == 2) {
-        // the 16 lanes of a row hold its 128-column chunk in order: quantize_store8's layout
-        const bool chunk_in = chunk128 < (ep.kp_out >> 7);
-#pragma unroll
-        for (int pass = 0; pass < 4; ++pass) {
-          const int64_t row = row0 + pass * 4;
-          if (row >= mp || !chunk_in) continue;
-          float y[8];
-          unpack8(yv[pass], y);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            float v = 0.f;
-            if (row < out_rows && col + e < n) {
-              v = round_bf16(y[e] + bias8[e]);
-              if (ep.act == 1) v = round_bf16(gelu_tanh(v));
-              bad = bad || !(fabsf(v) < INFINITY);
-            }
-            y[e] = v;
-          }
-          quantize_store8(y, chunk, row, chunk128, ep.kp_out, ep.q_out, ep.s_out);
-        }
-      } else if (col < n) {
+      if (col < n) {
 #pragma unroll
         for (int pass = 0; pass < 4; ++pass) {
           const int64_t row = row0 + pass * 4;
@@ -816,7 +892,10 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
     int tm, tn;
     tile_coords(static_cast<int>(blockIdx.x) + c_tile * grid, num_wg, tiles_m, tiles_n, group_m,
                 tm, tn);
-    epilogue(static_cast<int64_t>(tm) * kPTile, static_cast<int64_t>(tn) * kPTile);
+    if constexpr (kMode == 2)
+      epilogue_direct(static_cast<int64_t>(tm) * kPTile, static_cast<int64_t>(tn) * kPTile);
+    else
+      epilogue_staged(static_cast<int64_t>(tm) * kPTile, static_cast<int64_t>(tn) * kPTile);
   }
   // the DMAs issued past the last step must land before the workgroup's LDS is released
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");

@@ -727,26 +727,6 @@ struct GateProj {
   const uint16_t* up_b;
 };
 
-// Sum / max over the lanes l, l ^ 16, l ^ 32, l ^ 48. Every lane gets the same bits:
-// (x0 + x1) + (x2 + x3) with operand order immaterial (IEEE addition commutes).
-__device__ __forceinline__ float sum_quad_rows(float x) {
-  const uint32_t u = __float_as_uint(x);
-  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const uint32_t w = __float_as_uint(s);
-  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
-__device__ __forceinline__ float max_quad_rows(float x) {
-  const uint32_t u = __float_as_uint(x);
-  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  const float s = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const uint32_t w = __float_as_uint(s);
-  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-
 // acc[mt] += rows 16 mt .. 16 mt + 15 of the LDS matrix m ([row][k], row stride kQRow) times
 // the B operands b[ks] (this lane's token, K = 128 in 4 steps of 32).
 // The A rows are the same for every token group: `base` is made opaque per call, so the
