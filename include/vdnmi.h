@@ -113,6 +113,21 @@ int vdn_vda_prepare(const void* tokens, int64_t n, int heads, int64_t row_stride
                     void* out, void* stream);
 
 /*
+ * paper_prepare with the linear branch's separable short conv, fused: tokens [frames *
+ * frame_h * frame_w, heads, 128] bf16 (row/head strides in elements, token f*S + y*W + x)
+ * -> depthwise 5x5 spatial conv per frame (zero padding 2; w_sp [heads*128, 5, 5] bf16),
+ * rounded to bf16 -> depthwise 5-tap temporal conv across frames (zero padding 2;
+ * w_tm [heads*128, 5] bf16) in fp32 -> SiLU (+ L2 over the 128 channels when l2norm) ->
+ * out [frames, heads, S, 128] bf16. One frame of tokens must span < 2 GiB.
+ * Replaces: paper_prepare with conv (src/models/linear_attention/paper_stack.py:43-47) ->
+ * LinearAttentionSepConv.spatial (src/models/linear_attention/features.py:175-196) +
+ * vdn_temporal_conv_act (src/models/linear_attention/paper_sglang.py:165-203).
+ */
+int vdn_vda_conv_prepare(const void* tokens, int heads, int64_t row_stride, int64_t head_stride,
+                         int frames, int frame_h, int frame_w, const void* w_sp,
+                         const void* w_tm, int l2norm, void* out, void* stream);
+
+/*
  * Joint statistics per (frame, head): A = (K^T diag(beta) K + transpose) / 2 (fp32-grade),
  * B = bf16(bf16(v * bf16(beta))^T k) (fp32 storage), A, B: [frames, heads, 128, 128] fp32.
  * k, v: bf16 operands; beta: bf16 (beta_f32 = 0) or fp32, addressed (f, h, s). activate = 1

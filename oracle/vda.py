@@ -19,6 +19,9 @@ Pins (tests/test_oracle_vda.py):
                  (tests/test_paper_stack_vda_ops.py:300-307)
   statistics     A symmetric, equals sum_s beta k k^T; B == bf16(bf16(v beta)^T k)
   prepare        torch SiLU / L2 over D
+  short conv     torch conv2d / conv1d (groups = channels) in float64; the reference test's
+                 temporal loop (test_paper_stack_vda_ops.py:43-49); a unit impulse weight
+                 reduces it to prepare
   eager path     float64 restatement at relative error < 4e-3 (the reference's own
                  branch-vs-fp64 bound, test_paper_stack_vda_ops.py:208-256)
 """
@@ -78,6 +81,42 @@ def prepare(tokens: torch.Tensor, frames: int, spatial: int, l2norm: bool) -> to
         x = x / x.square().sum(-1, keepdim=True).clamp_min(1e-12).sqrt()
     n, h, d = x.shape
     return x.reshape(frames, spatial, h, d).permute(0, 2, 1, 3).contiguous()
+
+
+def short_conv_prepare(tokens: torch.Tensor, frames: int, frame_h: int, frame_w: int,
+                       w_sp: torch.Tensor, w_tm: torch.Tensor, l2norm: bool,
+                       round_spatial: bool = True) -> torch.Tensor:
+    """paper_prepare with the separable short conv (paper_stack.py:43-47): the depthwise 5x5
+    spatial conv of each frame (cross-correlation, zero padding 2, no bias;
+    LinearAttentionSepConv.spatial, features.py:175-196), rounded to bf16 as the reference's
+    bf16 conv2d output is (round_spatial); then the depthwise 5-tap temporal conv across
+    frames, out[t] = sum_j x[t + j - 2] w_tm[:, j] with zero frames outside [0, F)
+    (vdn_temporal_conv_act, paper_sglang.py:165-203; the reference test's loop,
+    test_paper_stack_vda_ops.py:43-49); SiLU (+ L2 over D). tokens [F*S, H, D], token
+    f*S + y*W + x; w_sp [H*D, 5, 5]; w_tm [H*D, 5]. Returns float64 [F, H, S, D], not rounded.
+    Written as explicit shifted sums (no convolution routine)."""
+    n, h, d = tokens.shape
+    c = h * d
+    x = tokens.double().reshape(frames, frame_h, frame_w, c)
+    ws, wt = w_sp.double().reshape(c, 5, 5), w_tm.double().reshape(c, 5)
+    xp = torch.zeros(frames, frame_h + 4, frame_w + 4, c, dtype=torch.float64)
+    xp[:, 2:2 + frame_h, 2:2 + frame_w] = x
+    sp = torch.zeros_like(x)
+    for i in range(5):
+        for j in range(5):
+            sp += xp[:, i:i + frame_h, j:j + frame_w] * ws[:, i, j]
+    if round_spatial:
+        sp = bf16(sp.float()).double()
+    tp = torch.zeros(frames + 4, frame_h, frame_w, c, dtype=torch.float64)
+    tp[2:2 + frames] = sp
+    y = torch.zeros_like(sp)
+    for j in range(5):
+        y += tp[j:j + frames] * wt[:, j]
+    y = F.silu(y)
+    if l2norm:
+        y = y.reshape(frames, frame_h, frame_w, h, d)
+        y = y / y.square().sum(-1, keepdim=True).clamp_min(1e-12).sqrt()
+    return y.reshape(frames, frame_h * frame_w, h, d).permute(0, 2, 1, 3).contiguous()
 
 
 # --------------------------------------------------------------------- statistics ----
@@ -162,19 +201,29 @@ def epilogue(readout: torch.Tensor, weight: torch.Tensor, gate: torch.Tensor, ep
 
 
 def paper_branch(q_raw, k_raw, v_raw, beta, gate, alpha, bounds, frames, spatial, weight, eps,
-                 text=None, bridge=True, chunk_size=8):
+                 text=None, bridge=True, chunk_size=8, conv=None, frame_size=None):
     """The paper VDA body (paper_stack.py:266-318) at float64 with the bf16 rounding points
     of the reference's bf16 path: prepared q/k/v, B, the gathered state and the readout are
     rounded to bf16; A, the factors, scans and gather run in float64.
 
     q_raw/k_raw/v_raw [F*S, H, D]; beta [F*S, H]; gate [F*S, H, D]; alpha [F, H, D].
     text = (tk_raw, tv_raw, text_beta [L, H]) seeds both scans with half its injection.
+    conv = {proj: (w_sp [H*D, 5, 5], w_tm [H*D, 5])} convolves those projections
+    (short_conv_prepare; frame_size = (H_f, W_f)).
     Returns float64 [F*S, H*D] (not rounded) and intermediates.
     """
     h = q_raw.shape[1]
-    q = bf16(prepare(q_raw, frames, spatial, True).float()).double()
-    k = bf16(prepare(k_raw, frames, spatial, True).float()).double()
-    v = bf16(prepare(v_raw, frames, spatial, False).float()).double()
+
+    def prep(raw, proj, l2):
+        if conv is not None and proj in conv:
+            x = short_conv_prepare(raw, frames, *frame_size, *conv[proj], l2)
+        else:
+            x = prepare(raw, frames, spatial, l2)
+        return bf16(x.float()).double()
+
+    q = prep(q_raw, "q", True)
+    k = prep(k_raw, "k", True)
+    v = prep(v_raw, "v", False)
     b = beta.double().reshape(frames, spatial, h).permute(0, 2, 1)
     A, B = statistics(k, v, b)
     seed = None

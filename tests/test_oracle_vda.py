@@ -159,3 +159,81 @@ def test_paper_branch_oracle_matches_eager_in_float64():
     ref = ov.eager_branch_fp64(*raw, beta, gate, alpha, bounds, frames, spatial, w)
     rel = (out - ref).norm() / ref.norm()
     assert rel < 4e-3, rel.item()
+
+
+# ------------------------------------------------------------------- short conv ----
+
+def _conv_operands(frames, fh, fw, h, seed, d=128):
+    g = torch.Generator().manual_seed(seed)
+    tokens = torch.randn(frames * fh * fw, h, d, generator=g)
+    w_sp = torch.randn(h * d, 5, 5, generator=g) / 5
+    w_tm = torch.randn(h * d, 5, generator=g) / 5 ** 0.5
+    return tokens, w_sp, w_tm
+
+
+@pytest.mark.parametrize("frames,fh,fw", [(1, 1, 1), (3, 4, 6), (6, 5, 3)])
+@pytest.mark.parametrize("l2", [False, True])
+def test_short_conv_matches_torch_convolutions(frames, fh, fw, l2):
+    """The shifted-sum restatement against torch's depthwise conv2d / conv1d in float64
+    (cross-correlation, zero padding 2, groups = channels), then SiLU / L2 in float64."""
+    h, d = 2, 16
+    tokens, w_sp, w_tm = _conv_operands(frames, fh, fw, h, frames + fh, d)
+    c = h * d
+    got = ov.short_conv_prepare(tokens, frames, fh, fw, w_sp, w_tm, l2, round_spatial=False)
+    vol = tokens.double().reshape(frames, fh, fw, c).permute(0, 3, 1, 2)
+    sp = F.conv2d(vol, w_sp.double()[:, None], padding=2, groups=c)        # [F, C, fh, fw]
+    seq = sp.permute(2, 3, 1, 0).reshape(fh * fw, c, frames)                # [S, C, F]
+    tm = F.conv1d(seq, w_tm.double()[:, None], padding=2, groups=c)         # [S, C, F]
+    y = F.silu(tm.permute(2, 0, 1).reshape(frames, fh * fw, h, d))
+    if l2:
+        y = y / y.square().sum(-1, keepdim=True).clamp_min(1e-12).sqrt()
+    torch.testing.assert_close(got, y.permute(0, 2, 1, 3), atol=1e-12, rtol=1e-12)
+
+
+def test_short_conv_rounds_the_spatial_output_to_bf16():
+    """round_spatial rounds the spatial conv's output before the temporal taps: equal to
+    the unrounded path fed bf16-rounded spatial values (a temporal identity makes the
+    difference visible as exactly the bf16 rounding of the spatial sum)."""
+    frames, fh, fw, h, d = 3, 4, 5, 1, 8
+    tokens, w_sp, _ = _conv_operands(frames, fh, fw, h, 3, d)
+    w_tm = torch.zeros(h * d, 5)
+    w_tm[:, 2] = 1
+    rounded = ov.short_conv_prepare(tokens, frames, fh, fw, w_sp, w_tm, False)
+    exact = ov.short_conv_prepare(tokens, frames, fh, fw, w_sp, w_tm, False, round_spatial=False)
+    vol = tokens.double().reshape(frames, fh, fw, h * d).permute(0, 3, 1, 2)
+    sp = F.conv2d(vol, w_sp.double()[:, None], padding=2, groups=h * d)
+    sp16 = sp.float().bfloat16().double().permute(0, 2, 3, 1).reshape(frames, fh * fw, h, d)
+    torch.testing.assert_close(rounded, F.silu(sp16).permute(0, 2, 1, 3), atol=1e-12, rtol=1e-12)
+    assert not torch.equal(rounded, exact)
+
+
+def test_short_conv_unit_impulse_is_prepare():
+    """Unit-impulse spatial and temporal weights reduce the short conv to paper_prepare's
+    SiLU / L2 (bf16 inputs survive the spatial rounding exactly)."""
+    frames, fh, fw, h, d = 4, 3, 5, 2, 128
+    tokens = _conv_operands(frames, fh, fw, h, 5)[0].bfloat16().double()
+    w_sp = torch.zeros(h * d, 5, 5)
+    w_sp[:, 2, 2] = 1
+    w_tm = torch.zeros(h * d, 5)
+    w_tm[:, 2] = 1
+    for l2 in (False, True):
+        got = ov.short_conv_prepare(tokens, frames, fh, fw, w_sp, w_tm, l2)
+        torch.testing.assert_close(got, ov.prepare(tokens, frames, fh * fw, l2), atol=0, rtol=0)
+
+
+def test_short_conv_temporal_loop_of_the_reference_test():
+    """The reference test's own temporal oracle (test_paper_stack_vda_ops.py:43-49):
+    acc[t] += x[t + j - 2] * w[:, j] for in-range frames, on a spatial identity."""
+    frames, fh, fw, h, d = 7, 2, 3, 1, 16
+    tokens, _, w_tm = _conv_operands(frames, fh, fw, h, 11, d)
+    w_sp = torch.zeros(h * d, 5, 5)
+    w_sp[:, 2, 2] = 1
+    x = tokens.bfloat16().double().reshape(frames, fh * fw, h * d)
+    acc = torch.zeros_like(x)
+    for t in range(frames):
+        for j in range(5):
+            if 0 <= t + j - 2 < frames:
+                acc[t] += x[t + j - 2] * w_tm[:, j].double()
+    expected = F.silu(acc).reshape(frames, fh * fw, h, d).permute(0, 2, 1, 3)
+    got = ov.short_conv_prepare(tokens.bfloat16().double(), frames, fh, fw, w_sp, w_tm, False)
+    torch.testing.assert_close(got, expected, atol=1e-12, rtol=1e-12)

@@ -332,3 +332,97 @@ def test_gated_readout_rejects_bad_operands(device):
                   q.stride(0), 1, state.data_ptr(), w.data_ptr(), 1, 1e-6, down.data_ptr(),
                   down.stride(0), up_w.data_ptr(), up_b.data_ptr(), None, 0, 0, 0, None, None, 0,
                   0, frames, h, spatial, _lib.stream(q.device))
+
+
+# ------------------------------------------------------------------- short conv ----
+
+def _sep_conv(h, projs, seed):
+    torch.manual_seed(seed)
+    return vv.LinearAttentionSepConv(h * 128, projs).to(torch.bfloat16)
+
+
+def _conv_weights(conv, proj):
+    w_sp, w_tm = conv.weights(proj, torch.bfloat16)
+    return w_sp.float().reshape(-1, 5, 5), w_tm.float()
+
+
+@pytest.mark.parametrize("frames,fh,fw", [(1, 1, 1), (3, 7, 5), (5, 9, 12), (2, 16, 8),
+                                          (6, 10, 17)])
+@pytest.mark.parametrize("l2", [False, True])
+def test_conv_prepare_against_oracle(device, frames, fh, fw, l2):
+    """Fused spatial + temporal short conv, SiLU / L2, frame-major store, against the float64
+    restatement with the reference's bf16 rounding of the spatial output, at the reference
+    test's bf16 bound (rtol 0.008; test_paper_stack_vda_ops.py:52-54). The reference test
+    feeds its oracle the conv2d's own bf16 output; this oracle recomputes it, so where the
+    kernel's fp32 spatial sum and the float64 one round to neighbouring bf16 values the
+    temporal sum moves by one such step times a tap weight: that is the absolute slack,
+    2^-8 * max|spatial| * max|w_tm|, and it may be used by at most 1e-4 of the outputs.
+    Frame sizes cover partial 8 x 8 tiles and a frame smaller than the 5 x 5 stencil."""
+    h = 2
+    conv = _sep_conv(h, ("k",), frames * 31 + fw)
+    g = torch.Generator().manual_seed(fh)
+    raw = torch.randn(frames * fh * fw, h, 128, generator=g).bfloat16()
+    out = vv.paper_prepare(raw.to(device), frames=frames, spatial=fh * fw, l2norm=l2,
+                           conv=conv.to(device), proj="k", frame_size=(fh, fw))
+    assert out.shape == (frames, h, fh * fw, 128) and out.is_contiguous()
+    w_sp, w_tm = _conv_weights(conv.cpu(), "k")
+    ref = ov.short_conv_prepare(raw, frames, fh, fw, w_sp, w_tm, l2).to(torch.bfloat16).double()
+    vol = raw.double().reshape(frames, fh, fw, h * 128).permute(0, 3, 1, 2)
+    spatial = F.conv2d(vol, w_sp.double()[:, None], padding=2, groups=h * 128)
+    slack = 2.0 ** -8 * spatial.abs().max().item() * w_tm.abs().max().item()
+    diff = (out.cpu().double() - ref).abs()
+    outside = diff > 0.008 * ref.abs()
+    assert bool((diff <= 0.008 * ref.abs() + slack).all()), diff.max().item()
+    assert outside.double().mean().item() <= 1e-4
+
+
+def test_conv_prepare_on_fused_qkv_strides(device):
+    """K and V as strided column slices of one fused projection (the block's layout) give the
+    same bytes as the contiguous copies."""
+    frames, fh, fw, h = 4, 6, 9, 3
+    conv = _sep_conv(h, ("k", "v"), 4).to(device)
+    g = torch.Generator().manual_seed(2)
+    qkv = torch.randn(frames * fh * fw, 3 * h * 128, generator=g).bfloat16().to(device)
+    for i, proj in ((1, "k"), (2, "v")):
+        view = qkv[:, i * h * 128:(i + 1) * h * 128].view(-1, h, 128)
+        got = vv.paper_prepare(view, frames=frames, spatial=fh * fw, l2norm=proj == "k",
+                               conv=conv, proj=proj, frame_size=(fh, fw))
+        ref = vv.paper_prepare(view.contiguous(), frames=frames, spatial=fh * fw,
+                               l2norm=proj == "k", conv=conv, proj=proj, frame_size=(fh, fw))
+        assert torch.equal(got, ref)
+
+
+def test_conv_prepare_rejects_bad_geometry(device):
+    conv = _sep_conv(2, ("k",), 1).to(device)
+    raw = torch.zeros(12, 2, 128, dtype=torch.bfloat16, device=device)
+    with pytest.raises(ValueError, match="frame_size"):
+        vv.paper_prepare(raw, frames=2, spatial=6, l2norm=True, conv=conv, proj="k",
+                         frame_size=(2, 2))
+    wide = _sep_conv(3, ("k",), 1).to(device)
+    with pytest.raises(ValueError, match="channels"):
+        vv.paper_prepare(raw, frames=2, spatial=6, l2norm=True, conv=wide, proj="k",
+                         frame_size=(2, 3))
+    # projections the conv does not list take the plain SiLU / L2 path
+    plain = vv.paper_prepare(raw, frames=2, spatial=6, l2norm=True, conv=conv, proj="q",
+                             frame_size=(2, 3))
+    assert torch.equal(plain, vv.paper_prepare(raw, frames=2, spatial=6, l2norm=True))
+
+
+@pytest.mark.parametrize("projs", [("k", "v"), ("q", "k", "v")])
+@pytest.mark.parametrize("text", [False, True])
+def test_branch_with_short_conv_against_fp64_oracle(device, projs, text):
+    """The VDA body with the short conv on K and V (the released checkpoints) or on all
+    three projections, against the float64 oracle with the same convolutions."""
+    frames, fh, fw, h = 6, 5, 7, 2
+    spatial = fh * fw
+    raw, beta, gate, alpha, w, tx = _branch_inputs(frames, spatial, h, 17, text)
+    conv = _sep_conv(h, projs, 9)
+    weights = {p: _conv_weights(conv, p) for p in projs}
+    bounds = ov.window_bounds(frames, 1)
+    dev = lambda x: x.to(device)
+    out = vv.vda_forward(*map(dev, raw), dev(beta), dev(gate), dev(alpha), bounds, frames, spatial,
+                         dev(w), 1e-6, text=None if tx is None else tuple(map(dev, tx)),
+                         conv=conv.to(device), frame_size=(fh, fw))
+    ref, _ = ov.paper_branch(*raw, beta, gate, alpha, bounds, frames, spatial, w, 1e-6, text=tx,
+                             conv=weights, frame_size=(fh, fw))
+    close_rel(out, ref, 0.004)

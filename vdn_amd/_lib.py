@@ -33,6 +33,8 @@ SIGNATURES = {
     "vdn_mxfp8_gemm_act_quantize": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _ptr, _i32, _ptr,
                                     _ptr, _i64, _i64, _ptr, _ptr],
     "vdn_vda_prepare": [_ptr, _i64, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _ptr, _ptr],
+    "vdn_vda_conv_prepare": [_ptr, _i32, _i64, _i64, _i32, _i32, _i32, _ptr, _ptr, _i32, _ptr,
+                             _ptr],
     "vdn_vda_statistics": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64,
                            _i32, _i32, _i32, _i32, _i32, _ptr, _ptr, _ptr],
     "vdn_vda_factors": [_ptr, _ptr, _ptr, _i64, _ptr, _ptr, _ptr],

@@ -63,26 +63,9 @@ __device__ __forceinline__ u32x4 pack8(const float* v) {
   return w;
 }
 
-// SiLU (+ L2 over the 16-lane group's 128 channels) of 8 values, rounded to bf16.
-// paper_sglang.py:235-238: y = silu(x); y / sqrt(max(sum y^2, 1e-12)).
-__device__ __forceinline__ void activate8(float* v, bool l2) {
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    v[i] = silu(v[i]);
-    ss += v[i] * v[i];
-  }
-  if (l2) {
-    ss = sum16(ss);
-    const float inv = __builtin_amdgcn_rsqf(fmaxf(ss, 1e-12f));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] *= inv;
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = round_bf16(v[i]);
-}
-
-// activate8 without the final rounding: the caller rounds through the packing conversion.
+// SiLU (+ L2 over the 16-lane group's 128 channels) of 8 values, not rounded: the caller
+// rounds through the packing conversion. paper_sglang.py:235-238: y = silu(x);
+// y / sqrt(max(sum y^2, 1e-12)).
 __device__ __forceinline__ void activate8_f32(float* v, bool l2) {
   float ss = 0.f;
 #pragma unroll
@@ -616,6 +599,179 @@ vda_recur_kernel(const float* __restrict__ Tm, const float* __restrict__ Jm, int
   }
 }
 
+// ---------------------------------------------------------------- short conv ----
+// paper_prepare with the linear branch's separable short conv: depthwise 5x5 spatial conv
+// per frame (zero padding 2, no bias; LinearAttentionSepConv.spatial, features.py:175-196),
+// its output rounded to bf16 as the reference's bf16 conv2d returns it, then the depthwise
+// 5-tap temporal conv across frames (zero padding 2) in fp32, SiLU, L2 over the head's 128
+// channels, one rounding and the frame-major [F, H, S, 128] store (vdn_temporal_conv_act,
+// paper_sglang.py:165-203).
+// One workgroup per (head, 8 x 8 spatial tile) walks the frames in order. A frame's 12 x 12
+// input positions (the tile and its 2-position halo) x 128 channels come into LDS by
+// buffer-resource DMA, double-buffered; positions outside the frame read as zero. Wave w
+// computes the 4 x 4 position block (w / 2, w % 2) of the tile and lane l holds channels
+// 2l, 2l + 1, so the LDS reads of one position are 256 contiguous bytes. The rounded
+// spatial output of the last five frames stays in registers: when frame t is done, frame
+// t - 2 gets its temporal taps, SiLU and L2 (one wave reduction per position) and is
+// stored, 256 contiguous bytes per position.
+constexpr int kCvTile = 8;
+constexpr int kCvHalo = kCvTile + 4;
+constexpr int kCvPos = kCvHalo * kCvHalo;       // 144 staged positions
+constexpr int kCvBuf = kCvPos * kD * 2;         // 36864 bytes per frame
+
+__device__ __forceinline__ void cv_buffer_to_lds16(__amdgpu_buffer_rsrc_t r, uint32_t voffset,
+                                                   uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               ::"s"(lds_base), "v"(voffset), "s"(r) : "memory");
+}
+
+// Sum over the 64 lanes of a wave (every lane gets the same bits).
+__device__ __forceinline__ float wave_sum(float x) { return sum_quad_rows(sum16(x)); }
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+vda_conv_prepare_kernel(const uint16_t* __restrict__ tokens, int64_t row_stride,
+                        int64_t head_stride, int frames, int fh, int fw, int heads, int tiles_x,
+                        const void* __restrict__ w_sp, const void* __restrict__ w_tm, int l2norm,
+                        uint16_t* __restrict__ out) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2][kCvBuf];
+  const int h = blockIdx.x % heads;
+  const int tile = blockIdx.x / heads;
+  const int ty = tile / tiles_x, tx = tile % tiles_x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: LDS bases go in M0
+  const int spatial = fh * fw;
+
+  // ---- DMA: 36 wave instructions per frame, 9 per wave; instruction i loads staged
+  // positions 4i .. 4i + 3 (16 lanes each) into LDS bytes [1024 i, 1024 i + 1024) ----
+  uint32_t voff[9];
+#pragma unroll
+  for (int j = 0; j < 9; ++j) {
+    const int q = (wave * 9 + j) * 4 + (lane >> 4);
+    const int y = ty * kCvTile + q / kCvHalo - 2, x = tx * kCvTile + q % kCvHalo - 2;
+    const bool in = y >= 0 && y < fh && x >= 0 && x < fw;
+    voff[j] = in ? static_cast<uint32_t>(((y * fw + x) * row_stride + h * head_stride) * 2 +
+                                         (lane & 15) * 16)
+                 : 0x80000000u;   // past the resource's end: reads as zero
+  }
+  const uint32_t frame_bytes = static_cast<uint32_t>(spatial * row_stride * 2);
+  auto dma_frame = [&](int f, int buf) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(tokens + static_cast<int64_t>(f) * spatial * row_stride), 0,
+        static_cast<int>(frame_bytes), 0x00020000);
+    const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+        (__attribute__((address_space(3))) void*)(&lds[buf][0])));
+#pragma unroll
+    for (int j = 0; j < 9; ++j) cv_buffer_to_lds16(r, voff[j], base + (wave * 9 + j) * 1024);
+  };
+
+  // ---- bf16 weights of channels c0 = 128 h + 2 lane, c0 + 1, as channel pairs per tap ----
+  const int c0 = h * kD + 2 * lane;
+  const uint16_t* wsp16 = static_cast<const uint16_t*>(w_sp);
+  const uint16_t* wtm16 = static_cast<const uint16_t*>(w_tm);
+  uint32_t wsp[25], wtm[5];
+#pragma unroll
+  for (int i = 0; i < 25; ++i)
+    wsp[i] = static_cast<uint32_t>(wsp16[c0 * 25 + i]) | (static_cast<uint32_t>(wsp16[(c0 + 1) * 25 + i]) << 16);
+#pragma unroll
+  for (int i = 0; i < 5; ++i)
+    wtm[i] = static_cast<uint32_t>(wtm16[c0 * 5 + i]) | (static_cast<uint32_t>(wtm16[(c0 + 1) * 5 + i]) << 16);
+  auto lo = [](uint32_t w) { return __uint_as_float(w << 16); };
+  auto hi = [](uint32_t w) { return __uint_as_float(w & 0xffff0000u); };
+
+  const int by = wave >> 1, bx = wave & 1;
+  // spatial outputs (bf16 channel pairs) of frames t - 4 .. t, oldest first
+  uint32_t win[5][16];
+#pragma unroll
+  for (int k = 0; k < 5; ++k)
+#pragma unroll
+    for (int p = 0; p < 16; ++p) win[k][p] = 0u;
+
+  if (frames > 0) dma_frame(0, 0);
+  for (int t = 0; t < frames + 2; ++t) {
+    const int buf = t & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();   // frame t is in LDS; every wave is done with frame t - 1's buffer
+    if (t + 1 < frames) dma_frame(t + 1, buf ^ 1);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int p = 0; p < 16; ++p) win[k][p] = win[k + 1][p];
+    if (t < frames) {
+      float acc[4][4][2];
+#pragma unroll
+      for (int oy = 0; oy < 4; ++oy)
+#pragma unroll
+        for (int ox = 0; ox < 4; ++ox) acc[oy][ox][0] = acc[oy][ox][1] = 0.f;
+      const uint8_t* src = &lds[buf][((by * 4) * kCvHalo + bx * 4) * 256 + lane * 4];
+#pragma unroll
+      for (int ir = 0; ir < 8; ++ir) {
+        // one input row in flight at a time: the scheduler would otherwise hoist all 64 LDS
+        // reads (and their 128 unpacked values) ahead of the arithmetic
+        __builtin_amdgcn_sched_barrier(0);
+        float xr[8][2];
+#pragma unroll
+        for (int ic = 0; ic < 8; ++ic) {
+          const uint32_t w2 = *reinterpret_cast<const uint32_t*>(src + (ir * kCvHalo + ic) * 256);
+          xr[ic][0] = __uint_as_float(w2 << 16);
+          xr[ic][1] = __uint_as_float(w2 & 0xffff0000u);
+        }
+#pragma unroll
+        for (int oy = 0; oy < 4; ++oy) {
+          const int i = ir - oy;
+          if (i < 0 || i > 4) continue;
+#pragma unroll
+          for (int j = 0; j < 5; ++j) {
+            const float w0 = lo(wsp[i * 5 + j]), w1 = hi(wsp[i * 5 + j]);
+#pragma unroll
+            for (int ox = 0; ox < 4; ++ox) {
+              acc[oy][ox][0] = __builtin_fmaf(xr[ox + j][0], w0, acc[oy][ox][0]);
+              acc[oy][ox][1] = __builtin_fmaf(xr[ox + j][1], w1, acc[oy][ox][1]);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int oy = 0; oy < 4; ++oy)
+#pragma unroll
+        for (int ox = 0; ox < 4; ++ox) win[4][oy * 4 + ox] = pack_bf16x2(acc[oy][ox][0], acc[oy][ox][1]);
+    } else {
+#pragma unroll
+      for (int p = 0; p < 16; ++p) win[4][p] = 0u;
+    }
+    if (t < 2) continue;
+    // ---- frame o = t - 2: temporal taps, SiLU, L2, store ----
+    const int o = t - 2;
+    uint16_t* out_f = out + (static_cast<int64_t>(o) * heads + h) * spatial * kD;
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      float y[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float a = 0.f;
+#pragma unroll
+        for (int k = 0; k < 5; ++k) {
+          const float xv = __uint_as_float(c ? win[k][p] & 0xffff0000u : win[k][p] << 16);
+          a = __builtin_fmaf(xv, c ? hi(wtm[k]) : lo(wtm[k]), a);
+        }
+        y[c] = silu(a);
+      }
+      if (l2norm) {
+        const float inv = __builtin_amdgcn_rsqf(fmaxf(wave_sum(y[0] * y[0] + y[1] * y[1]), 1e-12f));
+        y[0] *= inv;
+        y[1] *= inv;
+      }
+      const int yy = ty * kCvTile + by * 4 + (p >> 2), xx = tx * kCvTile + bx * 4 + (p & 3);
+      if (yy < fh && xx < fw) {
+        // a 32-bit offset from the frame's base (a frame spans < 2 GiB), made opaque so the
+        // 16 offsets are not kept as 64-bit values across the frame loop
+        uint32_t off = static_cast<uint32_t>((yy * fw + xx) * kD + 2 * lane);
+        asm volatile("" : "+v"(off));
+        *reinterpret_cast<uint32_t*>(out_f + off) = pack_bf16x2(y[0], y[1]);
+      }
+    }
+  }
+}
+
 // ----------------------------------------------------------------- log prefix ----
 // logp[n, h, j] = sum_{u < n} log(max(alpha[u, h, j], 1e-12)), summed in frame order.
 __global__ void vda_log_prefix_kernel(const float* __restrict__ alpha, int frames, int hd,
@@ -971,6 +1127,39 @@ VDN_API int vdn_vda_prepare(const void* tokens, int64_t n, int heads, int64_t ro
   else
     hipLaunchKernelGGL(vda_prepare_kernel<false>, grid, dim3(256), 0, st, tokens, n, heads,
                        row_stride, head_stride, spatial, l2norm, out);
+  return check_launch(name);
+}
+
+// Reference: paper_stack.py:30-48 with a short conv -> LinearAttentionSepConv.spatial
+// (features.py:175-196, cudnn depthwise 5x5, bf16 output) + vdn_temporal_conv_act
+// (paper_sglang.py:165-203, frame_major = True). tokens [F*S, H, 128] bf16 (row / head
+// strides in elements, unit channel stride), token f*S + y*W + x; w_sp [H*128, 5, 5] and
+// w_tm [H*128, 5] bf16 (the module in the activation dtype, as the reference's conv2d
+// requires); out [F, H, S, 128] bf16.
+VDN_API int vdn_vda_conv_prepare(const void* tokens, int heads, int64_t row_stride,
+                                 int64_t head_stride, int frames, int frame_h, int frame_w,
+                                 const void* w_sp, const void* w_tm, int l2norm, void* out,
+                                 void* stream) {
+  const char* name = "vdn_vda_conv_prepare";
+  if (tokens == nullptr || w_sp == nullptr || w_tm == nullptr || out == nullptr)
+    return set_error(kInvalidArgument, "%s: null pointer", name);
+  if (heads <= 0 || frames <= 0 || frame_h <= 0 || frame_w <= 0)
+    return set_error(kInvalidArgument, "%s: positive heads, frames and frame size required", name);
+  if (!aligned16(tokens) || !stride8(row_stride) || !stride8(head_stride) || row_stride <= 0 ||
+      head_stride < 0)
+    return set_error(kInvalidArgument, "%s: bf16 rows need 16-byte alignment", name);
+  const int64_t spatial = static_cast<int64_t>(frame_h) * frame_w;
+  if (spatial * row_stride * 2 >= (1ll << 31) ||
+      (static_cast<int64_t>(heads) - 1) * head_stride + kD > row_stride)
+    return set_error(kUnsupported, "%s: one frame of tokens must span < 2 GiB with the heads inside a row",
+                     name);
+  const int tiles_x = (frame_w + kCvTile - 1) / kCvTile;
+  const int64_t wgs = static_cast<int64_t>(heads) * tiles_x * ((frame_h + kCvTile - 1) / kCvTile);
+  if (wgs > (1ll << 31) - 1) return set_error(kUnsupported, "%s: grid too large", name);
+  hipLaunchKernelGGL(vda_conv_prepare_kernel, dim3(static_cast<unsigned>(wgs)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(tokens),
+                     row_stride, head_stride, frames, frame_h, frame_w, heads, tiles_x, w_sp, w_tm,
+                     l2norm, static_cast<uint16_t*>(out));
   return check_launch(name);
 }
 

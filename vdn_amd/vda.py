@@ -17,6 +17,7 @@ from dataclasses import dataclass
 from functools import lru_cache
 
 import torch
+from torch import nn
 
 from . import _lib
 from .mxfp8 import mxfp8_destination
@@ -37,16 +38,71 @@ def _stream(t):
 
 # -------------------------------------------------------------------- prepare ----
 
+class LinearAttentionSepConv(nn.Module):
+    """The linear branch's separable short conv on the projections named in `projs`
+    (features.py:133-196): per projection a depthwise 5x5 spatial Conv2d `{proj}_sp` and a
+    depthwise 5-tap temporal Conv1d `{proj}_tm`, both bias-free, initialised N(0, 1/25) and
+    N(0, 1/5) as the reference does. Parameter names and shapes match, so a reference
+    state dict loads. The convolution itself runs in vdn_vda_conv_prepare (paper_prepare)."""
+
+    KERNEL = 5
+
+    def __init__(self, channels, projs=("k", "v")):
+        super().__init__()
+        self.projs = tuple(projs)
+        k = self.KERNEL
+        for name in self.projs:
+            sp = nn.Conv2d(channels, channels, k, padding=k // 2, groups=channels, bias=False)
+            nn.init.normal_(sp.weight, std=(k * k) ** -0.5)
+            tm = nn.Conv1d(channels, channels, k, padding=k // 2, groups=channels, bias=False)
+            nn.init.normal_(tm.weight, std=k ** -0.5)
+            setattr(self, f"{name}_sp", sp)
+            setattr(self, f"{name}_tm", tm)
+
+    def weights(self, proj, dtype):
+        """(w_sp [C, 25], w_tm [C, 5]) in `dtype`, contiguous (the temporal weight is cast to
+        the activation dtype as in spatial(), features.py:193-195)."""
+        w_sp = getattr(self, f"{proj}_sp").weight
+        w_tm = getattr(self, f"{proj}_tm").weight
+        c = w_sp.shape[0]
+        return (w_sp.detach().reshape(c, 25).to(dtype).contiguous(),
+                w_tm.detach().reshape(c, 5).to(dtype).contiguous())
+
+
+def _conv_prepare(tokens, frames, spatial, l2norm, conv, proj, frame_size):
+    if frame_size is None or frame_size[0] * frame_size[1] != spatial:
+        raise ValueError("convolution requires the exact spatial frame_size")
+    if tokens.dtype != torch.bfloat16:
+        raise NotImplementedError("the gfx950 short-conv kernel takes bf16 tokens")
+    n, h, d = tokens.shape
+    w_sp, w_tm = conv.weights(proj, tokens.dtype)
+    if w_sp.shape != (h * d, 25) or w_tm.shape != (h * d, 5):
+        raise ValueError(f"{proj} conv has {w_sp.shape[0]} channels, tokens {h * d}")
+    if w_sp.device != tokens.device:
+        raise ValueError("conv weights must be on the tokens' device")
+    if tokens.stride(-1) != 1 or tokens.stride(0) % 8 or tokens.stride(1) % 8 or tokens.data_ptr() % 16:
+        tokens = tokens.contiguous()
+    out = torch.empty((frames, h, spatial, d), dtype=tokens.dtype, device=tokens.device)
+    _lib.call("vdn_vda_conv_prepare", tokens.data_ptr(), h, tokens.stride(0), tokens.stride(1),
+              frames, int(frame_size[0]), int(frame_size[1]), w_sp.data_ptr(), w_tm.data_ptr(),
+              int(bool(l2norm)), out.data_ptr(), _stream(tokens))
+    return out
+
+
 def paper_prepare(tokens, *, frames, spatial, l2norm, conv=None, proj=None, frame_size=None):
-    """Raw [F*S, H, D] -> contiguous [F, H, S, D]: SiLU (+ L2 over D) (paper_stack.py:30-48)."""
+    """Raw [F*S, H, D] -> contiguous [F, H, S, D]: SiLU (+ L2 over D) (paper_stack.py:30-48).
+    With a LinearAttentionSepConv listing `proj`, the spatial and temporal convolutions run
+    first, fused into the same kernel (bf16 tokens; frame_size = (H_f, W_f))."""
     _cuda(tokens, "tokens")
     if tokens.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("paper_prepare supports BF16/FP32")
     if tokens.ndim != 3 or tokens.shape[0] != frames * spatial or min(frames, spatial) < 1:
         raise ValueError("tokens must be [frames*spatial, heads, dim] with positive sizes")
-    if conv is not None and proj in getattr(conv, "projs", ()):
-        raise NotImplementedError("short convolution is not part of this build's hot path")
     n, h, d = tokens.shape
+    if d != HEAD_DIM:
+        raise ValueError("head_dim 128 required")
+    if conv is not None and proj in getattr(conv, "projs", ()):
+        return _conv_prepare(tokens, frames, spatial, l2norm, conv, proj, frame_size)
     if d != HEAD_DIM:
         raise ValueError("head_dim 128 required")
     if tokens.stride(-1) != 1:
@@ -352,11 +408,28 @@ def _gate_projection(gp, n, h, device):
     return down, w.contiguous(), b.contiguous()
 
 
+def _q_view(q, frames, spatial):
+    """(q, (frame, head, token) strides) of token-major raw q [F*S, H, D] (any row / head
+    stride) or frame-major prepared q [F, H, S, D]; unit channel stride, 16-byte rows."""
+    if q.ndim == 4:
+        if q.shape[0] != frames or q.shape[2] != spatial:
+            raise ValueError("readout geometry mismatch")
+        strides = (q.stride(0), q.stride(1), q.stride(2))
+    elif q.ndim == 3 and q.shape[0] == frames * spatial:
+        strides = (spatial * q.stride(0), q.stride(1), q.stride(0))
+    else:
+        raise ValueError("readout geometry mismatch")
+    if q.stride(-1) != 1:
+        raise ValueError("readout geometry mismatch")
+    return q, strides
+
+
 def linear_readout(q, state, norm_weight, gate, eps, frames, spatial, *, activate_q=True,
                    out=None, out_mxfp8=None):
     """Fused q activation + readout + epilogue.
 
-    q: raw [F*S, H, D] bf16 (any row/head stride; prepared q with activate_q=False);
+    q: raw [F*S, H, D] bf16 (any row/head stride), or prepared q (token-major, or frame-major
+    [F, H, S, D] from paper_prepare) with activate_q=False;
     state: [F, H, D, D] bf16 from paper_gather; gate [F*S, H, D] bf16, or an
     OutputGateProjection, which the kernel turns into that gate itself.
     Returns (or writes into `out`) [F*S, H*D] bf16 = RMSNorm(bf16(q'·stateᵀ))·w·gate.
@@ -366,9 +439,9 @@ def linear_readout(q, state, norm_weight, gate, eps, frames, spatial, *, activat
     """
     _cuda(q, "q", torch.bfloat16)
     _cuda(state, "state", torch.bfloat16)
-    n, h, d = q.shape
-    if (d != HEAD_DIM or n != frames * spatial or state.shape != (frames, h, d, d)
-            or q.stride(-1) != 1):
+    q, qs = _q_view(q, frames, spatial)
+    n, h, d = frames * spatial, q.shape[-3] if q.ndim == 4 else q.shape[1], q.shape[-1]
+    if d != HEAD_DIM or state.shape != (frames, h, d, d):
         raise ValueError("readout geometry mismatch")
     if isinstance(gate, OutputGateProjection):
         return _gated_readout(q, state, norm_weight, gate, eps, frames, spatial, activate_q,
@@ -378,7 +451,6 @@ def linear_readout(q, state, norm_weight, gate, eps, frames, spatial, *, activat
         raise ValueError("readout geometry mismatch")
     state = state.contiguous()
     w = norm_weight.to(device=q.device).contiguous()
-    qs = (spatial * q.stride(0), q.stride(1), q.stride(0))
     gs = (spatial * gate.stride(0), gate.stride(1), gate.stride(0))
     if out_mxfp8 is not None:
         if out is not None:
@@ -401,11 +473,11 @@ def linear_readout(q, state, norm_weight, gate, eps, frames, spatial, *, activat
 
 
 def _gated_readout(q, state, norm_weight, gp, eps, frames, spatial, activate_q, out, out_mxfp8):
-    n, h, d = q.shape
+    q, qs = _q_view(q, frames, spatial)
+    n, h, d = frames * spatial, state.shape[1], HEAD_DIM
     down, up_w, up_b = _gate_projection(gp, n, h, q.device)
     state = state.contiguous()
     w = norm_weight.to(device=q.device).contiguous()
-    qs = (spatial * q.stride(0), q.stride(1), q.stride(0))
     common = (q.data_ptr(), *qs, int(bool(activate_q)), state.data_ptr(), w.data_ptr(),
               _weight_flag(w), float(eps), down.data_ptr(), down.stride(0), up_w.data_ptr(),
               up_b.data_ptr())
@@ -429,13 +501,15 @@ def _gated_readout(q, state, norm_weight, gp, eps, frames, spatial, activate_q, 
 
 def vda_forward(q_raw, k_raw, v_raw, beta, gate, alpha, bounds, num_frames, tokens_per_frame,
                 norm_weight, eps, *, chunk_size=8, bridge=True, text=None, out=None,
-                out_mxfp8=None):
+                out_mxfp8=None, conv=None, frame_size=None):
     """The paper VDA branch body on raw projections (paper_stack.py:266-318).
 
     q_raw/k_raw/v_raw: [F*S, H, 128] bf16 raw projections; beta [F*S, H]; gate [F*S, H, 128]
-    or an OutputGateProjection; alpha [F, H, 128] fp32. `text` = (tk_raw, tv_raw, text_beta) adds the prompt's virtual
-    frame (its factors share the batch; half its injection seeds both scans). `out` /
-    `out_mxfp8` as in linear_readout.
+    or an OutputGateProjection; alpha [F, H, 128] fp32. `text` = (tk_raw, tv_raw, text_beta)
+    adds the prompt's virtual frame (its factors share the batch; half its injection seeds
+    both scans). `conv` (a LinearAttentionSepConv, frame_size = (H_f, W_f)) convolves the
+    projections it lists before their activation; the prompt's tokens are not convolved.
+    `out` / `out_mxfp8` as in linear_readout.
     """
     f, s = num_frames, tokens_per_frame
     h = q_raw.shape[1]
@@ -443,7 +517,18 @@ def vda_forward(q_raw, k_raw, v_raw, beta, gate, alpha, bounds, num_frames, toke
     extra = 1 if text is not None else 0
     a = torch.empty((f + extra, h, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=device)
     b = torch.empty_like(a)
-    statistics_from_projections(k_raw, v_raw, beta, f, s, a[extra:], b[extra:])
+    projs = getattr(conv, "projs", ()) if conv is not None else ()
+    if "k" in projs or "v" in projs:
+        kp = paper_prepare(k_raw, frames=f, spatial=s, l2norm=True, conv=conv, proj="k",
+                           frame_size=frame_size)
+        vp = paper_prepare(v_raw, frames=f, spatial=s, l2norm=False, conv=conv, proj="v",
+                           frame_size=frame_size)
+        bs = (s * beta.stride(0), beta.stride(1), beta.stride(0))
+        ks = (h * s * HEAD_DIM, s * HEAD_DIM, HEAD_DIM)
+        _stats_call(kp, ks, vp, ks, beta, bs, f, h, s, 0, a[extra:], b[extra:])
+        del kp, vp
+    else:
+        statistics_from_projections(k_raw, v_raw, beta, f, s, a[extra:], b[extra:])
     if text is not None:
         tk, tv, tb = text
         statistics_from_projections(tk, tv, tb, 1, tk.shape[0], a[:1], b[:1])
@@ -461,6 +546,11 @@ def vda_forward(q_raw, k_raw, v_raw, beta, gate, alpha, bounds, num_frames, toke
     del transitions, injections
     state = paper_gather(bank, alpha, plan, seed, torch.bfloat16, bridge)
     del bank
+    if "q" in projs:
+        q = paper_prepare(q_raw, frames=f, spatial=s, l2norm=True, conv=conv, proj="q",
+                          frame_size=frame_size)
+        return linear_readout(q, state, norm_weight, gate, eps, f, s, activate_q=False, out=out,
+                              out_mxfp8=out_mxfp8)
     return linear_readout(q_raw, state, norm_weight, gate, eps, f, s, out=out,
                           out_mxfp8=out_mxfp8)
 
@@ -470,8 +560,7 @@ def paper_readout(branch, xv, num_frames, tokens_per_frame, bounds, qkv_raw, fra
                   frame_mean=None, text_beta=None):
     """Branch body with the reference signature (paper_stack.py:266-318). `branch` supplies
     beta_proj, alpha, output_gate, norm, bridge and paper_vda_chunk_size."""
-    if getattr(branch, "short_conv", None) is not None:
-        raise NotImplementedError("short convolution is not part of this build's hot path")
+    conv = getattr(branch, "short_conv", None)
     q, k, v = qkv_raw
     h = q.shape[1]
     if beta is None:
@@ -493,7 +582,7 @@ def paper_readout(branch, xv, num_frames, tokens_per_frame, bounds, qkv_raw, fra
     return vda_forward(q, k, v, beta.reshape(-1, h), gate, alpha, bounds,
                        num_frames, tokens_per_frame, branch.norm.weight, branch.norm.eps,
                        chunk_size=branch.paper_vda_chunk_size, bridge=branch.bridge == "alpha",
-                       text=text)
+                       text=text, conv=conv, frame_size=frame_size)
 
 
 def _output_gate(module, xv, heads):
