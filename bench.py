@@ -139,6 +139,46 @@ def breakdown_of(per, steps):
     return out
 
 
+def short_conv_prepare(cfg, hidden, frames, steps):
+    """The linear branch's short-conv feature prep (vdn_vda_conv_prepare) on K and V of the
+    clip shape, outside the block (the block's configuration has no short conv): random
+    N(0,1) K/V columns of a fused [T, 3H] projection, a random-init LinearAttentionSepConv.
+    Algorithmic bytes per projection: the bf16 input read once and the bf16 output written
+    once (2 x 2 B per element)."""
+    if steps <= 0:
+        return None
+    import torch
+    from vdn_amd import _lib
+    from vdn_amd import vda as vv
+    tokens = frames * HEIGHT * WIDTH
+    hd, heads = cfg.hidden, cfg.heads
+    g = torch.Generator(device=hidden.device).manual_seed(7)
+    qkv = torch.randn(tokens, 3 * hd, generator=g, device=hidden.device).to(torch.bfloat16)
+    torch.manual_seed(7)
+    conv = vv.LinearAttentionSepConv(hd, ("k", "v")).to(torch.bfloat16).to(hidden.device)
+
+    def run():
+        for i, proj in ((1, "k"), (2, "v")):
+            view = qkv[:, i * hd:(i + 1) * hd].view(tokens, heads, D)
+            vv.paper_prepare(view, frames=frames, spatial=HEIGHT * WIDTH, l2norm=proj == "k",
+                             conv=conv, proj=proj, frame_size=(HEIGHT, WIDTH))
+
+    run()
+    torch.cuda.synchronize()
+    with _lib.LaunchTimer({"vdn_vda_conv_prepare"}) as timer:
+        for _ in range(steps):
+            run()
+        torch.cuda.synchronize()
+    times = [t for _, _, t in timer.durations()]
+    ms = sum(times) / len(times)
+    nbytes = 2 * tokens * hd * 2
+    log(f"short-conv prepare: {ms:.3f} ms per projection")
+    return {"workload": f"K or V of [{tokens}, {hd}] bf16, 5x5 spatial + 5-tap temporal depthwise "
+                        f"conv, SiLU (+L2), frame-major store", "ms_per_projection": round(ms, 4),
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+
+
 def visible_pairs(frames, spatial, radius):
     """Query-key pairs per head of the +-radius frame window."""
     total = 0
@@ -375,6 +415,7 @@ def main():
     hb_bytes = sum(iso[n][3] for n in VDA_HBM_BOUND if n in iso)
     hb_gbs = hb_bytes / (hb_t * 1e-3) / 1e9
     w = [sum(iso[nm][i] for nm in ATTENTION if nm in iso) for i in range(4)]
+    conv = short_conv_prepare(cfg, hidden, frames, args.isolated_steps)
     traffic = traffic_per_launch()
 
     result = {
@@ -406,6 +447,7 @@ def main():
                                  "ms": round(hb_t / iso_steps, 3)},
         "window_attention_tflops": round(w[2] / (w[1] * 1e-3) / 1e12, 1),
         "window_attention_bf16_frac": round(w[2] / (w[1] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "short_conv_prepare": conv,
         "breakdown": breakdown,
         "breakdown_isolated_branches": breakdown_of(iso, iso_steps),
         "cpu_baseline": None,
