@@ -179,6 +179,91 @@ def short_conv_prepare(cfg, hidden, frames, steps):
             "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
 
 
+def production_geometry(steps):
+    """Both attention branches at the H3 production call's geometry on one GPU (random
+    inputs): 37 latent frames of 28 x 36 = 1008 tokens (37,296 video rows) followed by 1,200
+    global (text) rows, 56 heads x 128; a chunk-aligned window (VAE chunks of 5 frames,
+    radius 1: up to 15 frames) with anchor frames 0 and 36 dense in both directions; the VDA
+    branch on frames 1..35 (the anchors skipped and the bounds rebased by -1), with the K/V
+    short conv, the 1,200 text rows as its virtual frame and boundary chunks of 8 frames.
+    Window q/k are RMS-normalised N(0,1) rows (the QK-norm/RoPE pass is measured in the
+    block)."""
+    if steps <= 0:
+        return None
+    import torch
+    import torch.nn.functional as F
+    from vdn_amd import _lib
+    from vdn_amd import vda as vv
+    from vdn_amd import window as vw
+    frames, fh, fw, heads, text = 37, 28, 36, 56, 1200
+    tpf = fh * fw
+    video = frames * tpf
+    rows = video + text
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(11)
+    qkv = torch.randn(rows, 3, heads, D, generator=g, device=dev)
+    q = F.normalize(qkv[:, 0], dim=-1).mul(D ** 0.5).bfloat16()
+    k = F.normalize(qkv[:, 1], dim=-1).mul(D ** 0.5).bfloat16()
+    v = qkv[:, 2].bfloat16()
+    raw = torch.randn(rows, 3 * heads * D, generator=g, device=dev).bfloat16()
+    del qkv
+    layout = vw.SequenceLayout(rows, 0, frames, tpf, frame_height=fh, frame_width=fw,
+                               text_start=video, text_len=text)
+    bounds = vw.window_bounds(frames, 1, 5)
+    plan = vw.prepare_paper_window_plan(layout, bounds, "both", device=dev)
+    pairs = 0
+    for p in plan.passes:
+        for grp in p.groups:
+            nq = sum(b - a for a, b in grp.query_ranges)
+            nk = sum(b - a for a, b in grp.key_ranges)
+            pairs += nq * nk
+    # linear branch: frames 1 .. F-2, bounds rebased (branch.py:380-400)
+    lf = frames - 2
+    lrows = slice(tpf, (frames - 1) * tpf)
+    hd = heads * D
+    rq, rk, rv = (raw[lrows, i * hd:(i + 1) * hd].view(-1, heads, D) for i in range(3))
+    tk, tv = (raw[video:, i * hd:(i + 1) * hd].view(-1, heads, D) for i in (1, 2))
+    beta = torch.sigmoid(torch.randn(lf * tpf, heads, generator=g, device=dev)).bfloat16()
+    tbeta = torch.sigmoid(torch.randn(text, heads, generator=g, device=dev)).bfloat16()
+    down = torch.randn(lf * tpf, D, generator=g, device=dev).bfloat16()
+    up_w = (torch.randn(hd, D, generator=g, device=dev) * 0.05).bfloat16()
+    up_b = (torch.randn(hd, generator=g, device=dev) * 0.05).bfloat16()
+    alpha = torch.rand(lf, heads, D, generator=g, device=dev) * 0.1 + 0.9
+    lbounds = [(lo - 1, hi - 1) for lo, hi in bounds[1:-1]]
+    torch.manual_seed(11)
+    conv = vv.LinearAttentionSepConv(hd, ("k", "v")).to(torch.bfloat16).to(dev)
+    normw = torch.ones(D, device=dev)
+    gp = vv.OutputGateProjection(down, up_w, up_b)
+
+    def run():
+        vw.paper_window_attention(q, k, v, plan, enabled=True)
+        vv.vda_forward(rq, rk, rv, beta, gp, alpha, lbounds, lf, tpf, normw, 1e-6,
+                       chunk_size=8, text=(tk, tv, tbeta), conv=conv, frame_size=(fh, fw))
+
+    with torch.no_grad():
+        run()
+        torch.cuda.synchronize()
+        names = set(VDA_ENTRIES) | set(ATTENTION) | {"vdn_vda_conv_prepare"}
+        with _lib.LaunchTimer(names) as timer:
+            for _ in range(steps):
+                run()
+            torch.cuda.synchronize()
+    per = {}
+    for name, _, t in timer.durations():
+        per[name] = per.get(name, 0.0) + t / steps
+    attn = sum(per.get(n, 0.0) for n in ATTENTION)
+    vda = sum(t for n, t in per.items() if n not in ATTENTION)
+    log(f"production geometry: window {attn:.2f} ms, VDA branch {vda:.2f} ms")
+    return {"workload": (f"{frames} frames x {fh}x{fw} + {text} global rows, {heads}x{D} heads, "
+                         f"window chunk 5 radius 1, anchors both; VDA on frames 1..{frames - 2} "
+                         f"with K/V short conv and text state, chunk 8"),
+            "window_attention_ms": round(attn, 3),
+            "window_attention_tflops": round(4.0 * D * heads * pairs / (attn * 1e-3) / 1e12, 1),
+            "vda_branch_ms": round(vda, 3),
+            "vda_breakdown_ms": {n: round(t, 4) for n, t in sorted(per.items(), key=lambda x: -x[1])
+                                 if n not in ATTENTION}}
+
+
 def visible_pairs(frames, spatial, radius):
     """Query-key pairs per head of the +-radius frame window."""
     total = 0
@@ -416,6 +501,7 @@ def main():
     hb_gbs = hb_bytes / (hb_t * 1e-3) / 1e9
     w = [sum(iso[nm][i] for nm in ATTENTION if nm in iso) for i in range(4)]
     conv = short_conv_prepare(cfg, hidden, frames, args.isolated_steps)
+    production = production_geometry(args.isolated_steps)
     traffic = traffic_per_launch()
 
     result = {
@@ -448,6 +534,7 @@ def main():
         "window_attention_tflops": round(w[2] / (w[1] * 1e-3) / 1e12, 1),
         "window_attention_bf16_frac": round(w[2] / (w[1] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "short_conv_prepare": conv,
+        "production_geometry": production,
         "breakdown": breakdown,
         "breakdown_isolated_branches": breakdown_of(iso, iso_steps),
         "cpu_baseline": None,

@@ -426,3 +426,28 @@ def test_branch_with_short_conv_against_fp64_oracle(device, projs, text):
     ref, _ = ov.paper_branch(*raw, beta, gate, alpha, bounds, frames, spatial, w, 1e-6, text=tx,
                              conv=weights, frame_size=(fh, fw))
     close_rel(out, ref, 0.004)
+
+
+def test_branch_at_production_structure(device):
+    """The structure of the released checkpoints' call (configs/training/
+    stage_a1_c1_vdn_anchor.yaml): a chunk-aligned window (chunk 3, radius 1), anchor frames
+    dense in the softmax branch so the linear branch runs on frames 1 .. F-2 with the bounds
+    rebased by -1 (branch.py:380-400), K/V short conv, the text state as a virtual frame and
+    boundary chunks of 4 frames (the compose pass), against the float64 oracle."""
+    frames, fh, fw, h = 12, 4, 5, 2
+    spatial = fh * fw
+    lf = frames - 2
+    raw, beta, gate, alpha, w, tx = _branch_inputs(lf, spatial, h, 23, text=True)
+    bounds = ov.window_bounds(frames, 1, 3)
+    lbounds = [(lo - 1, hi - 1) for lo, hi in bounds[1:-1]]
+    conv = _sep_conv(h, ("k", "v"), 12)
+    weights = {p: _conv_weights(conv, p) for p in ("k", "v")}
+    dev = lambda x: x.to(device)
+    out = vv.vda_forward(*map(dev, raw), dev(beta), dev(gate), dev(alpha), lbounds, lf, spatial,
+                         dev(w), 1e-6, chunk_size=4, text=tuple(map(dev, tx)),
+                         conv=conv.to(device), frame_size=(fh, fw))
+    ref, _ = ov.paper_branch(*raw, beta, gate, alpha, lbounds, lf, spatial, w, 1e-6, text=tx,
+                             chunk_size=4, conv=weights, frame_size=(fh, fw))
+    plan = vv.paper_boundary_plan(lbounds, lf, "cpu", 4)
+    assert len(plan.cuts) - 1 < lf, "the boundary plan must compose several frames per chunk"
+    close_rel(out, ref, 0.004)
