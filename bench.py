@@ -264,6 +264,50 @@ def production_geometry(steps):
                                  if n not in ATTENTION}}
 
 
+def h3_block(steps, plans_of):
+    """The block at VDN-H3's widths: hidden 5376, 56 x 128 heads (attention width 7168),
+    SwiGLU FFN 14336 (up 5376 -> 28672 = [a | g], bf16, then the SwiGLU MXFP8 producer), on the
+    production clip size of 37 frames x 28 x 36 = 37,296 tokens, +-1 frame window, 512
+    context rows; random-init weights, synthetic inputs, one warmup block."""
+    if steps <= 0:
+        return None
+    import torch
+    from vdn_amd import _lib
+    from vdn_amd import window as vw
+    from vdn_amd.block import (BlockConfig, BlockWeights, HybridDiTBlock, cross_attention_plan,
+                               make_inputs)
+    cfg = BlockConfig(hidden=5376, heads=56, head_dim=128, ffn=14336, ffn_act="swiglu")
+    frames, fh, fw = 37, 28, 36
+    weights = BlockWeights.random(cfg, seed=0, device="cuda")
+    block = HybridDiTBlock(cfg, weights)
+    del weights
+    hidden, temb, ctx, layout, rope = make_inputs(cfg, frames, fh, fw, seed=1, device="cuda")
+    plan = vw.prepare_paper_window_plan(layout, vw.window_bounds(frames, cfg.radius),
+                                        device="cuda")
+    cplan = cross_attention_plan(hidden.shape[0], ctx.shape[0], "cuda")
+    plans = plans_of(plan, cplan, frames, fh * fw, hidden.shape[0], ctx.shape[0])
+    with torch.no_grad():
+        block(hidden, temb, ctx, layout, rope, plan, cplan)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with _lib.LaunchTimer(set(GEMMS) | {"vdn_mxfp8_act_quantize"}) as timer:
+            start.record()
+            for _ in range(steps):
+                block(hidden, temb, ctx, layout, rope, plan, cplan)
+            end.record()
+            torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    per = aggregate(timer, plans)
+    g = [sum(per[nm][i] for nm in GEMMS if nm in per) for i in range(4)]
+    log(f"H3 widths: {ms:.2f} ms per block")
+    return {"workload": f"block at hidden {cfg.hidden}, {cfg.heads}x{cfg.head_dim} heads, SwiGLU FFN "
+                        f"{cfg.ffn}, {frames} frames x {fh}x{fw} = {hidden.shape[0]} tokens, "
+                        f"+-1 frame window, {cfg.context} context rows",
+            "ms_per_block": round(ms, 3),
+            "mxfp8_gemm_tflops": round(g[2] / (g[1] * 1e-3) / 1e12, 1),
+            "swiglu_producer_ms": round(per.get("vdn_mxfp8_act_quantize", [0, 0.0])[1] / steps, 3)}
+
+
 def visible_pairs(frames, spatial, radius):
     """Query-key pairs per head of the +-radius frame window."""
     total = 0
@@ -502,6 +546,10 @@ def main():
     w = [sum(iso[nm][i] for nm in ATTENTION if nm in iso) for i in range(4)]
     conv = short_conv_prepare(cfg, hidden, frames, args.isolated_steps)
     production = production_geometry(args.isolated_steps)
+    h3 = h3_block(args.isolated_steps,
+                  lambda p, c, f, s, t, l: {p.device_plan.intervals.data_ptr():
+                                            visible_pairs(f, s, cfg.radius),
+                                            c.intervals.data_ptr(): t * l})
     traffic = traffic_per_launch()
 
     result = {
@@ -535,6 +583,7 @@ def main():
         "window_attention_bf16_frac": round(w[2] / (w[1] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "short_conv_prepare": conv,
         "production_geometry": production,
+        "h3_widths": h3,
         "breakdown": breakdown,
         "breakdown_isolated_branches": breakdown_of(iso, iso_steps),
         "cpu_baseline": None,

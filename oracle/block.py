@@ -89,12 +89,12 @@ class QuantizedLinear:
 
 def merge_lora(weight, lora_a, lora_b, scale):
     """W + bf16(scale * (B @ A)) per Q/K/V slice (lora.py:80-107: fp32 product, added in the
-    weight dtype before MXFP8 conversion)."""
-    hd = weight.shape[1]
+    weight dtype before MXFP8 conversion). weight [3 * inner, hidden]."""
+    inner = weight.shape[0] // 3
     w = weight.clone()
     for i in range(3):
         delta = (lora_b[i].float() @ lora_a[i].float()) * scale
-        w[i * hd:(i + 1) * hd] += delta.to(w.dtype)
+        w[i * inner:(i + 1) * inner] += delta.to(w.dtype)
     return w
 
 
@@ -154,7 +154,7 @@ class BlockOracle:
         still computed here, from the given upstream values where present, so a run can be
         checked piece by piece on its own inputs."""
         cfg, w = self.cfg, self.w
-        heads, d, hd = cfg.heads, cfg.head_dim, cfg.hidden
+        heads, d, hd = cfg.heads, cfg.head_dim, cfg.heads * cfg.head_dim
         shift, scale, gate = tables[0], tables[1], tables[2]
         spatial = height * width
         t = h.shape[0]
@@ -205,13 +205,17 @@ class BlockOracle:
         return self.co(co_in, residual=h), dict(co=co)
 
     def ffn_stage(self, h, tables, given=None):
-        """h + gate_mlp * down(GELU_tanh(up(prenorm(h; norm2, scale_mlp, shift_mlp)))); `given`
-        may hold another run's activation as dequantized MXFP8 ("act")."""
+        """h + gate_mlp * down(act(up(prenorm(h; norm2, scale_mlp, shift_mlp)))) with act
+        GELU-tanh, or SwiGLU a * silu(g) of up = [a | g] (cfg.ffn_act); `given` may hold another
+        run's activation as dequantized MXFP8 ("act")."""
         w = self.w
         shift, scale, gate = tables[3], tables[4], tables[5]
         x2 = self.prenorm(h, w["norm2"], scale, shift)
         up = self.up(x2)
-        act = torch.from_numpy(_mx.gelu_tanh(up.float().numpy())).double()
+        if getattr(self.cfg, "ffn_act", "gelu_tanh") == "swiglu":
+            act = torch.from_numpy(_mx.swiglu(up.float().numpy())).double()
+        else:
+            act = torch.from_numpy(_mx.gelu_tanh(up.float().numpy())).double()
         act_in = (given or {}).get("act", act).double()
         return self.down(act_in, residual=h, gate=gate), dict(up=up, act=act)
 
@@ -232,7 +236,7 @@ def eager_block_fp32(w: dict, cfg, h, temb, context, frames, height, width, cos,
     branch (branch.py:404-482), gated residuals (_post_ref), cross-attention, GELU-tanh FFN.
     The timed CPU baseline. h [T, H] float; returns float32 [T, H]."""
     f32 = torch.float32
-    heads, d, hd, eps = cfg.heads, cfg.head_dim, cfg.hidden, cfg.eps
+    heads, d, hd, eps = cfg.heads, cfg.head_dim, cfg.heads * cfg.head_dim, cfg.eps
     t, spatial = h.shape[0], height * width
     W = {k: v.to(f32) if v.is_floating_point() else v for k, v in w.items()}
     h = h.to(f32)
@@ -250,7 +254,7 @@ def eager_block_fp32(w: dict, cfg, h, temb, context, frames, height, width, cos,
     soft_gate = torch.sigmoid(small[:, :heads] + W["soft_gate_b"])
     beta = torch.sigmoid(small[:, heads:2 * heads])
     lin_gate = torch.sigmoid(F.linear(small[:, 2 * heads:], W["lgate_up_w"], W["lgate_up_b"]))
-    mean = x1.reshape(frames, spatial, hd).mean(1)
+    mean = x1.reshape(frames, spatial, -1).mean(1)
     alpha = _vda.frame_kda_alpha(mean, W["alpha_down_w"], W["alpha_up_w"], W["dt_bias"],
                                  W["a_log"], heads, d)
     c, s = cos.to(f32)[:, None], sin.to(f32)[:, None]
@@ -279,7 +283,11 @@ def eager_block_fp32(w: dict, cfg, h, temb, context, frames, height, width, cos,
     h = h + F.linear(co, W["co_w"], W["co_b"])
     shift, scale, gate = tables[3:]
     x2 = rms(h, W["norm2"]) * (1 + scale) + shift
-    up = F.gelu(F.linear(x2, W["up_w"], W["up_b"]), approximate="tanh")
+    if getattr(cfg, "ffn_act", "gelu_tanh") == "swiglu":
+        a, g = F.linear(x2, W["up_w"], W["up_b"]).chunk(2, dim=-1)
+        up = a * F.silu(g)
+    else:
+        up = F.gelu(F.linear(x2, W["up_w"], W["up_b"]), approximate="tanh")
     return h + gate * F.linear(up, W["down_w"], W["down_b"])
 
 

@@ -18,6 +18,11 @@ pytestmark = pytest.mark.gpu
 SMALL = BlockConfig(hidden=256, heads=2, head_dim=128, ffn=384, context=16, lora_rank=8,
                     lora_scale=0.5)
 WIDE = BlockConfig()
+# VDN-H3's widths: hidden 5376, 56 x 128 heads (attention width 7168), SwiGLU FFN 14336
+# (up 5376 -> 28672 = [a | g]); and a small block with the same structure
+H3 = BlockConfig(hidden=5376, heads=56, head_dim=128, ffn=14336, ffn_act="swiglu")
+SMALL_H3 = BlockConfig(hidden=384, heads=2, head_dim=128, ffn=320, ffn_act="swiglu", context=16,
+                       lora_rank=8, lora_scale=0.5)
 REL = 1e-2
 END_TO_END = 5e-2
 
@@ -104,6 +109,14 @@ def test_small_block_matches_oracle():
 
 def test_full_width_block_short_clip_matches_oracle():
     check(run(WIDE, 4, 4, 8, seed=12))
+
+
+def test_small_swiglu_block_with_attention_width_unlike_hidden_matches_oracle():
+    check(run(SMALL_H3, 4, 4, 8, seed=21))
+
+
+def test_h3_width_block_short_clip_matches_oracle():
+    check(run(H3, 3, 4, 8, seed=22))
 
 
 def test_block_is_deterministic_and_leaves_its_input_alone():

@@ -107,3 +107,29 @@ def test_mxfp8_composition_tracks_the_fp32_eager_block(small):
     # a block with the FFN (its smallest stage here) dropped is well outside that bound
     no_ffn = parts["h2"] - h.double()
     assert (no_ffn - ref).norm() / ref.norm() > 0.2
+
+
+SWIGLU = BlockConfig(hidden=384, heads=2, head_dim=128, ffn=320, ffn_act="swiglu", context=16,
+                     lora_rank=8, lora_scale=0.5)
+
+
+def test_swiglu_block_with_attention_width_unlike_hidden():
+    """VDN-H3's structure at small widths (hidden 384, attention 2 x 128, SwiGLU FFN 320):
+    the MXFP8 composition tracks the fp32 eager block, the activation is a * silu(g) of the up
+    projection's halves [a | g], and swapping the halves is far outside the bound."""
+    w = BlockWeights.random(SWIGLU, seed=6)
+    orc = ob.BlockOracle(w.tensors, SWIGLU)
+    assert w.qkv_w.shape == (3 * 256, 384) and w.o_w.shape == (384, 256)
+    assert w.up_w.shape == (640, 384) and w.down_w.shape == (384, 320)
+    h, temb, ctx, cos, sin = inputs(SWIGLU)
+    out, parts = orc.forward(h, temb, ctx, FRAMES, HEIGHT, WIDTH, cos, sin)
+    eager = ob.eager_block_fp32(w.tensors, SWIGLU, h, temb, ctx, FRAMES, HEIGHT, WIDTH, cos, sin)
+    delta, ref = out - h.double(), eager.double() - h.double()
+    assert (delta - ref).norm() / ref.norm() < 0.12
+    h3, own = orc.ffn_stage(parts["h2"], parts["tables"])
+    up = own["up"]
+    a, g = up[:, :320], up[:, 320:]
+    expect = omx.bf16_round((a * g / (1 + torch.exp(-g))).numpy())
+    assert np.allclose(own["act"].numpy(), expect, rtol=2 ** -7, atol=1e-6)
+    swapped = omx.bf16_round((g * a / (1 + torch.exp(-a))).numpy())
+    assert not np.allclose(own["act"].numpy(), swapped, rtol=2 ** -7, atol=1e-6)

@@ -37,10 +37,14 @@ from . import window as vw
 
 @dataclass(frozen=True)
 class BlockConfig:
+    """Block widths. The attention width heads * head_dim may differ from the hidden width
+    (VDN-H3: hidden 5376, 56 x 128 heads). ffn_act "gelu_tanh" (up: hidden -> ffn) or
+    "swiglu" (VDN-H3, mxfp8_kernels.py:62-64: up: hidden -> 2 ffn = [a | g], a * silu(g))."""
     hidden: int = 5120
     heads: int = 40
     head_dim: int = 128
     ffn: int = 13824
+    ffn_act: str = "gelu_tanh"
     context: int = 512
     lora_rank: int = 64
     lora_scale: float = 1.0
@@ -50,6 +54,16 @@ class BlockConfig:
     rope_theta: float = 10000.0
     vda_chunk: int = 8
     init_std: float = 0.02
+
+    @property
+    def inner(self) -> int:
+        """Attention width: heads * head_dim."""
+        return self.heads * self.head_dim
+
+    @property
+    def ffn_up(self) -> int:
+        """Output width of the FFN's up projection."""
+        return 2 * self.ffn if self.ffn_act == "swiglu" else self.ffn
 
 
 @dataclass
@@ -66,8 +80,11 @@ class BlockWeights:
 
     @staticmethod
     def random(cfg: BlockConfig, seed: int = 0, device="cpu") -> "BlockWeights":
+        if cfg.ffn_act not in ("gelu_tanh", "swiglu"):
+            raise ValueError("ffn_act must be gelu_tanh or swiglu")
         g = torch.Generator(device=device).manual_seed(seed)
         hd, h, n, f, r = cfg.hidden, cfg.heads, cfg.head_dim, cfg.ffn, cfg.lora_rank
+        inner, fu = cfg.inner, cfg.ffn_up
 
         def normal(*shape, std=cfg.init_std):
             return (torch.randn(*shape, generator=g, device=device) * std).to(torch.bfloat16)
@@ -81,31 +98,31 @@ class BlockWeights:
         t = dict(
             adaln_w=normal(6 * hd, hd), adaln_b=normal(6 * hd),
             norm1=ones_ish(hd), norm2=ones_ish(hd), norm3=ones_ish(hd),
-            qkv_w=normal(3 * hd, hd), qkv_b=normal(3 * hd),
-            lora_a=normal(3, r, hd), lora_b=normal(3, hd, r),
+            qkv_w=normal(3 * inner, hd), qkv_b=normal(3 * inner),
+            lora_a=normal(3, r, hd), lora_b=normal(3, inner, r),
             norm_q=ones_ish(n), norm_k=ones_ish(n),
-            o_w=normal(hd, hd), o_b=normal(hd), olin_w=normal(hd, hd),
+            o_w=normal(hd, inner), o_b=normal(hd), olin_w=normal(hd, inner),
             soft_gate_w=normal(h, hd), soft_gate_b=normal(h),
             beta_w=normal(h, hd),
-            lgate_down_w=normal(n, hd), lgate_up_w=normal(hd, n), lgate_up_b=normal(hd),
-            alpha_down_w=normal(n, hd), alpha_up_w=normal(hd, n),
+            lgate_down_w=normal(n, hd), lgate_up_w=normal(inner, n), lgate_up_b=normal(inner),
+            alpha_down_w=normal(n, hd), alpha_up_w=normal(inner, n),
             a_log=torch.log(a).float(), dt_bias=(dt + torch.log(-torch.expm1(-dt))).float(),
             vda_norm=ones_ish(n),
-            cq_w=normal(hd, hd), cq_b=normal(hd), ck_w=normal(hd, hd), ck_b=normal(hd),
-            cv_w=normal(hd, hd), cv_b=normal(hd), co_w=normal(hd, hd), co_b=normal(hd),
+            cq_w=normal(inner, hd), cq_b=normal(inner), ck_w=normal(inner, hd), ck_b=normal(inner),
+            cv_w=normal(inner, hd), cv_b=normal(inner), co_w=normal(hd, inner), co_b=normal(hd),
             norm_qc=ones_ish(n), norm_kc=ones_ish(n),
-            up_w=normal(f, hd), up_b=normal(f), down_w=normal(hd, f), down_b=normal(hd),
+            up_w=normal(fu, hd), up_b=normal(fu), down_w=normal(hd, f), down_b=normal(hd),
         )
         return BlockWeights(t)
 
     def merged_qkv(self, scale: float) -> torch.Tensor:
         """W_qkv with the rank-r LoRA of Q, K, V folded in: W += bf16(scale * (B @ A) in fp32)
         (lora.py:105-107)."""
-        hd = self.qkv_w.shape[1]
+        inner = self.qkv_w.shape[0] // 3
         w = self.qkv_w.clone()
         for i in range(3):
             delta = (self.lora_b[i].float() @ self.lora_a[i].float()) * scale
-            w[i * hd:(i + 1) * hd].add_(delta.to(w.dtype))
+            w[i * inner:(i + 1) * inner].add_(delta.to(w.dtype))
         return w
 
 
@@ -182,6 +199,7 @@ class HybridDiTBlock(nn.Module):
         cfg, k = self.cfg, self.keep
         T, hd = hidden.shape
         heads, d = cfg.heads, cfg.head_dim
+        inner = cfg.inner
         frames, spatial = layout.num_frames, layout.tokens_per_frame
         dev = hidden.device
         shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = self.adaln_tables(temb)
@@ -199,9 +217,9 @@ class HybridDiTBlock(nn.Module):
         snap("tables", (shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp))
         snap("x1", x1)
         snap("qkv", qkv)
-        raw_q = qkv[:, :hd].view(T, heads, d)
-        raw_k = qkv[:, hd:2 * hd].view(T, heads, d)
-        value = qkv[:, 2 * hd:].view(T, heads, d)
+        raw_q = qkv[:, :inner].view(T, heads, d)
+        raw_k = qkv[:, inner:2 * inner].view(T, heads, d)
+        value = qkv[:, 2 * inner:].view(T, heads, d)
         small = F.linear(x1, self.small_w)
         soft_gate = torch.sigmoid(small[:, :heads] + k["soft_gate_b"])
         beta = torch.sigmoid(small[:, heads:2 * heads])
@@ -216,7 +234,7 @@ class HybridDiTBlock(nn.Module):
         # snapshots and quantized afterwards, which gives the same bytes.
         bounds = window_plan.bounds
         if parts is None:
-            qb, sb = mx.empty_activation(T, 2 * hd, dev)
+            qb, sb = mx.empty_activation(T, 2 * inner, dev)
 
             def linear_branch():
                 vv.vda_forward(raw_q, raw_k, value, beta, lin_gate, alpha, bounds,
@@ -246,15 +264,15 @@ class HybridDiTBlock(nn.Module):
         else:
             q, kk = vw.paper_qk_rmsnorm_rope(raw_q, raw_k, k["norm_q"], k["norm_k"], cfg.eps,
                                              cos, sin, enabled=True)
-            both = torch.empty((T, 2 * hd), dtype=torch.bfloat16, device=dev)
+            both = torch.empty((T, 2 * inner), dtype=torch.bfloat16, device=dev)
             vw.paper_window_attention(q, kk, value, window_plan, d ** -0.5, enabled=True,
-                                      gate=soft_gate, out=both[:, :hd].view(T, heads, d))
+                                      gate=soft_gate, out=both[:, :inner].view(T, heads, d))
             del q, kk
             vv.vda_forward(raw_q, raw_k, value, beta, lin_gate, alpha, bounds,
                            frames, spatial, k["vda_norm"], cfg.eps, chunk_size=cfg.vda_chunk,
-                           out=both[:, hd:])
-            snap("soft", both[:, :hd])
-            snap("far", both[:, hd:])
+                           out=both[:, inner:])
+            snap("soft", both[:, :inner])
+            snap("far", both[:, inner:])
             qb, sb = mx.launch_quantize(both)
             del both
         del qkv, raw_q, raw_k, value, lin_gate
@@ -276,12 +294,12 @@ class HybridDiTBlock(nn.Module):
         cq = vw.qk_rmsnorm(cq, k["norm_qc"], cfg.eps)
         ck = vw.qk_rmsnorm(ck, k["norm_kc"], cfg.eps)
         if parts is None:
-            qo, so = mx.empty_activation(T, hd, dev)
+            qo, so = mx.empty_activation(T, inner, dev)
             cross_attention(cq, ck, cv, cross_plan, d ** -0.5, out_mxfp8=(qo, so, 0))
         else:
             co = cross_attention(cq, ck, cv, cross_plan, d ** -0.5)
-            snap("co", co.view(T, hd))
-            qo, so = mx.launch_quantize(co.view(T, hd))
+            snap("co", co.view(T, inner))
+            qo, so = mx.launch_quantize(co.view(T, inner))
             del co
         del cq, ck, cv
         self.co.forward_quantized(qo, so, rows=T, out=h, residual=h)
@@ -291,7 +309,14 @@ class HybridDiTBlock(nn.Module):
         # ---- FFN ----
         _, q4, s4, _ = mx.launch_prenorm_quantize(h, k["norm2"], cfg.eps, scale_mlp, shift_mlp,
                                                   idx, write_bf16=False)
-        q5, s5 = self.up.forward_act_quantized(q4, s4, rows=T, act="gelu_tanh")
+        if cfg.ffn_act == "swiglu":
+            # up -> bf16 [T, 2 ffn] = [a | g], then the SwiGLU producer (tp_ff_forward,
+            # tensor_parallel.py:147-161: project, launch_swiglu_quantize)
+            up = self.up.forward_quantized(q4, s4, rows=T)
+            q5, s5, _ = mx.launch_swiglu_quantize(up)
+            del up
+        else:
+            q5, s5 = self.up.forward_act_quantized(q4, s4, rows=T, act="gelu_tanh")
         snap("ffn_codes", (q5, s5))
         self.down.forward_quantized(q5, s5, rows=T, out=h, residual=h, gate=gate_mlp)
         return (h, parts) if return_parts else h
