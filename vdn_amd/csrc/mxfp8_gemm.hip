@@ -735,8 +735,9 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
 #pragma unroll
       for (int pass = 0; pass < 4; ++pass) {
         const int64_t row = rows0 + mt * 16 + pass * 4;
-        if (row < out_rows)
-          r[pass] = *reinterpret_cast<const u32x4*>(ep.residual + row * ep.ld_res + col);
+        if (row < out_rows)   // read once: a streaming load, like the output store
+          r[pass] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4*>(ep.residual + row * ep.ld_res + col));
       }
     };
     if constexpr (kMode == 1) load_residual(0, res_next);
@@ -794,7 +795,9 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
             }
             packed[e / 2] = pack_bf16x2(yy[0], yy[1]);
           }
-          *reinterpret_cast<u32x4*>(ep.out + row * ep.ldc + col) = packed;
+          // streaming store: the output is not read again here, and in L2 it would only evict
+          // the A / W panels the next tiles need
+          __builtin_nontemporal_store(packed, reinterpret_cast<u32x4*>(ep.out + row * ep.ldc + col));
           // nonfinite outputs: bf16 exponent all ones, tested on the packed words with a
           // running 16-bit max of the magnitudes (checked once at the end)
 #pragma unroll
