@@ -77,7 +77,8 @@ __device__ __forceinline__ void quantize_store8(const float* v, int lane16, int6
 #pragma unroll
   for (int i = 0; i < 8; ++i) scaled[i] = v[i] * inv;
   const u32x2 codes = e4m3x8(scaled);
-  *reinterpret_cast<u32x2*>(q + r * kp + chunk * 128 + lane16 * 8) = codes;
+  // 16 lanes write the chunk's 128 contiguous bytes: a streaming store of whole lines
+  __builtin_nontemporal_store(codes, reinterpret_cast<u32x2*>(q + r * kp + chunk * 128 + lane16 * 8));
   const uint32_t s1 = dpp_u32<0x104>(scale);  // lane + 4 of the 16-lane row
   const uint32_t s2 = dpp_u32<0x108>(scale);
   const uint32_t s3 = dpp_u32<0x10C>(scale);

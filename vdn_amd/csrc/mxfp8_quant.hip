@@ -175,7 +175,7 @@ __device__ __forceinline__ void prenorm_row_straight(const uint16_t* __restrict_
   u32x4 raw[kS];
 #pragma unroll
   for (int j = 0; j < kS; ++j)
-    raw[j] = *reinterpret_cast<const u32x4*>(xrow + (lane + 64 * j) * 8);
+    raw[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xrow + (lane + 64 * j) * 8));
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < kS; ++j) {
@@ -214,7 +214,7 @@ __device__ __forceinline__ void prenorm_row_straight(const uint16_t* __restrict_
       packed[i] = pack_bf16x2(t0 * u[2 * i] + sh[2 * i], t1 * u[2 * i + 1] + sh[2 * i + 1]);
       mag = __builtin_elementwise_max(mag, __builtin_bit_cast(u16x2, packed[i] & 0x7fff7fffu));
     }
-    if (y != nullptr) *reinterpret_cast<u32x4*>(y + r * kCols + c0) = packed;
+    if (y != nullptr) __builtin_nontemporal_store(packed, reinterpret_cast<u32x4*>(y + r * kCols + c0));
     float v[8];
     unpack_bf16x8(packed, v);
     quantize_store8(v, lane & 15, r, 4 * j + (lane >> 4), kp, q, s);

@@ -47,6 +47,17 @@ __device__ __forceinline__ void load8(const void* __restrict__ p, int f32, int64
   }
 }
 
+// Eight bf16 values of a q / k row, read once: a streaming load (the weights and the
+// cos / sin rows, reused across heads, go through load8 and stay cached).
+__device__ __forceinline__ void load8_row(const uint16_t* __restrict__ p, float* out) {
+  const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffff));
+    out[2 * i + 1] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
+  }
+}
+
 // kVec: unit channel strides, 16-byte aligned rows, weights and table rows, rot % 8 == 0;
 // every load is one (or two, fp32) 16-byte access per lane.
 template <int kD, bool kVec>
@@ -70,7 +81,7 @@ qk_rope_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float eps,
   const uint16_t* src = a.x + t * a.st + h * a.sh + static_cast<int64_t>(sub) * 8 * a.sd;
   if (kVec) {
     if (live) {
-      load8(src, 0, 0, false, v);
+      load8_row(src, v);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = 0.f;
@@ -171,7 +182,7 @@ qk_rope_row128_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float e
     const int64_t t = row / heads;
     const int h = static_cast<int>(row - t * heads);
     float v[8];
-    load8(a.x + t * a.st + h * a.sh, 0, sub * 8, false, v);
+    load8_row(a.x + t * a.st + h * a.sh + sub * 8, v);
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
@@ -198,7 +209,7 @@ qk_rope_row128_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float e
     u32x4 packed;
 #pragma unroll
     for (int i = 0; i < 4; ++i) packed[i] = pack_bf16x2(o[2 * i], o[2 * i + 1]);
-    *reinterpret_cast<u32x4*>(a.out + row * kD + sub * 8) = packed;
+    __builtin_nontemporal_store(packed, reinterpret_cast<u32x4*>(a.out + row * kD + sub * 8));
   }
 }
 
