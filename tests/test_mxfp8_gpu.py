@@ -359,3 +359,35 @@ def test_gemm_reports_nonfinite_result(device):
     p.weight_data.fill_(127)  # E4M3 NaN code, a corrupted compressed weight
     with pytest.raises(ValueError, match="nonfinite MXFP8 result"):
         p(x)
+
+
+@pytest.mark.parametrize("m,f,k", [(1100, 640, 512), (2048, 704, 256), (300, 384, 256),
+                                   (1024, 520, 128)])
+def test_gemm_swiglu_producer_matches_separate_passes(device, m, f, k):
+    """The fused SwiGLU producer (the up projection's a and g halves interleaved in 128-row
+    blocks, met in the GEMM epilogue) writes the same bytes as the plain [a | g] GEMM fed to
+    the stand-alone SwiGLU producer (tp_ff_forward's two steps). Shapes cover the persistent
+    kernel, the small-problem path, a SwiGLU width not a multiple of 128 and rows past a tile."""
+    g = torch.Generator().manual_seed(m + f)
+    x = (torch.randn(m, k, generator=g) * 2).to(torch.bfloat16).to(device)
+    w = (torch.randn(2 * f, k, generator=g) * 0.05).to(torch.bfloat16).to(device)
+    bias = torch.randn(2 * f, generator=g).to(torch.bfloat16).to(device)
+    q, s = vm.quantize_activation(x)
+    plain = vm.MXFP8Linear(_as_linear(w, bias)).to(device)
+    fused = vm.MXFP8Linear.swiglu_up(_as_linear(w, bias)).to(device)
+    fq, fs = fused.forward_act_quantized(q, s, rows=m, act="swiglu")
+    y = plain.forward_quantized(q, s, rows=m)
+    rq, rs, _ = vm.launch_swiglu_quantize(y)
+    assert fq.shape == rq.shape and fs.shape == rs.shape
+    assert torch.equal(fq, rq)
+    assert torch.equal(fs, rs)
+    with pytest.raises(ValueError, match="swiglu_up"):
+        plain.forward_act_quantized(q, s, rows=m, act="swiglu")
+
+
+def _as_linear(w, bias):
+    lin = nn.Linear(w.shape[1], w.shape[0], dtype=torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(w.cpu())
+        lin.bias.copy_(bias.cpu())
+    return lin

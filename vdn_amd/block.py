@@ -149,7 +149,11 @@ class HybridDiTBlock(nn.Module):
         self.o_cat = mk(torch.cat((w.o_w, w.olin_w), dim=1), w.o_b)
         self.cq, self.ck, self.cv, self.co = (mk(w.cq_w, w.cq_b), mk(w.ck_w, w.ck_b),
                                               mk(w.cv_w, w.cv_b), mk(w.co_w, w.co_b))
-        self.up, self.down = mk(w.up_w, w.up_b), mk(w.down_w, w.down_b)
+        if cfg.ffn_act == "swiglu":   # [a | g] interleaved for the fused SwiGLU producer
+            self.up = mx.MXFP8Linear.swiglu_up(_linear(w.up_w, w.up_b), check_finite=False)
+        else:
+            self.up = mk(w.up_w, w.up_b)
+        self.down = mk(w.down_w, w.down_b)
         # small bf16 projections of the attention input, one GEMM: softmax gate | beta | gate down
         self.small_w = torch.cat((w.soft_gate_w, w.beta_w, w.lgate_down_w))
         self.keep = {k: w.tensors[k] for k in (
@@ -309,14 +313,9 @@ class HybridDiTBlock(nn.Module):
         # ---- FFN ----
         _, q4, s4, _ = mx.launch_prenorm_quantize(h, k["norm2"], cfg.eps, scale_mlp, shift_mlp,
                                                   idx, write_bf16=False)
-        if cfg.ffn_act == "swiglu":
-            # up -> bf16 [T, 2 ffn] = [a | g], then the SwiGLU producer (tp_ff_forward,
-            # tensor_parallel.py:147-161: project, launch_swiglu_quantize)
-            up = self.up.forward_quantized(q4, s4, rows=T)
-            q5, s5, _ = mx.launch_swiglu_quantize(up)
-            del up
-        else:
-            q5, s5 = self.up.forward_act_quantized(q4, s4, rows=T, act="gelu_tanh")
+        # up + activation + MXFP8 in the GEMM's epilogue (for SwiGLU the [a | g] halves meet
+        # in it: tp_ff_forward's project + launch_swiglu_quantize, tensor_parallel.py:147-161)
+        q5, s5 = self.up.forward_act_quantized(q4, s4, rows=T, act=cfg.ffn_act)
         snap("ffn_codes", (q5, s5))
         self.down.forward_quantized(q5, s5, rows=T, out=h, residual=h, gate=gate_mlp)
         return (h, parts) if return_parts else h

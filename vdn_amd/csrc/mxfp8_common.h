@@ -59,6 +59,19 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(z));
 }
 
+// SwiGLU's gate half g * sigmoid(g), and a * silu(g), in fp32 (mxfp8_kernels.py:62-64); the
+// stand-alone producer and the GEMM's producer epilogue share them, so both write the same
+// bytes. The sigmoid takes the hardware exp2 and reciprocal (a few fp32 ulp from
+// 1 / (1 + exp(-g)), far below the bf16 rounding of the product).
+#pragma clang fp contract(off)
+__device__ __forceinline__ float swiglu_gate(float g) {
+  constexpr float kMinusLog2e = -1.4426950408889634f;
+  const float sig = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(g * kMinusLog2e));
+  return g * sig;
+}
+__device__ __forceinline__ float silu_mul(float a, float g) { return a * swiglu_gate(g); }
+#pragma clang fp contract(on)
+
 // Quantizes the 8 values a lane holds (one quarter of a 32-block), stores the 8 codes
 // and, from lane 0 of each 16-lane group, the chunk's 4 scale bytes. A group is one DPP
 // row (lanes 16k .. 16k + 15) whose lanes are all active: the amax and the scale bytes move

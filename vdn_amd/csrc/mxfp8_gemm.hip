@@ -504,8 +504,9 @@ __device__ __forceinline__ void pin_column_from(const f32x4 (&acc)[8][8], int nt
 }
 
 // kMode: 0 bf16 output, 1 bf16 output with a residual (Epilogue::residual, prefetched one
-// row group ahead), 2 the MXFP8 producer epilogue (Epilogue::q_out). The bf16 modes need
-// 16-byte accesses (Epilogue::vec) and no addend.
+// row group ahead), 2 the MXFP8 producer epilogue (Epilogue::q_out, act 0 / 1), 3 the SwiGLU
+// producer epilogue (act 2, interleaved weight). The bf16 modes need 16-byte accesses
+// (Epilogue::vec) and no addend.
 template <int kHead, int kMode>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
@@ -514,7 +515,10 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
                              int64_t n, int tiles_m, int tiles_n, int group_m) {
   constexpr int TM = 8, TN = 8;
   static_assert(kHead >= 1 && kHead < TM, "head groups");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kPStep + (kMode == 2 ? 0 : 4 * kPStageBytes)];
+  // after the two step buffers: the bf16 modes' staging strips, or the producer's SwiGLU
+  // hand-over slots (2 wave pairs x 64 lanes x 32 fp32)
+  __shared__ __attribute__((aligned(1024))) uint8_t
+      lds[2 * kPStep + (kMode == 3 ? 2 * 64 * 32 * 4 : kMode == 2 ? 0 : 4 * kPStageBytes)];
 
   const int num_wg = tiles_m * tiles_n;
   const int grid = gridDim.x;
@@ -619,9 +623,20 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
   // leave as one 4-byte store, with no LDS staging. A 32-column block is nt = 2b, 2b + 1 of
   // the four lanes g of a row (two permlane swaps give its amax), and the wave's 128 columns
   // are one MXFP8 chunk, whose 4 scale bytes are one dword of the swizzled layout.
+  // SwiGLU (ep.act 2) reads W with its a and g halves interleaved in 128-row blocks: block j
+  // of a is W rows [256 j, 256 j + 128), block j of g the next 128. A 256-column tile then
+  // holds a-block j in wave column wn = 0 and g-block j in wn = 1, for the same rows: the g
+  // wave passes g * sigmoid(g) of its values through an 8 KB LDS slot per wave pair (lane
+  // l's 32 values at its own offset, the a wave's lane l reads them), and the a wave forms
+  // bf16(a * that), quantizes and stores output chunk j. Bias is interleaved the same way.
+  constexpr bool swiglu = kMode == 3;
+  float* pass_slot = reinterpret_cast<float*>(lds + 2 * kPStep) + (wm * 64 + lane) * 32;
   auto epilogue_direct = [&](int64_t m0, int64_t n0) __attribute__((always_inline)) {
-    const int64_t col0 = n0 + wn * 128 + c_lo * 4;       // + 16 nt
+    const int64_t col0 = n0 + wn * 128 + c_lo * 4;       // + 16 nt (physical columns)
     const int64_t rows0 = m0 + wm * 128 + frag_row;      // + 16 mt
+    // the output columns of the lane: physical for GELU / none, block j of a for SwiGLU
+    const int64_t ocol0 = swiglu ? (n0 >> 1) + c_lo * 4 : col0;
+    const int64_t n_phys = swiglu ? 2 * ep.kp_out : n;
     // bias of the lane's 32 columns; a missing bias is -0: bf16(y + -0) = y exactly
     float bias4[TN][4];
 #pragma unroll
@@ -630,15 +645,15 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
 #pragma unroll
       for (int v = 0; v < 4; ++v) bias4[nt][v] = -0.f;
       if (ep.bias == nullptr) continue;
-      if (ep.vec && col < n) {   // n % 8 == 0: the lane's 4 columns are all inside
+      if ((ep.vec || swiglu) && col < n_phys) {   // the lane's 4 columns are all inside
         unpack4(*reinterpret_cast<const u32x2*>(ep.bias + col), bias4[nt]);
-      } else if (!ep.vec) {
+      } else if (!ep.vec && !swiglu) {
 #pragma unroll
         for (int v = 0; v < 4; ++v)
           if (col + v < n) bias4[nt][v] = bf16_bits_to_f32(ep.bias[col + v]);
       }
     }
-    const int64_t chunk128 = (n0 + wn * 128) >> 7;
+    const int64_t chunk128 = swiglu ? n0 >> 8 : (n0 + wn * 128) >> 7;
     const bool chunk_in = chunk128 < (ep.kp_out >> 7);
     // A rolled loop over the 8 row groups keeps one copy of the code; the accumulators
     // (registers) are picked by a uniform branch chain, not indexed.
@@ -662,17 +677,46 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
         }
       }
       const int64_t row = rows0 + mt * 16;
-      // bias, activation and bf16 rounding; rows >= out_rows and columns >= n are zero
+      if constexpr (swiglu) {
+        // bf16(acc + bias) of both halves; the g wave hands over g * sigmoid(g)
+        if (wn == 1) {
 #pragma unroll
-      for (int nt = 0; nt < TN; ++nt)
+          for (int nt = 0; nt < TN; ++nt) {
+            f32x4 gs;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          float val = round_bf16(y[nt][v] + bias4[nt][v]);
-          if (ep.act == 1) val = round_bf16(gelu_tanh(val));
-          if (ep.nonfinite != nullptr) bad = bad || !(fabsf(val) < INFINITY);
-          const bool in = row < out_rows && col0 + nt * 16 + v < n;
-          y[nt][v] = in ? val : 0.f;
+            for (int v = 0; v < 4; ++v) gs[v] = swiglu_gate(round_bf16(y[nt][v] + bias4[nt][v]));
+            *reinterpret_cast<f32x4*>(pass_slot + nt * 4) = gs;
+          }
         }
+        __syncthreads();
+        if (wn == 0) {
+#pragma unroll
+          for (int nt = 0; nt < TN; ++nt) {
+            const f32x4 gs = *reinterpret_cast<const f32x4*>(pass_slot + nt * 4);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const float val = round_bf16(round_bf16(y[nt][v] + bias4[nt][v]) * gs[v]);
+              if (ep.nonfinite != nullptr) bad = bad || !(fabsf(val) < INFINITY);
+              const bool in = row < out_rows && ocol0 + nt * 16 + v < n;
+              y[nt][v] = in ? val : 0.f;
+            }
+          }
+        }
+        __syncthreads();   // the slot is free for the next row group
+        if (wn == 1) continue;   // the a wave quantizes and stores the chunk
+      } else {
+        // bias, activation and bf16 rounding; rows >= out_rows and columns >= n are zero
+#pragma unroll
+        for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            float val = round_bf16(y[nt][v] + bias4[nt][v]);
+            if (ep.act == 1) val = round_bf16(gelu_tanh(val));
+            if (ep.nonfinite != nullptr) bad = bad || !(fabsf(val) < INFINITY);
+            const bool in = row < out_rows && col0 + nt * 16 + v < n;
+            y[nt][v] = in ? val : 0.f;
+          }
+      }
       // every lane takes part in the block maxima; only the stores are predicated
       const bool store = chunk_in && row < mp;
       uint8_t* qrow = ep.q_out + row * ep.kp_out + chunk128 * 128 + c_lo * 4;
@@ -895,7 +939,7 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
     int tm, tn;
     tile_coords(static_cast<int>(blockIdx.x) + c_tile * grid, num_wg, tiles_m, tiles_n, group_m,
                 tm, tn);
-    if constexpr (kMode == 2)
+    if constexpr (kMode >= 2)
       epilogue_direct(static_cast<int64_t>(tm) * kPTile, static_cast<int64_t>(tn) * kPTile);
     else
       epilogue_staged(static_cast<int64_t>(tm) * kPTile, static_cast<int64_t>(tn) * kPTile);
@@ -939,7 +983,10 @@ int launch_persistent(const uint8_t* a, const uint8_t* as, int64_t mp, const uin
   const int64_t tiles = tiles_m * tiles_n;
   const int grid = static_cast<int>(tiles < cu_count() ? tiles : cu_count());
   const int tm = static_cast<int>(tiles_m), tn = static_cast<int>(tiles_n);
-  if (ep.q_out != nullptr)
+  if (ep.q_out != nullptr && ep.act == 2)
+    hipLaunchKernelGGL((mxfp8_gemm_persistent_kernel<VDN_GEMM_HEAD, 3>), dim3(grid), dim3(256),
+                       0, stream, a, as, w, ws, mp, np, kp, ep, out_rows, n, tm, tn, kPGroupM);
+  else if (ep.q_out != nullptr)
     hipLaunchKernelGGL((mxfp8_gemm_persistent_kernel<VDN_GEMM_HEAD, 2>), dim3(grid), dim3(256),
                        0, stream, a, as, w, ws, mp, np, kp, ep, out_rows, n, tm, tn, kPGroupM);
   else if (ep.residual != nullptr)
@@ -1020,9 +1067,10 @@ VDN_API int vdn_mxfp8_gemm(const void* a, const void* a_scales, int64_t mp, cons
   return launch_gemm<128, 128, 2, 2>(ap, asp, mp, wp, wsp, np, kp, ep, out_rows, n, st);
 }
 
-// Fused FFN producer: the GEMM of vdn_mxfp8_gemm (+ bias), then act (0 none, 1 GELU-tanh)
-// rounded to bf16 and quantized to MXFP8 in the epilogue, in place of the bf16 output and
-// a separate producer pass. Output: codes q [mp, pad128(n)] and swizzled scales s
+// Fused FFN producer: the GEMM of vdn_mxfp8_gemm (+ bias), then act (0 none, 1 GELU-tanh,
+// 2 SwiGLU a * silu(g) over a weight with a and g interleaved in 128-row blocks) rounded to
+// bf16 and quantized to MXFP8 in the epilogue, in place of the bf16 output and a separate
+// producer pass. Output: codes q [mp, pad128(n)] and swizzled scales s
 // (mp * pad128(n) / 32 bytes); rows >= out_rows and columns >= n are zero. nonfinite
 // (nullable) receives 1 when an activated value is not finite.
 // Reference: MXFP8Linear.forward_quantized (src/models/ops/mxfp8_linear.py:61-93) followed
@@ -1041,7 +1089,8 @@ VDN_API int vdn_mxfp8_gemm_act_quantize(const void* a, const void* a_scales, int
     return set_error(kInvalidArgument, "%s: padded M/N/K must be positive multiples of 128", name);
   if (n <= 0 || n > np || out_rows < 0 || out_rows > mp)
     return set_error(kInvalidArgument, "%s: invalid output geometry", name);
-  if (act != 0 && act != 1) return set_error(kInvalidArgument, "%s: unknown activation %d", name, act);
+  if (act != 0 && act != 1 && act != 2)
+    return set_error(kInvalidArgument, "%s: unknown activation %d", name, act);
   if (!aligned(a, 16) || !aligned(w, 16) || !aligned(a_scales, 4) || !aligned(w_scales, 4) ||
       !aligned(q, 16) || !aligned(scales, 4) || (bias != nullptr && !aligned(bias, 16)))
     return set_error(kInvalidArgument, "%s: misaligned buffer", name);
@@ -1049,6 +1098,12 @@ VDN_API int vdn_mxfp8_gemm_act_quantize(const void* a, const void* a_scales, int
   const int64_t kp_out = (n + 127) / 128 * 128;
   // Every column chunk up to kp_out must be produced: the padded GEMM width covers it.
   if (kp_out > np) return set_error(kInvalidArgument, "%s: padded N smaller than pad128(n)", name);
+  // SwiGLU: W holds a and g interleaved in 128-row blocks (np = 2 pad128(n)); the hand-over
+  // between the a and g waves exists in the persistent kernel only.
+  if (act == 2 && (np != 2 * kp_out || mp < 1024 || np < 1024))
+    return set_error(kUnsupported,
+                     "%s: SwiGLU takes the interleaved [a | g] weight (padded N = 2 pad128(n)) "
+                     "and M >= 1024, N >= 512", name);
   const Epilogue ep{static_cast<const uint16_t*>(bias), nullptr, 0, nullptr, 0, nullptr, nullptr,
                     0, nonfinite, n % 8 == 0 ? 1 : 0, static_cast<uint8_t*>(q),
                     static_cast<uint8_t*>(scales), kp_out, act};

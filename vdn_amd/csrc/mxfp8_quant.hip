@@ -61,12 +61,6 @@ __device__ __forceinline__ void load_row8(const uint16_t* __restrict__ x, int64_
   }
 }
 
-#pragma clang fp contract(off)
-__device__ __forceinline__ float silu_mul(float a, float g) {
-  const float sig = 1.f / (1.f + expf(-g));
-  return a * (g * sig);
-}
-#pragma clang fp contract(on)
 
 template <int kAct, bool kVec>
 __global__ void __launch_bounds__(kThreads)

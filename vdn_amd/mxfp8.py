@@ -318,18 +318,78 @@ def mxfp8_gemm(data, scales, weight_data, weight_scale, n, *, rows=None, bias=No
     return out
 
 
+def interleave_swiglu(weight: torch.Tensor, bias: torch.Tensor | None = None):
+    """[a | g] rows of a SwiGLU up projection ([2F, K], bias [2F]) -> the layout of the fused
+    SwiGLU producer: each half padded to pad128(F) rows with zeros, then 128-row blocks
+    interleaved a0, g0, a1, g1, ... ([2 pad128(F), K]); the bias likewise."""
+    if weight.shape[0] % 2:
+        raise ValueError("a SwiGLU up projection has an even number of rows")
+    f = weight.shape[0] // 2
+    fp = -(-f // 128) * 128
+
+    def arrange(t):
+        a, g = t[:f], t[f:]
+        pad = (0, 0) * (t.ndim - 1) + (0, fp - f)
+        a, g = torch.nn.functional.pad(a, pad), torch.nn.functional.pad(g, pad)
+        rest = t.shape[1:]
+        return torch.stack((a.reshape(fp // 128, 128, *rest), g.reshape(fp // 128, 128, *rest)),
+                           dim=1).reshape(2 * fp, *rest)
+    return arrange(weight), None if bias is None else arrange(bias)
+
+
+def _gemm_swiglu_quantize(data, scales, weight_data, weight_scale, n, rows, bias, check_finite):
+    mp, kp = data.shape
+    np_ = weight_data.shape[0]
+    kp_out = -(-n // 128) * 128
+    if np_ != 2 * kp_out:
+        raise ValueError("SwiGLU takes the interleave_swiglu weight (2 pad128(n) rows)")
+    rows = mp if rows is None else rows
+    if mp < 1024 or np_ < 1024:
+        # small problems: the GEMM's bf16 [a0 g0 a1 g1 ...] output, regrouped as [a | g], then
+        # the stand-alone SwiGLU producer (the fused hand-over is in the persistent kernel)
+        y = mxfp8_gemm(data, scales, weight_data, weight_scale, np_, rows=rows, bias=bias,
+                       check_finite=check_finite)
+        y = y.view(rows, kp_out // 128, 2, 128).transpose(1, 2).reshape(rows, 2, kp_out)
+        q, s, _ = launch_swiglu_quantize(y[:, :, :n].reshape(rows, 2 * n))
+        if q.shape[0] != mp:
+            q2 = torch.zeros((mp, kp_out), dtype=torch.uint8, device=data.device)
+            s2 = torch.zeros(mp * kp_out // 32, dtype=torch.uint8, device=data.device)
+            q2[:q.shape[0]] = q
+            s2[:s.numel()] = s
+            q, s = q2, s2
+        return q, s
+    q = torch.empty((mp, kp_out), dtype=torch.uint8, device=data.device)
+    s = torch.empty(mp * kp_out // 32, dtype=torch.uint8, device=data.device)
+    flag = torch.zeros(1, dtype=torch.int32, device=data.device) if check_finite else None
+    if rows:
+        _lib.call("vdn_mxfp8_gemm_act_quantize", data.data_ptr(), scales.data_ptr(), mp,
+                  weight_data.data_ptr(), weight_scale.data_ptr(), np_, kp, _lib.ptr(bias), 2,
+                  q.data_ptr(), s.data_ptr(), rows, n, _lib.ptr(flag), _lib.stream(data.device))
+    else:
+        q.zero_()
+        s.zero_()
+    if check_finite and int(flag.item()) != 0:
+        raise ValueError("nonfinite MXFP8 activation")
+    return q, s
+
+
 def mxfp8_gemm_act_quantize(data, scales, weight_data, weight_scale, n, *, rows=None, bias=None,
                             act="gelu_tanh", check_finite=False):
     """MXFP8 codes/scales of act(bf16(dequant(data) @ dequant(weight)ᵀ + bias)) for the next
     projection, produced in the GEMM epilogue. Bit-identical to mxfp8_gemm followed by
-    launch_gelu_quantize (act "gelu_tanh") or launch_quantize (act None).
+    launch_gelu_quantize (act "gelu_tanh"), launch_quantize (act None) or, for act "swiglu"
+    over a weight from interleave_swiglu (n = the SwiGLU width), launch_swiglu_quantize of
+    the [a | g] output.
     Returns (codes u8 [RP, pad128(n)], flat swizzled scales u8)."""
     mp, kp = data.shape
     np_, kpw = weight_data.shape
     if kp != kpw:
         raise ValueError("activation and weight padded K differ")
-    if act not in ("gelu_tanh", None):
-        raise ValueError("act must be 'gelu_tanh' or None")
+    if act not in ("gelu_tanh", "swiglu", None):
+        raise ValueError("act must be 'gelu_tanh', 'swiglu' or None")
+    if act == "swiglu":
+        return _gemm_swiglu_quantize(data, scales, weight_data, weight_scale, n, rows, bias,
+                                     check_finite)
     rows = mp if rows is None else rows
     kp_out = -(-n // 128) * 128
     q = torch.empty((mp, kp_out), dtype=torch.uint8, device=data.device)
@@ -410,10 +470,31 @@ class MXFP8Linear(nn.Module):
                           rows=rows, bias=bias, out=out, accumulate=accumulate, addend=addend,
                           residual=residual, gate=gate, check_finite=self.check_finite)
 
+    @classmethod
+    def swiglu_up(cls, linear: nn.Linear, *, chunk_rows=128, check_finite=True):
+        """The up projection of a SwiGLU FFN (rows [a | g], mxfp8_kernels.py:62-64) stored in
+        the fused SwiGLU producer's layout (interleave_swiglu). forward_act_quantized(
+        act="swiglu") then returns the MXFP8 activation a * silu(g), of width
+        linear.out_features // 2; forward_quantized returns the GEMM in that layout."""
+        if type(linear) is not nn.Linear:
+            raise TypeError("MXFP8 requires an ordinary merged nn.Linear")
+        w, b = interleave_swiglu(linear.weight.detach(),
+                                 None if linear.bias is None else linear.bias.detach())
+        inter = nn.Linear(w.shape[1], w.shape[0], bias=b is not None, dtype=w.dtype,
+                          device=w.device)
+        with torch.no_grad():
+            inter.weight.copy_(w)
+            if b is not None:
+                inter.bias.copy_(b)
+        module = cls(inter, chunk_rows=chunk_rows, check_finite=check_finite)
+        module.swiglu_width = linear.out_features // 2
+        return module
+
     @torch.no_grad()
     def forward_act_quantized(self, data, scales, *, rows=None, act="gelu_tanh"):
         """Consume MXFP8 input and return the MXFP8 codes/scales of act(bf16 output): the
-        producer of the next projection fused into this GEMM's epilogue."""
+        producer of the next projection fused into this GEMM's epilogue. act "swiglu" needs a
+        module built by swiglu_up."""
         if data.device.type != "cuda":
             raise RuntimeError("native MXFP8 requires a HIP device; no fallback")
         np_, kp = padded_shape(self.out_features, self.in_features)
@@ -424,8 +505,13 @@ class MXFP8Linear(nn.Module):
         bias = None
         if self.bias is not None:
             bias = self.bias.to(device=data.device, dtype=torch.bfloat16).contiguous()
+        n = self.out_features
+        if act == "swiglu":
+            n = getattr(self, "swiglu_width", None)
+            if n is None:
+                raise ValueError("act 'swiglu' needs the interleaved weight of swiglu_up")
         return mxfp8_gemm_act_quantize(data, scales, self.weight_data, self.weight_scale,
-                                       self.out_features, rows=rows, bias=bias, act=act,
+                                       n, rows=rows, bias=bias, act=act,
                                        check_finite=self.check_finite)
 
     @torch.no_grad()
