@@ -46,3 +46,26 @@ def test_invalid_arguments_are_rejected_without_a_device():
     assert lib.vdn_mxfp8_gemm(None, None, 128, None, None, 128, 128, None, None, 0, None, 0,
                               None, None, 1, 1, 1, None, None) != 0
     assert b"null pointer" in lib.vdn_last_error()
+
+
+def test_short_conv_and_swiglu_entry_points_validate_before_launching():
+    """The fused short-conv prepare and the SwiGLU producer reject bad arguments before any
+    HIP call (fake, never dereferenced, 256-aligned addresses)."""
+    lib = _lib.load()
+    fake = 1 << 20
+    assert lib.vdn_vda_conv_prepare(None, 2, 256, 128, 3, 4, 5, fake, fake, 1, fake, None) != 0
+    assert b"null pointer" in lib.vdn_last_error()
+    assert lib.vdn_vda_conv_prepare(fake, 2, 256, 128, 3, 0, 5, fake, fake, 1, fake, None) != 0
+    assert b"positive" in lib.vdn_last_error()
+    assert lib.vdn_vda_conv_prepare(fake, 2, 250, 128, 3, 4, 5, fake, fake, 1, fake, None) != 0
+    assert b"16-byte" in lib.vdn_last_error()
+    # heads that do not fit inside a row
+    assert lib.vdn_vda_conv_prepare(fake, 3, 256, 128, 3, 4, 5, fake, fake, 1, fake, None) != 0
+    assert b"inside a row" in lib.vdn_last_error()
+    # SwiGLU needs the interleaved weight: padded N = 2 pad128(n)
+    assert lib.vdn_mxfp8_gemm_act_quantize(fake, fake, 2048, fake, fake, 1280, 256, None, 2, fake,
+                                           fake, 2048, 700, None, None) != 0
+    assert b"interleaved" in lib.vdn_last_error()
+    assert lib.vdn_mxfp8_gemm_act_quantize(fake, fake, 2048, fake, fake, 1280, 256, None, 3, fake,
+                                           fake, 2048, 640, None, None) != 0
+    assert b"unknown activation" in lib.vdn_last_error()
