@@ -119,6 +119,10 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
   // ---- Q fragments: query q0 + 32 wave + col, channels 16 ks + 8 g .. +8 ----
   const int my_q = q0 + wave * 32 + col;
   const bool q_live = my_q < q1;
+  // A group's last block can hold a few rows only (3600 rows per frame = 14 blocks of 256 + 16):
+  // waves without a live query still load their share of every tile and meet every barrier,
+  // but skip the arithmetic, so the live waves of their SIMDs run at the full MFMA rate.
+  const bool wave_live = q0 + wave * 32 < q1;
   bf16x8 qf[8];
   {
     const uint16_t* src = in.q + static_cast<int64_t>(q_live ? my_q : q0) * in.q_st + h * in.q_sh;
@@ -198,6 +202,7 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
       issue_tile(na, min(na + kBN, b0), kBuf == 0 ? sK1 : sK0, kBuf == 0 ? sV1 : sV0);
     }
     const int a = a0 + t * kBN, b = min(a + kBN, b0);
+    if (!wave_live) return;
 
     // ---- Sᵀ = K Qᵀ for the tile's 64 keys (two 32-key accumulators) ----
     f32x16 s[kKT];
