@@ -40,6 +40,25 @@ def test_dense_fp32_oracle(device, before, after, frames, chunk, radius, anchor)
     assert out.is_contiguous() and out.data_ptr() != backing.data_ptr()
 
 
+@pytest.mark.parametrize("spatial", [300, 470])
+@torch.no_grad()
+def test_partial_last_query_block(device, spatial):
+    """Frames of 300 and 470 tokens end in a 44- and a 214-row query block: some waves of that
+    block hold queries, the rest hold none and only stage tiles. Dense fp32 oracle."""
+    torch.manual_seed(31)
+    frames = 3
+    layout = vw.SequenceLayout(frames * spatial, 0, frames, spatial)
+    bounds = vw.window_bounds(frames, 1)
+    q, k, v = [torch.randn(layout.seq_len, 2, 128, device=device, dtype=torch.bfloat16)
+               for _ in range(3)]
+    plan = vw.prepare_paper_window_plan(layout, bounds, device=device)
+    out, lse = vw.paper_window_attention(q, k, v, plan, enabled=True, return_lse=True)
+    mask = ow.dense_mask(layout.seq_len, 0, frames, spatial, bounds, "none")
+    expected, el = ow.attention_dense(q.cpu(), k.cpu(), v.cpu(), mask, 128 ** -.5)
+    torch.testing.assert_close(out.float().cpu(), expected, atol=.009, rtol=.015)
+    torch.testing.assert_close(lse.cpu(), el, atol=3e-5, rtol=3e-6)
+
+
 @torch.no_grad()
 def test_constant_values_anchor_union_mass(device):
     layout = vw.SequenceLayout(45, 2, 13, 3)
