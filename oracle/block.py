@@ -130,15 +130,42 @@ class BlockOracle:
                         scale.float().numpy(), shift.float().numpy(), np.zeros(t, np.int64))
         return torch.from_numpy(y).double()
 
-    def small_projections(self, x1):
+    def small_projections(self, x1, heads=None):
         """softmax gate sigmoid(x Wg^T + b) [T, H]; beta sigmoid(x Wb^T) [T, H]; output gate
-        sigmoid(up(down x)) [T, H*D] (attention_gates.py:52-55), bf16 at each torch op."""
-        w, heads = self.w, self.cfg.heads
-        small = bf16(x1 @ torch.cat((w["soft_gate_w"], w["beta_w"], w["lgate_down_w"])).double().T)
-        soft_gate = bf16(torch.sigmoid(bf16(small[:, :heads] + w["soft_gate_b"].double())))
-        beta = bf16(torch.sigmoid(small[:, heads:2 * heads]))
-        up = bf16(small[:, 2 * heads:] @ w["lgate_up_w"].double().T + w["lgate_up_b"].double())
+        sigmoid(up(down x)) [T, H*D] (attention_gates.py:52-55), bf16 at each torch op.
+        `heads` (a list) restricts the three outputs to those heads' columns, in that order;
+        each column is computed exactly as in the full projection."""
+        w, nh, d = self.w, self.cfg.heads, self.cfg.head_dim
+        hs = list(range(nh)) if heads is None else list(heads)
+        cols = torch.tensor([i * d + c for i in hs for c in range(d)], dtype=torch.long)
+        gw, gb = w["soft_gate_w"][hs], w["soft_gate_b"][hs]
+        small = bf16(x1 @ torch.cat((gw, w["beta_w"][hs], w["lgate_down_w"])).double().T)
+        n = len(hs)
+        soft_gate = bf16(torch.sigmoid(bf16(small[:, :n] + gb.double())))
+        beta = bf16(torch.sigmoid(small[:, n:2 * n]))
+        up = bf16(small[:, 2 * n:] @ w["lgate_up_w"][cols].double().T
+                  + w["lgate_up_b"][cols].double())
         return soft_gate, beta, bf16(torch.sigmoid(up))
+
+    def out_projection(self, soft, far, h, gate, order="fused"):
+        """The attention stage's residual update h + gate * (to_out(soft) + to_out_linear(far)).
+
+        order "fused": one projection of [soft | far] with [W_O | W_Olin], one accumulation:
+            bf16(h + bf16(gate * bf16(bf16(acc_O + acc_Olin) + b_O)))   (the product's GEMM)
+        order "reference": the reference's two projections, each rounded, then added in bf16
+            (hybrid_attention.py:252-254; to_out_linear has no bias, :100-101), then the
+            gated residual of _post_ref (fused_block.py:49-51) in bf16:
+            o = bf16(bf16(acc_O) + b_O); o = bf16(o + bf16(acc_Olin));
+            bf16(h + bf16(gate * o))"""
+        if order == "fused":
+            return self.o_cat(torch.cat((soft, far), dim=1), residual=h, gate=gate)
+        if order != "reference":
+            raise ValueError("order must be 'fused' or 'reference'")
+        if not hasattr(self, "_o_pair"):
+            self._o_pair = (QuantizedLinear(self.w["o_w"], self.w["o_b"]),
+                            QuantizedLinear(self.w["olin_w"]))
+        o, olin = self._o_pair
+        return olin(far, addend=o(soft), residual=h, gate=gate)
 
     def alpha(self, x1, frames, spatial):
         w, cfg = self.w, self.cfg
@@ -180,8 +207,7 @@ class BlockOracle:
                                    bounds, frames, spatial, w["vda_norm"].double(), cfg.eps,
                                    chunk_size=cfg.vda_chunk)
         far = bf16(far)
-        both = torch.cat((use("soft", soft), use("far", far)), dim=1)
-        out = self.o_cat(both, residual=h, gate=gate)
+        out = self.out_projection(use("soft", soft), use("far", far), h, gate)
         return out, dict(x1=x1, qkv=qkv, soft=soft, far=far, alpha=alpha)
 
     def cross_stage(self, h, context, given=None):

@@ -331,6 +331,20 @@ def test_gemm_epilogue_argument_errors(device):
     with pytest.raises(ValueError, match="residual must be"):
         vm.mxfp8_gemm(q, s, wq, ws, 8, rows=4, residual=torch.ones(4, 7, dtype=torch.bfloat16,
                                                                     device=device))
+    with pytest.raises(ValueError, match="bias must be bf16"):
+        vm.mxfp8_gemm(q, s, wq, ws, 8, rows=4, bias=torch.ones(8, device=device))
+    with pytest.raises(ValueError, match="bias must be bf16"):
+        vm.mxfp8_gemm(q, s, wq, ws, 8, rows=4, bias=torch.ones(7, dtype=torch.bfloat16,
+                                                               device=device))
+    with pytest.raises(ValueError, match="scales must hold"):
+        vm.mxfp8_gemm(q, s[:-4], wq, ws, 8, rows=4)
+    with pytest.raises(ValueError, match="codes must be contiguous uint8"):
+        vm.mxfp8_gemm(q.view(torch.int8), s, wq, ws, 8, rows=4)
+    store = torch.zeros(5, 8, dtype=torch.bfloat16, device=device)
+    with pytest.raises(ValueError, match="overlaps residual"):
+        vm.mxfp8_gemm(q, s, wq, ws, 8, rows=4, out=store[1:], residual=store[:4])
+    # the same view is allowed: in place over the residual
+    vm.mxfp8_gemm(q, s, wq, ws, 8, rows=4, out=store[:4], residual=store[:4])
 
 
 def test_linear_api_paths_agree(device):

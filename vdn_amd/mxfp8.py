@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 from torch import nn
 
@@ -268,13 +269,57 @@ def launch_prenorm_quantize(x, weight, eps, scale, shift, indices, *, write_bf16
 # block-scaled GEMM (mxfp8_linear.py:36-142)
 # --------------------------------------------------------------------------------------
 
-def _matrix_arg(t, rows, n, name):
+def _matrix_arg(t, rows, n, name, device):
     if t is None:
         return None, 0
     if (t.dtype != torch.bfloat16 or t.ndim != 2 or t.shape[0] < rows or t.shape[1] != n
             or (t.shape[1] > 1 and t.stride(-1) != 1)):
         raise ValueError(f"{name} must be bf16 [rows, N] with contiguous N")
+    if t.device != device:
+        raise ValueError(f"{name} must be on the activation's device")
+    if rows > 1 and t.stride(0) < n:
+        raise ValueError(f"{name} rows overlap (row stride below N)")
     return t.data_ptr(), (t.stride(0) if rows > 1 else n)
+
+
+def _row_starts(t, rows, n):
+    """Element addresses (bf16 units) of the first element of each of `rows` rows."""
+    stride = t.stride(0) if rows > 1 else n
+    return t.data_ptr() // 2 + stride * np.arange(rows, dtype=np.int64)
+
+
+def _check_alias(out, other, rows, n, name):
+    """`out` may be exactly `other` (same address and row stride: each element is read and
+    written by one lane) or share no element with it (for example the interleaved column
+    halves of one buffer); a partial overlap would read values the kernel has already
+    overwritten."""
+    if other is None or rows == 0:
+        return
+    if out.data_ptr() == other.data_ptr() and (rows == 1 or out.stride(0) == other.stride(0)):
+        return
+    a, b = _row_starts(out, rows, n), _row_starts(other, rows, n)
+    if a[-1] + n <= b[0] or b[-1] + n <= a[0]:
+        return
+    # rows of each view are disjoint and ascending: a row of `out` meets a row of `other`
+    # when the first `other` row starting after a - n starts before a + n
+    first = np.searchsorted(b, a - n + 1)
+    hit = first < rows
+    if np.any(b[np.minimum(first, rows - 1)][hit] < a[hit] + n):
+        raise ValueError(f"out overlaps {name} without being the same view")
+
+
+def _check_operand(t, rows, kp, what):
+    if t.dtype != torch.uint8 or t.ndim != 2 or not t.is_contiguous():
+        raise ValueError(f"{what} codes must be contiguous uint8 [rows, KP]")
+    if t.shape[0] % 128 or t.shape[1] % 128 or t.shape[1] != kp or t.shape[0] < rows:
+        raise ValueError(f"{what} codes must be padded to 128 rows and K")
+
+
+def _check_scales(s, rows, kp, device, what):
+    if s.dtype != torch.uint8 or not s.is_contiguous() or s.device != device:
+        raise ValueError(f"{what} scales must be contiguous uint8 on the activation's device")
+    if s.numel() != rows * (kp // 32):
+        raise ValueError(f"{what} scales must hold RP * KP / 32 bytes")
 
 
 def mxfp8_gemm(data, scales, weight_data, weight_scale, n, *, rows=None, bias=None, out=None,
@@ -285,15 +330,36 @@ def mxfp8_gemm(data, scales, weight_data, weight_scale, n, *, rows=None, bias=No
     accumulate=True adds into `out` (addend = out), as `out += linear(x)`; `residual` /
     `gate` ([n]) fuse the block's gated residual `hidden + gate * branch`.
     """
+    if data.device.type != "cuda":
+        raise RuntimeError("native MXFP8 requires a HIP device; no fallback")
+    dev = data.device
+    if data.ndim != 2 or weight_data.ndim != 2:
+        raise ValueError("MXFP8 codes must be 2D [rows, KP]")
     mp, kp = data.shape
     np_, kpw = weight_data.shape
     if kp != kpw:
         raise ValueError("activation and weight padded K differ")
+    if weight_data.device != dev:
+        raise ValueError("weight codes must be on the activation's device")
+    _check_operand(data, 0, kp, "activation")
+    _check_operand(weight_data, n, kp, "weight")
+    _check_scales(scales, mp, kp, dev, "activation")
+    _check_scales(weight_scale, np_, kp, dev, "weight")
     rows = mp if rows is None else rows
+    if not 0 <= rows <= mp or not 0 < n <= np_:
+        raise ValueError("rows and N must lie within the padded operands")
     if out is None:
-        out = torch.empty((rows, n), dtype=torch.bfloat16, device=data.device)
+        out = torch.empty((rows, n), dtype=torch.bfloat16, device=dev)
     elif out.shape != (rows, n) or out.dtype != torch.bfloat16 or (n > 1 and out.stride(-1) != 1):
         raise ValueError("out must be bf16 [rows, N] with contiguous N")
+    elif out.device != dev:
+        raise ValueError("out must be on the activation's device")
+    elif rows > 1 and out.stride(0) < n:
+        raise ValueError("out rows overlap (row stride below N)")
+    if bias is not None:
+        if bias.dtype != torch.bfloat16 or bias.shape != (n,) or bias.device != dev:
+            raise ValueError("bias must be bf16 [N] on the activation's device")
+        bias = bias.contiguous()
     if accumulate:
         if addend is not None:
             raise ValueError("accumulate and addend are exclusive")
@@ -302,11 +368,13 @@ def mxfp8_gemm(data, scales, weight_data, weight_scale, n, *, rows=None, bias=No
         if residual is None:
             raise ValueError("a gate needs a residual")
         gate = gate.reshape(-1)
-        if gate.shape != (n,) or gate.dtype != torch.bfloat16:
-            raise ValueError("gate must be bf16 [N]")
+        if gate.shape != (n,) or gate.dtype != torch.bfloat16 or gate.device != dev:
+            raise ValueError("gate must be bf16 [N] on the activation's device")
         gate = gate.contiguous()
-    add_ptr, ld_add = _matrix_arg(addend, rows, n, "addend")
-    res_ptr, ld_res = _matrix_arg(residual, rows, n, "residual")
+    add_ptr, ld_add = _matrix_arg(addend, rows, n, "addend", dev)
+    res_ptr, ld_res = _matrix_arg(residual, rows, n, "residual", dev)
+    _check_alias(out, addend, rows, n, "addend")
+    _check_alias(out, residual, rows, n, "residual")
     flag = torch.zeros(1, dtype=torch.int32, device=data.device) if check_finite else None
     if rows:
         _lib.call("vdn_mxfp8_gemm", data.data_ptr(), scales.data_ptr(), mp,
