@@ -40,11 +40,15 @@ int vdn_mxfp8_quantize(const void* x, int64_t rows, int64_t k, int64_t row_strid
 /*
  * Activation + MXFP8 producer: act = 1 quantizes bf16(gelu_tanh(x[rows, k]));
  * act = 2 quantizes bf16(a * silu(g)) for x = [a | g] of width 2k.
+ * finite_tiles (nullable; uint8 [ceil(RP/16) * ceil(KP/256)], set to 1 by the caller): the
+ * byte of tile (r / 16, c / 256) is cleared when the tile's inputs or activations hold a
+ * nonfinite value, the reference's per-program FINITE output.
  * Replaces: src/models/ops/mxfp8_kernels.py:62-84, 113-124 (_swiglu_mx /
  * launch_swiglu_quantize); GELU-tanh is the same producer for a GELU-tanh FFN.
  */
 int vdn_mxfp8_act_quantize(const void* x, int64_t rows, int64_t k, int64_t row_stride, int act,
-                           void* q, void* scales, uint32_t* nonfinite, void* stream);
+                           void* q, void* scales, uint32_t* nonfinite, uint8_t* finite_tiles,
+                           void* stream);
 
 /*
  * Fused RMSNorm + AdaLN + MXFP8 producer:

@@ -168,6 +168,30 @@ def test_activation_quantize(device, act):
     assert (np.abs(dq - dr) <= amax * 2.0 ** -3 + 1e-6).all()
 
 
+@pytest.mark.parametrize("act", ["gelu", "swiglu"])
+def test_activation_finite_flags_per_tile(device, act):
+    """One finite flag per (16-row, 256-column) output tile, like the reference producer's
+    grid (mxfp8_kernels.py:113-124): R = 300 rows (RP 384 -> 24 row tiles), K = 1000 output
+    columns (KP 1024 -> 4 column tiles). A nonfinite input clears exactly its tile's flag;
+    for SwiGLU both the a and the g half count, and an overflowing a * silu(g) does too."""
+    rows, k = 300, 1000
+    width = 2 * k if act == "swiglu" else k
+    x = torch.ones(rows, width, dtype=torch.bfloat16)
+    bad = {(0, 0): float("nan"), (17, 300): float("inf"), (299, 999): -float("inf")}
+    if act == "swiglu":
+        bad.update({(40, k + 600): float("nan"), (100, 255): 3e38})   # g half; overflow
+        x[100, k + 255] = 3e38
+    for (r, c), v in bad.items():
+        x[r, c] = v
+    fn = vm.launch_swiglu_quantize if act == "swiglu" else vm.launch_gelu_quantize
+    _, _, finite = fn(x.to(device))
+    assert finite.shape == (24 * 4,) and finite.dtype == torch.bool
+    expect = torch.ones(24, 4, dtype=torch.bool)
+    for r, c in bad:
+        expect[r // 16, (c % k if act == "swiglu" else c) // 256] = False
+    assert torch.equal(finite.cpu().view(24, 4), expect)
+
+
 # ---------------------------------------------------------------------------- GEMM ----
 
 @pytest.mark.parametrize("mnk", KAT["gemm_shapes"]["mnk"])

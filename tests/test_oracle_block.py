@@ -67,18 +67,163 @@ def test_zero_gate_tables_make_the_gated_stages_identities(small):
         assert (live - hd).abs().max() > 1e-2, stage
 
 
-def test_table_order_shift_scale_gate(small):
-    """Tables are (shift, scale, gate) x (attention, mlp): the first prenorm uses tables 0/1."""
+def _silu(x):
+    return x / (1.0 + np.exp(-x))
+
+
+def _bf16(x):
+    """Nearest bf16 value(s); a scalar argument gives a Python float."""
+    r = omx.bf16_round(np.asarray(x, dtype=np.float64))
+    return float(r.reshape(-1)[0]) if np.ndim(x) == 0 else r
+
+
+def _tables_both(tensors, cfg, temb):
+    """AdaLN tables from the oracle and from the product's torch glue (CPU)."""
+    from vdn_amd.block import HybridDiTBlock
+    block = HybridDiTBlock(cfg, BlockWeights(tensors))
+    return ([t.double() for t in ob.BlockOracle(tensors, cfg).tables(temb)],
+            [t.double() for t in block.adaln_tables(temb)])
+
+
+def test_adaln_tables_closed_forms(small):
+    """AdaLN tables = Linear(bf16(SiLU(temb in fp32))) in the order shift, scale, gate
+    (attention), then shift, scale, gate (MLP) (paper_adaln.py:186, 205-212).
+    temb = 0 gives SiLU = 0, so every table is its bias; a weight row that is one-hot at
+    column j gives bf16(SiLU(temb_j)) at exactly that row's table and position."""
+    w, _ = small
+    hd = SMALL.hidden
+    temb = torch.linspace(-3, 3, hd)[None]
+    for tables in _tables_both(w.tensors, SMALL, torch.zeros(1, hd)):
+        bias = w.adaln_b.double()
+        for c in range(6):
+            assert torch.equal(tables[c][0], bias[c * hd:(c + 1) * hd]), c
+    tensors = dict(w.tensors)
+    tensors["adaln_w"] = torch.zeros_like(w.adaln_w)
+    tensors["adaln_b"] = torch.zeros_like(w.adaln_b)
+    picks = {0: (3, 17), 1: (100, 200), 2: (5, 255), 3: (254, 0), 4: (77, 77), 5: (0, 128)}
+    for c, (i, j) in picks.items():
+        tensors["adaln_w"][c * hd + i, j] = 1.0
+    for tables in _tables_both(tensors, SMALL, temb):
+        for c, (i, j) in picks.items():
+            expect = torch.zeros(hd, dtype=torch.float64)
+            expect[i] = _bf16(_bf16(_silu(float(temb[0, j]))))
+            assert torch.equal(tables[c][0], expect), c
+
+
+def _alpha_both(tensors, cfg, mean):
+    from vdn_amd.block import HybridDiTBlock
+    from oracle import vda as ov
+    block = HybridDiTBlock(cfg, BlockWeights(tensors))
+    return (ov.frame_kda_alpha(mean, tensors["alpha_down_w"], tensors["alpha_up_w"],
+                               tensors["dt_bias"], tensors["a_log"], cfg.heads, cfg.head_dim),
+            block.frame_alpha(mean))
+
+
+def test_frame_alpha_closed_forms(small):
+    """FrameKDAAlpha (layers.py:29-34, 36-69): alpha = exp(-exp(A_log) softplus(up(down(m)) +
+    dt_bias)). With zero down/up weights and the fla init dt_bias = dt + log(-expm1(-dt)),
+    softplus(dt_bias) = dt exactly, so alpha = exp(-A dt) per head and channel. With
+    A_log = 0, dt_bias = 0 and one-hot down/up rows routing frame-mean channel j to output
+    (h, c), alpha(h, c) = exp(-softplus(m_j)) = 1 / (1 + e^m_j) and every other channel
+    is exp(-softplus(0)) = 1/2."""
+    w, _ = small
+    nh, d, hd = SMALL.heads, SMALL.head_dim, SMALL.hidden
+    g = np.random.default_rng(7)
+    a = g.uniform(1, 16, nh)
+    dt = np.exp(g.uniform(np.log(1e-3), np.log(1e-1), nh * d))
+    tensors = dict(w.tensors)
+    tensors["alpha_down_w"] = torch.zeros_like(w.alpha_down_w)
+    tensors["alpha_up_w"] = torch.zeros_like(w.alpha_up_w)
+    tensors["a_log"] = torch.tensor(np.log(a), dtype=torch.float32)
+    tensors["dt_bias"] = torch.tensor(dt + np.log(-np.expm1(-dt)), dtype=torch.float32)
+    mean = torch.randn(3, hd)
+    expect = np.exp(-a[:, None] * dt.reshape(nh, d))[None].repeat(3, 0)
+    for alpha in _alpha_both(tensors, SMALL, mean):
+        assert alpha.shape == (3, nh, d) and alpha.dtype == torch.float32
+        np.testing.assert_allclose(alpha.numpy(), expect, rtol=3e-6)
+    tensors["a_log"] = torch.zeros(nh)
+    tensors["dt_bias"] = torch.zeros(nh * d)
+    routes = [(11, 4, 1, 127), (200, 9, 0, 0)]      # (mean channel j, latent r, head, channel)
+    for j, r, h, c in routes:
+        tensors["alpha_down_w"][r, j] = 1.0
+        tensors["alpha_up_w"][h * d + c, r] = 1.0
+    mean = torch.linspace(-4, 4, 3 * hd).reshape(3, hd)
+    expect = np.full((3, nh, d), 0.5)
+    for j, r, h, c in routes:
+        expect[:, h, c] = 1.0 / (1.0 + np.exp(mean[:, j].double().numpy()))
+    for alpha in _alpha_both(tensors, SMALL, mean):
+        np.testing.assert_allclose(alpha.numpy(), expect, rtol=2e-6)
+
+
+def test_gate_projections_closed_forms(small):
+    """The softmax gate sigmoid(x Wg^T + b) per head, beta sigmoid(x Wb^T) and the output
+    gate sigmoid(up(down x)) (attention_gates.py:52-55): zero weights give sigmoid(bias)
+    (OutputGate's constant init: bias logit(p) gives p), beta 1/2; one-hot rows give
+    sigmoid(x_j + b) at exactly the routed head / channel."""
+    w, _ = small
+    nh, d, hd = SMALL.heads, SMALL.head_dim, SMALL.hidden
+    tensors = dict(w.tensors)
+    for name in ("soft_gate_w", "beta_w", "lgate_down_w", "lgate_up_w"):
+        tensors[name] = torch.zeros_like(w.tensors[name])
+    logit = lambda p: float(np.log(p / (1 - p)))
+    tensors["soft_gate_b"] = torch.full((nh,), logit(0.99)).to(torch.bfloat16)
+    tensors["lgate_up_b"] = torch.full((nh * d,), logit(0.9)).to(torch.bfloat16)
+    x1 = torch.linspace(-2, 2, 5 * hd).reshape(5, hd).to(torch.bfloat16).double()
+    soft, beta, lin = ob.BlockOracle(tensors, SMALL).small_projections(x1)
+    sig = lambda v: 1.0 / (1.0 + np.exp(-v))
+    assert torch.equal(beta, torch.full((5, nh), 0.5, dtype=torch.float64))
+    np.testing.assert_allclose(soft.numpy(), sig(_bf16(logit(0.99))), rtol=2 ** -8)
+    np.testing.assert_allclose(lin.numpy(), sig(_bf16(logit(0.9))), rtol=2 ** -8)
+    tensors["soft_gate_b"] = torch.zeros(nh, dtype=torch.bfloat16)
+    tensors["lgate_up_b"] = torch.zeros(nh * d, dtype=torch.bfloat16)
+    tensors["soft_gate_w"][1, 33] = 1.0
+    tensors["beta_w"][0, 250] = 1.0
+    tensors["lgate_down_w"][7, 3] = 1.0
+    tensors["lgate_up_w"][1 * d + 5, 7] = 1.0
+    soft, beta, lin = ob.BlockOracle(tensors, SMALL).small_projections(x1)
+    xs = x1.numpy()
+    np.testing.assert_allclose(soft[:, 1].numpy(), sig(xs[:, 33]), rtol=2 ** -8)
+    np.testing.assert_allclose(soft[:, 0].numpy(), 0.5)
+    np.testing.assert_allclose(beta[:, 0].numpy(), sig(xs[:, 250]), rtol=2 ** -8)
+    np.testing.assert_allclose(lin[:, d + 5].numpy(), sig(xs[:, 3]), rtol=2 ** -8)
+    others = np.delete(lin.numpy(), d + 5, axis=1)
+    np.testing.assert_allclose(others, 0.5)
+
+
+def test_prenorm_uses_tables_scale_then_shift(small):
+    """The first prenorm takes (scale, shift) = tables (1, 0): x_hat (1 + scale) + shift
+    (fused_block.py:43-46), checked with a zero-scale / constant-shift table pair."""
     w, orc = small
-    h, temb, *_ = inputs(SMALL)
-    t = orc.tables(temb)
-    x = orc.prenorm(h.double(), w.norm1, t[1], t[0])
-    f = np.float32
-    hf = h.float().numpy()
-    inv = 1 / np.sqrt((hf.astype(np.float64) ** 2).mean(1, keepdims=True) + SMALL.eps)
-    expect = (hf * inv) * w.norm1.float().numpy() * (1 + t[1].numpy()) + t[0].numpy()
-    assert np.allclose(x.numpy(), expect, rtol=2 ** -7, atol=2 ** -7)
-    assert t[0].shape == (1, SMALL.hidden) and len(t) == 6
+    h, *_ = inputs(SMALL)
+    zero = torch.zeros(1, SMALL.hidden, dtype=torch.float64)
+    shift = torch.full((1, SMALL.hidden), 0.25, dtype=torch.float64)
+    x = orc.prenorm(h.double(), w.norm1, zero, shift)
+    hf = h.double().numpy()
+    xhat = hf / np.sqrt((hf ** 2).mean(1, keepdims=True) + SMALL.eps) * w.norm1.double().numpy()
+    np.testing.assert_allclose(x.numpy(), _bf16(xhat + 0.25), rtol=2 ** -7, atol=2 ** -9)
+    doubled = orc.prenorm(h.double(), w.norm1, torch.ones_like(zero), zero)
+    np.testing.assert_allclose(doubled.numpy(), _bf16(2 * xhat), rtol=2 ** -7, atol=2 ** -9)
+
+
+def test_output_projection_orders_agree_to_one_rounding(small):
+    """The fused [O | O_lin] projection (one accumulation) and the reference's order (two
+    projections rounded to bf16, then added) differ by bf16 rounding only, well inside
+    1e-2 of the update; with to_out_linear's weight zeroed they are identical."""
+    w, orc = small
+    g = torch.Generator().manual_seed(9)
+    inner = SMALL.inner
+    soft = torch.randn(64, inner, generator=g).to(torch.bfloat16).double()
+    far = torch.randn(64, inner, generator=g).to(torch.bfloat16).double()
+    h = torch.randn(64, SMALL.hidden, generator=g).to(torch.bfloat16).double()
+    gate = torch.randn(SMALL.hidden, generator=g).to(torch.bfloat16).double()
+    fused = orc.out_projection(soft, far, h, gate)
+    ref = orc.out_projection(soft, far, h, gate, order="reference")
+    assert 0 < float((fused - ref).norm() / (ref - h).norm()) < 1e-2
+    tensors = dict(w.tensors)
+    tensors["olin_w"] = torch.zeros_like(w.olin_w)
+    zo = ob.BlockOracle(tensors, SMALL)
+    assert torch.equal(zo.out_projection(soft, far, h, gate),
+                       zo.out_projection(soft, far, h, gate, order="reference"))
 
 
 def test_constant_context_value_passes_through_cross_attention(small):

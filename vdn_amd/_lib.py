@@ -25,7 +25,7 @@ _ptr = ctypes.c_void_p
 # name -> argtypes; every entry point returns int status.
 SIGNATURES = {
     "vdn_mxfp8_quantize": [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr],
-    "vdn_mxfp8_act_quantize": [_ptr, _i64, _i64, _i64, _i32, _ptr, _ptr, _ptr, _ptr],
+    "vdn_mxfp8_act_quantize": [_ptr, _i64, _i64, _i64, _i32, _ptr, _ptr, _ptr, _ptr, _ptr],
     "vdn_mxfp8_prenorm_quantize": [_ptr, _i64, _i64, _i64, _ptr, _f32, _ptr, _i64, _ptr, _i64,
                                    _ptr, _i32, _ptr, _ptr, _ptr, _ptr, _ptr],
     "vdn_mxfp8_gemm": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _ptr, _ptr, _i64, _ptr, _i64,

@@ -66,12 +66,12 @@ template <int kAct, bool kVec>
 __global__ void __launch_bounds__(kThreads)
 mxfp8_quantize_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t k, int64_t stride,
                       uint8_t* __restrict__ q, uint8_t* __restrict__ s, int64_t kp, int64_t items,
-                      uint32_t* __restrict__ nonfinite) {
+                      uint32_t* __restrict__ nonfinite, uint8_t* __restrict__ finite_tiles) {
   const int lane16 = threadIdx.x & 15;
   const int64_t ngroups = static_cast<int64_t>(gridDim.x) * (kThreads / 16);
   const int64_t group = static_cast<int64_t>(blockIdx.x) * (kThreads / 16) + (threadIdx.x >> 4);
   const int64_t chunks = kp >> 7;
-  bool bad = false;
+  bool bad[kItemsPerGroup];
   float v[kItemsPerGroup][8];
   // Issue every load of the group's items before any arithmetic.
 #pragma unroll
@@ -79,16 +79,18 @@ mxfp8_quantize_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t k, i
     const int64_t item = group + j * ngroups;
     const int64_t r = item < items ? item / chunks : rows;  // rows => zero fill
     const int64_t c0 = (item % chunks) * 128 + lane16 * 8;
+    bad[j] = false;
     if (kAct == kActSwiGLU) {
       float g[8];
-      load_row8<kVec>(x, r, c0, rows, k, stride, v[j], bad);
-      load_row8<kVec>(x + k, r, c0, rows, k, stride, g, bad);
+      load_row8<kVec>(x, r, c0, rows, k, stride, v[j], bad[j]);
+      load_row8<kVec>(x + k, r, c0, rows, k, stride, g, bad[j]);
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[j][i] = round_bf16(silu_mul(v[j][i], g[i]));
     } else {
-      load_row8<kVec>(x, r, c0, rows, k, stride, v[j], bad);
+      load_row8<kVec>(x, r, c0, rows, k, stride, v[j], bad[j]);
     }
   }
+  bool any_bad = false;
 #pragma unroll
   for (int j = 0; j < kItemsPerGroup; ++j) {
     const int64_t item = group + j * ngroups;
@@ -101,11 +103,16 @@ mxfp8_quantize_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t k, i
     }
     if (kAct != kActNone) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) bad |= !(fabsf(v[j][i]) < INFINITY);
+      for (int i = 0; i < 8; ++i) bad[j] |= !(fabsf(v[j][i]) < INFINITY);
     }
     quantize_store8(v[j], lane16, r, chunk, kp, q, s);
+    // Per (16-row, 256-column) tile finite flags, cleared (by every lane that saw a
+    // nonfinite input or activation; all write the same 0) in a host-initialised array.
+    if (finite_tiles != nullptr && bad[j])
+      finite_tiles[(r >> 4) * ((kp + 255) >> 8) + (chunk >> 1)] = 0;
+    any_bad |= bad[j];
   }
-  if (__ballot(bad) != 0 && (threadIdx.x & 63) == 0) atomicOr(nonfinite, 1u);
+  if (__ballot(any_bad) != 0 && (threadIdx.x & 63) == 0) atomicOr(nonfinite, 1u);
 }
 
 // One workgroup per padded row. The row stays in registers: slice j of thread t is
@@ -434,7 +441,8 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 template <int kAct>
 int launch_quantize(const void* x, int64_t rows, int64_t k, int64_t stride, void* q, void* s,
-                    uint32_t* nonfinite, hipStream_t stream, const char* name) {
+                    uint32_t* nonfinite, uint8_t* finite_tiles, hipStream_t stream,
+                    const char* name) {
   if (rows < 0 || k <= 0) return set_error(kInvalidArgument, "%s: rows must be >= 0 and K > 0", name);
   if (stride < k * (kAct == kActSwiGLU ? 2 : 1))
     return set_error(kInvalidArgument, "%s: row stride %lld smaller than row width", name,
@@ -453,10 +461,10 @@ int launch_quantize(const void* x, int64_t rows, int64_t k, int64_t stride, void
   auto* sp = static_cast<uint8_t*>(s);
   if (vec) {
     hipLaunchKernelGGL((mxfp8_quantize_kernel<kAct, true>), dim3(blocks), dim3(kThreads), 0, stream,
-                       xp, rows, k, stride, qp, sp, kp, items, nonfinite);
+                       xp, rows, k, stride, qp, sp, kp, items, nonfinite, finite_tiles);
   } else {
     hipLaunchKernelGGL((mxfp8_quantize_kernel<kAct, false>), dim3(blocks), dim3(kThreads), 0, stream,
-                       xp, rows, k, stride, qp, sp, kp, items, nonfinite);
+                       xp, rows, k, stride, qp, sp, kp, items, nonfinite, finite_tiles);
   }
   return check_launch(name);
 }
@@ -469,22 +477,25 @@ using namespace vdn;
 // Reference: src/models/ops/mxfp8_kernels.py:31-58 (_quantize / launch_quantize).
 VDN_API int vdn_mxfp8_quantize(const void* x, int64_t rows, int64_t k, int64_t row_stride,
                                void* q, void* scales, uint32_t* nonfinite, void* stream) {
-  return launch_quantize<kActNone>(x, rows, k, row_stride, q, scales, nonfinite,
+  return launch_quantize<kActNone>(x, rows, k, row_stride, q, scales, nonfinite, nullptr,
                                    static_cast<hipStream_t>(stream), "vdn_mxfp8_quantize");
 }
 
 // Reference: src/models/ops/mxfp8_kernels.py:62-84, 113-124 (_swiglu_mx) and the block's
 // GELU-tanh FFN activation. act: 1 = GELU-tanh over [R,K]; 2 = SwiGLU a*silu(g) over [R,2K].
+// finite_tiles (nullable, caller-initialised to 1): byte (r / 16) * ceil(KP / 256) + c / 256
+// is cleared when tile (16 rows, 256 output columns) holds a nonfinite input or activation,
+// the FINITE output of _swiglu_mx (mxfp8_kernels.py:73-75).
 VDN_API int vdn_mxfp8_act_quantize(const void* x, int64_t rows, int64_t k, int64_t row_stride,
                                    int act, void* q, void* scales, uint32_t* nonfinite,
-                                   void* stream) {
+                                   uint8_t* finite_tiles, void* stream) {
   auto st = static_cast<hipStream_t>(stream);
   if (act == kActGeluTanh)
-    return launch_quantize<kActGeluTanh>(x, rows, k, row_stride, q, scales, nonfinite, st,
-                                         "vdn_mxfp8_act_quantize");
+    return launch_quantize<kActGeluTanh>(x, rows, k, row_stride, q, scales, nonfinite,
+                                         finite_tiles, st, "vdn_mxfp8_act_quantize");
   if (act == kActSwiGLU)
-    return launch_quantize<kActSwiGLU>(x, rows, k, row_stride, q, scales, nonfinite, st,
-                                       "vdn_mxfp8_act_quantize");
+    return launch_quantize<kActSwiGLU>(x, rows, k, row_stride, q, scales, nonfinite,
+                                       finite_tiles, st, "vdn_mxfp8_act_quantize");
   return set_error(kInvalidArgument, "vdn_mxfp8_act_quantize: unknown activation %d", act);
 }
 

@@ -203,17 +203,22 @@ def quantize_activation(x: torch.Tensor, *, check_finite: bool = True):
 def _act_quantize(x: torch.Tensor, k: int, act: int):
     r = x.shape[0]
     q, s, flag = _new_outputs(x, r, k)
+    rp, kp = q.shape
+    # one flag per (16-row, 256-column) tile, the reference producer's program grid
+    finite = torch.ones(-(-rp // 16) * -(-kp // 256), dtype=torch.bool, device=x.device)
     if r:
         _lib.call("vdn_mxfp8_act_quantize", x.data_ptr(), r, k, _row_stride(x, x.shape[1]), act,
-                  q.data_ptr(), s.data_ptr(), flag.data_ptr(), _lib.stream(x.device))
-    return q, s, flag == 0
+                  q.data_ptr(), s.data_ptr(), flag.data_ptr(), finite.data_ptr(),
+                  _lib.stream(x.device))
+    return q, s, finite
 
 
 def launch_swiglu_quantize(x: torch.Tensor):
     """[R, 2K] -> MXFP8 of bf16(a * silu(g)), a = x[:, :K], g = x[:, K:] (mxfp8_kernels.py:113-124).
 
-    Returns (codes, scales, finite) where `finite` is a bool tensor that is all-true when
-    every input and activated value is finite.
+    Returns (codes, scales, finite): `finite` is bool [ceil(RP/16) * ceil(KP/256)], one flag
+    per (16-row, 256-column) tile of the output, False where the tile's a, g or activation
+    holds a nonfinite value (the reference producer's FINITE, one per program).
     """
     _check_activation(x)
     if x.shape[1] % 2:
