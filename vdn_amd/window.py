@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass, field
-from itertools import accumulate
+from functools import cached_property
 from numbers import Real
 
 import torch
@@ -67,46 +67,30 @@ def window_bounds(num_frames, radius, chunk=0):
 
 
 # --------------------------------------------------------------------------- plan ----
-
-def _union(ranges):
-    out = []
-    for a, b in sorted(ranges):
-        if a >= b:
-            continue
-        if out and out[-1][1] >= a:
-            out[-1] = (out[-1][0], max(b, out[-1][1]))
-        else:
-            out.append((a, b))
-    return tuple(out)
-
-
-def _count(ranges):
-    return sum(b - a for a, b in ranges)
-
-
-def _split(ranges, budget):
-    current, size = [], 0
-    for a, b in ranges:
-        while a < b:
-            end = min(b, a + budget - size)
-            current.append((a, end))
-            size += end - a
-            a = end
-            if size == budget:
-                yield tuple(current)
-                current, size = [], 0
-    if current:
-        yield tuple(current)
+#
+# The plan is built from row *units* in row order: the non-video rows before the video,
+# each video frame, and the non-video rows after it. What a query row sees is a subset of
+# units (all of them for non-video rows and row-anchor frames; for frame t the non-video
+# rows, the frames of its clamped window and the column-anchor frames), and a run of
+# adjacent visible units is one contiguous key interval. The kernel takes, per group of
+# query rows with one visible set, at most MAX_INTERVALS such intervals, and walks K and V
+# in place: nothing is gathered, so the plan allocates no index tensors on the device.
+# The reference's pass structure (budgeted varlen passes over gathered rows) is kept as a
+# lazily built host-side view with the same groups, budgets and errors.
 
 
 @dataclass(frozen=True)
 class VisibleGroup:
+    """Query rows (ranges) that see exactly the key rows `key_ranges` (sorted, disjoint)."""
     query_ranges: tuple
     key_ranges: tuple
 
 
 @dataclass(frozen=True)
 class PackedPass:
+    """One budgeted pass of the reference's plan (paper_window.py:60-70): groups, their
+    concatenated query / key row indices (int64), cumulative segment lengths (int32) and the
+    longest segments. Host tensors: the gfx950 kernel reads the interval form instead."""
     groups: tuple
     query_rows: torch.Tensor
     key_rows: torch.Tensor | None
@@ -127,119 +111,194 @@ class DevicePlan:
     nblocks: int
 
 
+def _rows(ranges):
+    return sum(b - a for a, b in ranges)
+
+
+def _cut(ranges, size):
+    """The concatenation of `ranges` (in order) cut into consecutive pieces of `size` rows
+    (the last may be shorter); each piece is a tuple of ranges."""
+    pieces, piece, room = [], [], size
+    for a, b in ranges:
+        while a < b:
+            step = min(room, b - a)
+            piece.append((a, a + step))
+            a, room = a + step, room - step
+            if room == 0:
+                pieces.append(tuple(piece))
+                piece, room = [], size
+    return pieces + ([tuple(piece)] if piece else [])
+
+
+def _join(ranges):
+    """Sorted ranges with touching neighbours joined (inputs never overlap)."""
+    joined = []
+    for a, b in sorted(r for r in ranges if r[0] < r[1]):
+        if joined and joined[-1][1] == a:
+            joined[-1] = (joined[-1][0], b)
+        else:
+            joined.append((a, b))
+    return tuple(joined)
+
+
 @dataclass(frozen=True)
 class PaperWindowPlan:
+    """Visible-set plan of one request (paper_window.py:72-84). `groups` holds one entry per
+    run of consecutive video frames with the same visible set, `dense_rows` the query rows
+    that see every row; `device_plan` is what the kernel reads."""
     layout: SequenceLayout
     bounds: tuple
     anchor_frames: str
     max_gather_rows: int
     max_query_rows: int
     device: torch.device
-    passes: tuple
+    dense_rows: tuple = ()
+    groups: tuple = ()
     device_plan: DevicePlan = field(default=None, compare=False)
+
+    @cached_property
+    def passes(self):
+        """The reference's budgeted passes: each chunk of at most max_query_rows dense rows
+        is a pass of its own; the groups' query rows, cut into chunks of at most
+        max_query_rows, are packed in order, a new pass starting before a chunk that would
+        take the pass over max_query_rows queries or max_gather_rows keys."""
+        seq = self.layout.seq_len
+        out = [_packed((VisibleGroup(chunk, ((0, seq),)),), dense=True)
+               for chunk in _cut(self.dense_rows, self.max_query_rows)]
+        open_pass, nq, nk = [], 0, 0
+        for group in self.groups:
+            keys = _rows(group.key_ranges)
+            for chunk in _cut(group.query_ranges, self.max_query_rows):
+                q = _rows(chunk)
+                if open_pass and (nq + q > self.max_query_rows or nk + keys > self.max_gather_rows):
+                    out.append(_packed(tuple(open_pass)))
+                    open_pass, nq, nk = [], 0, 0
+                open_pass.append(VisibleGroup(chunk, group.key_ranges))
+                nq, nk = nq + q, nk + keys
+        if open_pass:
+            out.append(_packed(tuple(open_pass)))
+        return tuple(out)
 
     @property
     def peak_gather_rows(self):
-        return max((p.key_rows.numel() for p in self.passes if not p.dense), default=0)
+        """Largest number of key rows a non-dense pass of the reference gathers."""
+        return max((_rows(r for g in p.groups for r in g.key_ranges)
+                    for p in self.passes if not p.dense), default=0)
 
 
-def _device_plan(groups_with_keys, device):
-    blocks, intervals, counts = [], [], []
-    for gi, (query_ranges, key_ranges) in enumerate(groups_with_keys):
-        if len(key_ranges) > MAX_INTERVALS:
-            raise ValueError(f"a visible set needs {len(key_ranges)} key intervals; the kernel "
+def _packed(groups, dense=False):
+    def index(ranges):
+        return torch.cat([torch.arange(a, b, dtype=torch.long) for a, b in ranges])
+
+    def offsets(lengths):
+        return torch.tensor([0, *lengths], dtype=torch.int64).cumsum(0).to(torch.int32)
+
+    q_len = [_rows(g.query_ranges) for g in groups]
+    k_len = [_rows(g.key_ranges) for g in groups]
+    return PackedPass(groups, index(r for g in groups for r in g.query_ranges),
+                      None if dense else index(r for g in groups for r in g.key_ranges),
+                      offsets(q_len), offsets(k_len), max(q_len), max(k_len), dense)
+
+
+def _device_plan(sets, device):
+    """Kernel form of [(query ranges, key intervals)]: every query range cut into blocks of
+    BLOCK_M rows, each naming its range end and its set; one transfer to the device."""
+    nsets = max(len(sets), 1)
+    intervals = torch.zeros(nsets, MAX_INTERVALS, 2, dtype=torch.int32)
+    counts = torch.zeros(nsets, dtype=torch.int32)
+    blocks = []
+    for index, (query_ranges, keys) in enumerate(sets):
+        if len(keys) > MAX_INTERVALS:
+            raise ValueError(f"a visible set needs {len(keys)} key intervals; the kernel "
                              f"takes at most {MAX_INTERVALS}")
-        pad = list(key_ranges) + [(0, 0)] * (MAX_INTERVALS - len(key_ranges))
-        intervals.append([list(r) for r in pad])
-        counts.append(len(key_ranges))
-        for a, b in query_ranges:
-            for q0 in range(a, b, BLOCK_M):
-                blocks.append([q0, b, gi])
-    bt = torch.tensor(blocks if blocks else [[0, 0, 0]], dtype=torch.int32)
-    it = torch.tensor(intervals if intervals else [[[0, 0]] * MAX_INTERVALS], dtype=torch.int32)
-    ct = torch.tensor(counts if counts else [0], dtype=torch.int32)
-    return DevicePlan(bt.to(device), it.to(device), ct.to(device), len(blocks))
+        if keys:
+            intervals[index, :len(keys)] = torch.tensor(keys, dtype=torch.int32)
+        counts[index] = len(keys)
+        blocks += [(q0, b, index) for a, b in query_ranges for q0 in range(a, b, BLOCK_M)]
+    block_t = torch.tensor(blocks or [(0, 0, 0)], dtype=torch.int32)
+    # one host buffer, one copy: [blocks | intervals | counts]
+    flat = torch.cat((block_t.reshape(-1), intervals.reshape(-1), counts)).to(device)
+    nb, ni = block_t.numel(), intervals.numel()
+    return DevicePlan(flat[:nb].view(-1, 3), flat[nb:nb + ni].view(nsets, MAX_INTERVALS, 2),
+                      flat[nb + ni:], len(blocks))
 
 
-def prepare_paper_window_plan(layout: SequenceLayout, bounds, anchor_frames="none", *,
-                              device="cpu", max_gather_rows=65_536, max_query_rows=8_192):
-    """Plan of visible sets per query group (paper_window.py:86-168), with the same
-    validation, grouping, pass budgets and errors; adds the kernel's interval form."""
+def _check_plan_arguments(layout, bounds, anchor_frames, max_gather_rows, max_query_rows):
+    """The reference's argument contract and messages (paper_window.py:103-115)."""
     if not isinstance(layout, SequenceLayout):
         raise TypeError("layout must be SequenceLayout")
-    s, vs, f, tpf = layout.seq_len, layout.video_start, layout.num_frames, layout.tokens_per_frame
-    if (any(type(x) is not int for x in (s, vs, f, tpf)) or s <= 0 or f < 0 or tpf <= 0 or vs < 0
-            or vs + f * tpf > s):
+    geometry = (layout.seq_len, layout.video_start, layout.num_frames, layout.tokens_per_frame)
+    if any(type(x) is not int for x in geometry):
+        raise ValueError("invalid used-row/video geometry")
+    seq, start, frames, per_frame = geometry
+    if seq <= 0 or frames < 0 or per_frame <= 0 or start < 0 or start + frames * per_frame > seq:
         raise ValueError("invalid used-row/video geometry")
     if anchor_frames not in ("none", "rows", "columns", "both"):
         raise ValueError("anchor_frames must be none, rows, columns, or both")
     if any(type(x) is not int or x <= 0 for x in (max_gather_rows, max_query_rows)):
         raise ValueError("row budgets must be positive integers")
     bounds = tuple(tuple(b) for b in bounds)
-    if len(bounds) != f or any(len(b) != 2 or any(type(x) is not int for x in b) or b[0] > b[1]
-                               for b in bounds):
+    well_formed = all(len(b) == 2 and type(b[0]) is int and type(b[1]) is int and b[0] <= b[1]
+                      for b in bounds)
+    if len(bounds) != frames or not well_formed:
         raise ValueError("one ordered integer bound pair required per video frame")
+    return bounds
+
+
+def prepare_paper_window_plan(layout: SequenceLayout, bounds, anchor_frames="none", *,
+                              device="cpu", max_gather_rows=65_536, max_query_rows=8_192):
+    """Plan of each query row's visible key rows (the contract of paper_window.py:86-168:
+    inclusive frame bounds clamped to the video, non-video rows seen by and seeing every
+    row, anchor frames 0 and F-1 as rows and/or columns, a visible set over
+    max_gather_rows refused, the same errors), in the kernel's interval form."""
+    bounds = _check_plan_arguments(layout, bounds, anchor_frames, max_gather_rows,
+                                   max_query_rows)
     device = torch.device(device)
     if device.type == "cuda" and device.index is None:
         device = torch.device("cuda", torch.cuda.current_device())
-    ve = vs + f * tpf
-    globals_ = _union(((0, vs), (ve, s)))
-    anchors = {0, f - 1} if f else set()
-    row_anchors = anchors if anchor_frames in ("rows", "both") else set()
-    col_anchors = anchors if anchor_frames in ("columns", "both") else set()
-    dense_ranges, groups = list(globals_), []
-    for frame in range(f):
-        qr = (vs + frame * tpf, vs + (frame + 1) * tpf)
-        lo, hi = bounds[frame]
-        kr = _union(list(globals_) + [(vs + max(0, lo) * tpf, vs + min(f, hi + 1) * tpf)]
-                    + [(vs + a * tpf, vs + (a + 1) * tpf) for a in col_anchors])
-        if frame in row_anchors or kr == ((0, s),):
-            dense_ranges.append(qr)
+    seq, start, frames, per_frame = (layout.seq_len, layout.video_start, layout.num_frames,
+                                     layout.tokens_per_frame)
+    end = start + frames * per_frame
+    # units in row order: (first row, end row, frame or -1 for non-video rows)
+    units = ([(0, start, -1)] if start else []) + \
+        [(start + t * per_frame, start + (t + 1) * per_frame, t) for t in range(frames)] + \
+        ([(end, seq, -1)] if end < seq else [])
+    edge = {0, frames - 1} if frames else set()
+    row_anchor = edge if anchor_frames in ("rows", "both") else set()
+    col_anchor = edge if anchor_frames in ("columns", "both") else set()
+
+    def keys_of(t):
+        lo, hi = max(0, bounds[t][0]), min(frames - 1, bounds[t][1])
+        return _join((a, b) for a, b, u in units
+                     if u < 0 or lo <= u <= hi or u in col_anchor)
+
+    everything = ((0, seq),)
+    frame_keys = [everything if t in row_anchor else keys_of(t) for t in range(frames)]
+    dense = [(a, b) for a, b, u in units if u < 0 or frame_keys[u] == everything]
+    groups = []
+    for t, keys in enumerate(frame_keys):
+        if keys == everything:
+            continue
+        if not keys:
+            raise ValueError(f"video frame {t} has no visible keys")
+        if _rows(keys) > max_gather_rows:
+            raise ValueError(f"visible set requires {_rows(keys)} gather rows, "
+                             f"budget={max_gather_rows}; increase max_gather_rows")
+        rows = (start + t * per_frame, start + (t + 1) * per_frame)
+        # consecutive frames with one visible set share a group (one run of query rows)
+        if groups and groups[-1][1] == keys and groups[-1][0][-1] == rows[0]:
+            groups[-1][0][-1] = rows[1]
         else:
-            if not kr:
-                raise ValueError(f"video frame {frame} has no visible keys")
-            if _count(kr) > max_gather_rows:
-                raise ValueError(f"visible set requires {_count(kr)} gather rows, "
-                                 f"budget={max_gather_rows}; increase max_gather_rows")
-            if groups and groups[-1].key_ranges == kr and groups[-1].query_ranges[-1][1] == qr[0]:
-                groups[-1] = VisibleGroup(_union(groups[-1].query_ranges + (qr,)), kr)
-            else:
-                groups.append(VisibleGroup((qr,), kr))
-
-    def indices(ranges):
-        return torch.cat([torch.arange(a, b, dtype=torch.long) for a, b in ranges]).to(device)
-
-    def make_pass(gs, dense=False):
-        qlens = [_count(g.query_ranges) for g in gs]
-        klens = [_count(g.key_ranges) for g in gs]
-
-        def cumulative(lengths):
-            return torch.tensor([0] + list(accumulate(lengths)), dtype=torch.int32, device=device)
-        return PackedPass(tuple(gs), indices(tuple(r for g in gs for r in g.query_ranges)),
-                          None if dense else indices(tuple(r for g in gs for r in g.key_ranges)),
-                          cumulative(qlens), cumulative(klens), max(qlens), max(klens), dense)
-
-    dense_union = _union(dense_ranges)
-    passes = [make_pass([VisibleGroup(qr, ((0, s),))], True)
-              for qr in _split(dense_union, max_query_rows)]
-    current, nq, nk = [], 0, 0
-    for group in groups:
-        for qr in _split(group.query_ranges, max_query_rows):
-            small = VisibleGroup(qr, group.key_ranges)
-            qlen, klen = _count(qr), _count(small.key_ranges)
-            if current and (nq + qlen > max_query_rows or nk + klen > max_gather_rows):
-                passes.append(make_pass(current))
-                current, nq, nk = [], 0, 0
-            current.append(small)
-            nq, nk = nq + qlen, nk + klen
-    if current:
-        passes.append(make_pass(current))
-    if sum(p.query_rows.numel() for p in passes) != s:
-        raise AssertionError("internal plan coverage mismatch")
-    kernel_groups = ([(dense_union, ((0, s),))] if dense_union else []) + \
+            groups.append(([rows[0], rows[1]], keys))
+    dense_rows = _join(dense)
+    groups = tuple(VisibleGroup(((a, b),), keys) for (a, b), keys in groups)
+    sets = ([(dense_rows, everything)] if dense_rows else []) + \
         [(g.query_ranges, g.key_ranges) for g in groups]
+    covered = _rows(dense_rows) + sum(_rows(g.query_ranges) for g in groups)
+    if covered != seq:
+        raise AssertionError(f"window plan covers {covered} of {seq} query rows")
     return PaperWindowPlan(layout, bounds, anchor_frames, max_gather_rows, max_query_rows, device,
-                           tuple(passes), _device_plan(kernel_groups, device))
+                           dense_rows, groups, _device_plan(sets, device))
 
 
 # ---------------------------------------------------------------------- attention ----
