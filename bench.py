@@ -290,7 +290,7 @@ def h3_block(steps, plans_of):
         block(hidden, temb, ctx, layout, rope, plan, cplan)
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        with _lib.LaunchTimer(set(GEMMS) | {"vdn_mxfp8_act_quantize"}) as timer:
+        with _lib.LaunchTimer(set(GEMMS)) as timer:
             start.record()
             for _ in range(steps):
                 block(hidden, temb, ctx, layout, rope, plan, cplan)
@@ -305,7 +305,174 @@ def h3_block(steps, plans_of):
                         f"+-1 frame window, {cfg.context} context rows",
             "ms_per_block": round(ms, 3),
             "mxfp8_gemm_tflops": round(g[2] / (g[1] * 1e-3) / 1e12, 1),
-            "swiglu_producer_ms": round(per.get("vdn_mxfp8_act_quantize", [0, 0.0])[1] / steps, 3)}
+            # the FFN up projection with the SwiGLU producer in its epilogue (one launch)
+            "ffn_up_swiglu_gemm_ms": round(
+                per.get("vdn_mxfp8_gemm_act_quantize", [0, 0.0])[1] / steps, 3)}
+
+
+def _launch_ms(timer, name):
+    times = [t for n, _, t in timer.durations() if n == name]
+    return sum(times) / len(times) if times else float("nan")
+
+
+def c2_quantize_gemm(steps):
+    """MXFP8 quantize + block-scaled GEMM alone: bf16 activations [32768, 5120] ~ N(0,1)
+    with 1% of the channels (51, seeded) scaled x20; weights [N, 5120] ~ N(0, 0.02) for
+    N = 5120, 15360 (fused QKV), 13824 (FFN up); bf16 output. Algorithmic work: the
+    quantize reads 2 B and writes 1 + 1/32 B per (padded) element; a GEMM is 2 M N K FLOP."""
+    if steps <= 0:
+        return None
+    import torch
+    from vdn_amd import _lib
+    from vdn_amd import mxfp8 as vm
+    m, k = 32768, 5120
+    g = torch.Generator(device="cuda").manual_seed(2)
+    x = torch.randn(m, k, generator=g, device="cuda")
+    cols = torch.randperm(k, generator=g, device="cuda")[:k // 100]
+    x[:, cols] *= 20
+    x = x.to(torch.bfloat16)
+    qbytes = m * k * 2 + m * k * (1 + 1 / 32)
+    vm.launch_quantize(x)
+    torch.cuda.synchronize()
+    with _lib.LaunchTimer({"vdn_mxfp8_quantize"}) as timer:
+        for _ in range(steps):
+            q, s = vm.launch_quantize(x)
+        torch.cuda.synchronize()
+    qms = _launch_ms(timer, "vdn_mxfp8_quantize")
+    out = {"workload": f"bf16 [{m}, {k}] N(0,1) with {k // 100} outlier channels x20; "
+                       f"weights [N, {k}] N(0,0.02); bf16 output",
+           "quantize": {"us": round(qms * 1e3, 2), "gbs": round(qbytes / (qms * 1e-3) / 1e9, 1),
+                        "hbm_frac": round(qbytes / (qms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                        "target_us": 90.8}}
+    del x
+    for n in (5120, 15360, 13824):
+        w = (torch.randn(n, k, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+        wq, ws = vm.launch_quantize(w)
+        del w
+        y = vm.mxfp8_gemm(q, s, wq, ws, n, rows=m)
+        torch.cuda.synchronize()
+        with _lib.LaunchTimer({"vdn_mxfp8_gemm"}) as timer:
+            for _ in range(steps):
+                vm.mxfp8_gemm(q, s, wq, ws, n, rows=m, out=y)
+            torch.cuda.synchronize()
+        ms = _launch_ms(timer, "vdn_mxfp8_gemm")
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        out[f"gemm_n{n}"] = {"ms": round(ms, 4), "tflops": round(tf, 1),
+                             "mxfp8_frac": round(tf / PEAK_MXFP8_TFLOPS, 4)}
+        del wq, ws, y
+    log("C2: " + ", ".join(f"{key} {v.get('ms', v.get('us'))}" for key, v in out.items()
+                           if isinstance(v, dict)))
+    return out
+
+
+def c3_vda(steps, frames=30):
+    """The VDA linear-attention branch alone at the clip shape: 30 frames x 3600 tokens, 40
+    heads x 128, bf16 q, k, v ~ N(0,1) with q and k L2-normalised, beta = sigmoid(N(0,1)),
+    alpha = exp(-A_h dt_c) (A ~ U(1,16) per head, dt log-uniform in [1e-3, 1e-1]), output
+    gate sigmoid(N(0,1)), norm weight 1, one chunk per frame, +-1 frame window, fp32 state.
+    The branch runs statistics, factors, both scans, the gather and the gated readout."""
+    if steps <= 0:
+        return None
+    import torch
+    import torch.nn.functional as F
+    from vdn_amd import _lib
+    from vdn_amd import vda as vv
+    heads, spatial = 40, HEIGHT * WIDTH
+    t = frames * spatial
+    g = torch.Generator(device="cuda").manual_seed(3)
+
+    def normal(*shape):
+        return torch.randn(*shape, generator=g, device="cuda")
+
+    q = F.normalize(normal(t, heads, D), dim=-1).to(torch.bfloat16)
+    k = F.normalize(normal(t, heads, D), dim=-1).to(torch.bfloat16)
+    v = normal(t, heads, D).to(torch.bfloat16)
+    beta = torch.sigmoid(normal(t, heads)).to(torch.bfloat16)
+    gate = torch.sigmoid(normal(t, heads, D)).to(torch.bfloat16)
+    a = torch.rand(heads, generator=g, device="cuda") * 15 + 1
+    dt = torch.exp(torch.rand(heads, D, generator=g, device="cuda")
+                   * (math.log(0.1) - math.log(1e-3)) + math.log(1e-3))
+    alpha = torch.exp(-a[:, None] * dt)[None].expand(frames, heads, D).contiguous()
+    normw = torch.ones(D, device="cuda")
+    bounds = [(f - 1, f + 1) for f in range(frames)]
+    out = torch.empty(t, heads * D, dtype=torch.bfloat16, device="cuda")
+
+    def run():
+        vv.vda_forward(q, k, v, beta, gate, alpha, bounds, frames, spatial, normw, 1e-6,
+                       chunk_size=8, out=out)
+
+    with torch.no_grad():
+        run()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with _lib.LaunchTimer(set(VDA_ENTRIES)) as timer:
+            start.record()
+            for _ in range(steps):
+                run()
+            end.record()
+            torch.cuda.synchronize()
+    wall = start.elapsed_time(end) / steps
+    per = aggregate(timer, {})
+    kern = sum(e[1] for e in per.values()) / steps
+    nbytes = sum(e[3] for e in per.values()) / steps
+    hb = [sum(per[n][i] for n in VDA_HBM_BOUND if n in per) for i in range(4)]
+    hb_gbs = hb[3] / (hb[1] * 1e-3) / 1e9
+    log(f"C3: VDA branch {wall:.3f} ms per call ({kern:.3f} ms in kernels)")
+    return {"workload": f"VDA branch, {frames} frames x {spatial} tokens, {heads}x{D} heads, "
+                        f"bf16 q,k,v N(0,1) (q, k L2-normalised), fp32 state",
+            "ms": round(wall, 4), "kernel_ms": round(kern, 4),
+            "gbs": round(nbytes / (kern * 1e-3) / 1e9, 1),
+            "hbm_bound_passes": {"entries": [n for n in VDA_HBM_BOUND if n in per],
+                                 "ms": round(hb[1] / steps, 4), "gbs": round(hb_gbs, 1),
+                                 "hbm_frac": round(hb_gbs / PEAK_HBM_GBS, 4)},
+            "passes": breakdown_of(per, steps)}
+
+
+def c4_window(steps, frames=30):
+    """The frame-window softmax branch alone: 30 frames x 3600 tokens, 40 heads x 128, bf16
+    q, k, v ~ N(0,1)/sqrt(128); QK RMSNorm (weight 1) + 3D RoPE (t, h, w split 44/42/42,
+    theta 1e4), then exact softmax over the frame and its +-1 neighbours. Algorithmic work of
+    the attention: 4 d FLOP per visible (query, key) pair per head (2.336e13 FLOP)."""
+    if steps <= 0:
+        return None
+    import torch
+    from vdn_amd import _lib
+    from vdn_amd import window as vw
+    heads, spatial = 40, HEIGHT * WIDTH
+    t = frames * spatial
+    g = torch.Generator(device="cuda").manual_seed(4)
+    q, k, v = ((torch.randn(t, heads, D, generator=g, device="cuda") * D ** -0.5)
+               .to(torch.bfloat16) for _ in range(3))
+    ones = torch.ones(D, dtype=torch.bfloat16, device="cuda")
+    cos, sin = vw.rope_tables_3d(frames, HEIGHT, WIDTH, device="cuda", dtype=torch.bfloat16)
+    layout = vw.SequenceLayout(t, 0, frames, spatial, frame_height=HEIGHT, frame_width=WIDTH)
+    plan = vw.prepare_paper_window_plan(layout, vw.window_bounds(frames, 1), device="cuda")
+    pairs = visible_pairs(frames, spatial, 1)
+    flop = 4.0 * D * heads * pairs
+
+    def run():
+        qo, ko = vw.paper_qk_rmsnorm_rope(q, k, ones, ones, 1e-6, cos, sin, enabled=True)
+        return vw.paper_window_attention(qo, ko, v, plan, enabled=True)
+
+    with torch.no_grad():
+        run()
+        torch.cuda.synchronize()
+        with _lib.LaunchTimer({"vdn_qk_rmsnorm_rope", "vdn_window_attention"}) as timer:
+            for _ in range(steps):
+                run()
+            torch.cuda.synchronize()
+    rope = _launch_ms(timer, "vdn_qk_rmsnorm_rope")
+    attn = _launch_ms(timer, "vdn_window_attention")
+    tf = flop / (attn * 1e-3) / 1e12
+    rope_bytes = 2 * t * heads * D * 4 + 2 * t * D * 2
+    log(f"C4: RoPE {rope:.3f} ms, window attention {attn:.3f} ms ({tf:.0f} TFLOP/s)")
+    return {"workload": f"QK RMSNorm + 3D RoPE, then +-1 frame window softmax, {frames} frames x "
+                        f"{spatial} tokens, {heads}x{D} heads, bf16",
+            "ms": round(rope + attn, 4), "attention_ms": round(attn, 4),
+            "attention_tflops": round(tf, 1), "attention_bf16_frac": round(tf / PEAK_BF16_TFLOPS, 4),
+            "attention_frac_of_mxfp8_peak": round(tf / PEAK_MXFP8_TFLOPS, 4),
+            "flop": flop, "qk_rope_ms": round(rope, 4),
+            "qk_rope_gbs": round(rope_bytes / (rope * 1e-3) / 1e9, 1)}
 
 
 def visible_pairs(frames, spatial, radius):
@@ -317,11 +484,23 @@ def visible_pairs(frames, spatial, radius):
     return total
 
 
+def host_threads():
+    """Host cores this process may run on (its CPU affinity; os.cpu_count() counts the
+    whole machine, which a GPU box shares among its GPUs)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
 def cpu_baseline(cfg, weights, hidden, temb, ctx, cos, sin, frames_total, sample_frames):
     """The fp32 CPU block (the oracle's eager path) on the first `sample_frames` frames,
-    extrapolated linearly in frames to the full clip."""
+    extrapolated linearly in frames to the full clip, on every host core available."""
     import torch
     from oracle import block as ob
+    threads = host_threads()
+    torch.set_num_threads(threads)
+    log(f"CPU baseline on {torch.get_num_threads()} threads (os.cpu_count() = {os.cpu_count()})")
     spatial = HEIGHT * WIDTH
     t = sample_frames * spatial
     w = {k: v.cpu() for k, v in weights.tensors.items()}
@@ -353,6 +532,44 @@ def summarize_counters(path):
                   key=lambda r: -r[1])
     for (kernel, counter), mean, n in rows:
         print(f"{counter}\t{mean:.1f}\t{n}\t{kernel[:150]}")
+
+
+def summarize_trace(stats_csv, bench_log, command):
+    """Markdown summary of a rocprofv3 --kernel-trace --stats run of bench.py: one row per
+    kernel (calls, total, average, share) and the MXFP8 GEMM family's average launch time
+    beside the one the same run's bench line reports (HIP events on the launch stream)."""
+    import csv
+    rows = []
+    with open(stats_csv) as f:
+        for r in csv.DictReader(f):
+            rows.append((r["Name"], int(r["Calls"]), float(r["TotalDurationNs"]) / 1e6))
+    total = sum(t for _, _, t in rows)
+    line = None
+    with open(bench_log) as f:
+        for text in f:
+            if text.startswith("{"):
+                line = json.loads(text)
+    gemm = [(c, t) for n, c, t in rows if GEMM_KERNEL.search(n)]
+    g_calls, g_ms = sum(c for c, _ in gemm), sum(t for _, t in gemm)
+
+    def short(name):
+        name = name.replace("void ", "").replace("(anonymous namespace)::", "")
+        return name.split("(")[0][:80]
+
+    out = [f"Command (from the repository root, on one MI355X):", "", f"    {command}", "",
+           f"All kernels: {total:.1f} ms over {sum(c for _, c, _ in rows)} dispatches "
+           "(the whole process, input setup included).", ""]
+    if line is not None:
+        out += [f"The same run's bench line: {line['value']:.2f} ms per block; its MXFP8 GEMM "
+                f"family averages {line['roofline']['avg_launch_ms']:.4f} ms per launch (HIP "
+                f"events), the trace {g_ms / g_calls:.4f} ms ({g_calls} launches).", ""]
+    out += ["| kernel | calls | total ms | avg ms | % |", "|---|---:|---:|---:|---:|"]
+    for name, calls, t in sorted(rows, key=lambda r: -r[2]):
+        if t / total < 2e-4:
+            continue
+        out.append(f"| `{short(name)}` | {calls} | {t:.3f} | {t / calls:.4f} | "
+                   f"{100 * t / total:.2f} |")
+    print("\n".join(out))
 
 
 TRAFFIC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
@@ -443,6 +660,9 @@ def main():
     p.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                    help="print the GEMM HBM-traffic summary of a FETCH_SIZE and a WRITE_SIZE "
                         "pass and exit")
+    p.add_argument("--summarize-trace", nargs=3, metavar=("STATS_CSV", "BENCH_LOG", "COMMAND"),
+                   help="print the markdown kernel-trace summary of a rocprofv3 --stats run of "
+                        "bench.py (its kernel_stats.csv, its output, the command) and exit")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="after the timed steps, negate one 1 GiB bf16 buffer into another (an "
                         "elementwise kernel of known traffic for scaling HBM byte counters)")
@@ -452,6 +672,9 @@ def main():
     p.add_argument("--frames", type=int, default=30)
     p.add_argument("--cpu-sample-frames", type=int, default=6)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--config-steps", type=int, default=5,
+                   help="timed repeats of the stand-alone config measurements (C2 quantize + "
+                        "GEMMs, C3 VDA branch, C4 RoPE + window attention); 0 skips them")
     p.add_argument("--isolated-steps", type=int, default=2,
                    help="untimed-for-value steps with the VDA branch after the window attention "
                         "on one stream, for the branch kernels' own launch times")
@@ -461,6 +684,9 @@ def main():
         return
     if args.summarize_traffic:
         summarize_traffic(*args.summarize_traffic)
+        return
+    if args.summarize_trace:
+        summarize_trace(*args.summarize_trace)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the block runs whole on a single MI355X "
@@ -550,6 +776,9 @@ def main():
                   lambda p, c, f, s, t, l: {p.device_plan.intervals.data_ptr():
                                             visible_pairs(f, s, cfg.radius),
                                             c.intervals.data_ptr(): t * l})
+    configs = {"C2": c2_quantize_gemm(args.config_steps),
+               "C3": c3_vda(args.config_steps, frames),
+               "C4": c4_window(args.config_steps, frames)}
     traffic = traffic_per_launch()
 
     result = {
@@ -571,6 +800,11 @@ def main():
                      "achieved": round(gemm_tflops, 1), "peak": PEAK_MXFP8_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_MXFP8_TFLOPS, 4),
                      "traffic": traffic,
+                     "traffic_source": ("recorded, not measured in this run: " +
+                                        os.path.relpath(TRAFFIC_SUMMARY, os.path.dirname(
+                                            os.path.abspath(__file__))) +
+                                        " (rocprofv3 FETCH_SIZE + WRITE_SIZE passes)")
+                     if traffic is not None else None,
                      "avg_launch_ms": round(g[1] / g[0], 4),
                      "flop_per_launch": g[2] / g[0]},
         "mxfp8_tflops": round(gemm_tflops, 1),
@@ -581,6 +815,7 @@ def main():
                                  "ms": round(hb_t / iso_steps, 3)},
         "window_attention_tflops": round(w[2] / (w[1] * 1e-3) / 1e12, 1),
         "window_attention_bf16_frac": round(w[2] / (w[1] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "configs": configs,
         "short_conv_prepare": conv,
         "production_geometry": production,
         "h3_widths": h3,
