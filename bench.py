@@ -518,20 +518,57 @@ def cpu_baseline(cfg, weights, hidden, temb, ctx, cos, sin, frames_total, sample
                         f"to {frames_total} frames"))
 
 
-def summarize_counters(path):
-    """Mean per dispatch of each counter per kernel from a rocprofv3 counter_collection.csv
-    (one row per dispatch and counter), printed as text, largest first."""
+def summarize_counters(paths, command=""):
+    """Markdown table of per-dispatch means of every counter in one or more rocprofv3 --pmc
+    counter_collection.csv files (one pass each), one row per kernel. FETCH_SIZE and
+    WRITE_SIZE (KiB) are scaled to bytes by the factor that maps their reading for the
+    calibration kernel (a torch.neg of 1 GiB into 1 GiB, --calibrate-copy) onto 1 GiB."""
     import csv
-    sums, dispatches = {}, {}
-    with open(path) as f:
-        for row in csv.DictReader(f):
-            key = (row["Kernel_Name"], row["Counter_Name"])
-            sums[key] = sums.get(key, 0.0) + float(row["Counter_Value"])
-            dispatches.setdefault(key, set()).add(row["Dispatch_Id"])
-    rows = sorted(((k, v / len(dispatches[k]), len(dispatches[k])) for k, v in sums.items()),
-                  key=lambda r: -r[1])
-    for (kernel, counter), mean, n in rows:
-        print(f"{counter}\t{mean:.1f}\t{n}\t{kernel[:150]}")
+    means, names = {}, {}
+    for path in paths:
+        per = {}
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                key = (r["Kernel_Name"], r["Counter_Name"])
+                d = r["Dispatch_Id"]
+                per.setdefault(key, {})
+                per[key][d] = per[key].get(d, 0.0) + float(r["Counter_Value"])
+        for (kernel, counter), by_dispatch in per.items():
+            means.setdefault(kernel, {})[counter] = (sum(by_dispatch.values()) / len(by_dispatch),
+                                                     len(by_dispatch))
+            names[counter] = True
+    scale = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        cal = [v[counter][0] for k, v in means.items() if CALIBRATION_KERNEL in k and counter in v]
+        if cal:
+            scale[counter] = CALIBRATION_KIB / max(cal) * 1024   # KiB reading -> bytes
+    counters = sorted(names)
+
+    def short(name):
+        name = name.replace("void ", "").replace("(anonymous namespace)::", "")
+        return name.split("(")[0].replace("vdn::", "")[:60]
+
+    def fmt(counter, value):
+        if counter in scale:
+            return f"{value * scale[counter] / 1e9:.3f} GB"
+        return f"{value:.3g}"
+
+    out = []
+    if command:
+        out += ["Commands (from the repository root, on one MI355X):", "", *[f"    {c}" for c in
+                                                                          command.split(" ;; ")], ""]
+    if scale:
+        out += ["Byte counters are scaled by the calibration kernel (1 GiB read, 1 GiB written): " +
+                ", ".join(f"{c} x{scale[c] / 1024:.4f}" for c in scale) + ".", ""]
+    out += ["| kernel | dispatches | " + " | ".join(counters) + " |",
+            "|---|---:|" + "---:|" * len(counters)]
+    for kernel, vals in sorted(means.items(), key=lambda kv: kv[0]):
+        if CALIBRATION_KERNEL not in kernel and not any(t in kernel for t in ("vdn::", "vda_", "mxfp8", "window_attn", "qk_rope", "prenorm")):
+            continue
+        n = max(v[1] for v in vals.values())
+        out.append(f"| `{short(kernel)}` | {n} | " +
+                   " | ".join(fmt(c, vals[c][0]) if c in vals else "" for c in counters) + " |")
+    print("\n".join(out))
 
 
 def summarize_trace(stats_csv, bench_log, command):
@@ -653,10 +690,24 @@ def traffic_per_launch():
     return None
 
 
+def calibrate_copy():
+    """One elementwise kernel of known traffic (torch.neg of 2^29 bf16 values into another
+    buffer: 1 GiB read, 1 GiB written) for scaling HBM byte counters."""
+    import torch
+    src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    log("negated 1 GiB into 1 GiB (calibration kernel: 1 GiB read, 1 GiB written)")
+
+
 def main():
     p = argparse.ArgumentParser()
-    p.add_argument("--summarize-counters", metavar="CSV",
-                   help="print per-kernel mean counters of a rocprofv3 --pmc CSV and exit")
+    p.add_argument("--summarize-counters", nargs="+", metavar="CSV",
+                   help="print the markdown table of per-kernel mean counters of one or more "
+                        "rocprofv3 --pmc CSVs and exit")
+    p.add_argument("--command", default="",
+                   help="the profiling commands to quote in a summary (separated by ' ;; ')")
     p.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                    help="print the GEMM HBM-traffic summary of a FETCH_SIZE and a WRITE_SIZE "
                         "pass and exit")
@@ -675,12 +726,15 @@ def main():
     p.add_argument("--config-steps", type=int, default=5,
                    help="timed repeats of the stand-alone config measurements (C2 quantize + "
                         "GEMMs, C3 VDA branch, C4 RoPE + window attention); 0 skips them")
+    p.add_argument("--configs-only", action="store_true",
+                   help="run only the stand-alone config measurements (C2, C3, C4) and print "
+                        "them as one JSON line (for profiling their kernels apart from the block)")
     p.add_argument("--isolated-steps", type=int, default=2,
                    help="untimed-for-value steps with the VDA branch after the window attention "
                         "on one stream, for the branch kernels' own launch times")
     args = p.parse_args()
     if args.summarize_counters:
-        summarize_counters(args.summarize_counters)
+        summarize_counters(args.summarize_counters, args.command)
         return
     if args.summarize_traffic:
         summarize_traffic(*args.summarize_traffic)
@@ -703,6 +757,13 @@ def main():
     _lib.load()
     cfg = BlockConfig()
     frames = args.frames
+    if args.configs_only:
+        steps = max(args.config_steps, 1)
+        print(json.dumps({"configs": {"C2": c2_quantize_gemm(steps), "C3": c3_vda(steps, frames),
+                                      "C4": c4_window(steps, frames)}}), flush=True)
+        if args.calibrate_copy:
+            calibrate_copy()
+        return
     spatial = HEIGHT * WIDTH
     tokens = frames * spatial
     log(f"building block weights (hidden {cfg.hidden}, ffn {cfg.ffn}) and inputs "
@@ -736,12 +797,7 @@ def main():
     ms = start.elapsed_time(end) / args.steps
     log(f"timed {args.steps} steps: {ms:.2f} ms per block")
     if args.calibrate_copy:
-        src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda")
-        dst = torch.empty_like(src)
-        torch.neg(src, out=dst)
-        torch.cuda.synchronize()
-        log("negated 1 GiB into 1 GiB (calibration kernel: 1 GiB read, 1 GiB written)")
-        del src, dst
+        calibrate_copy()
 
     per = aggregate(timer, plans)
     breakdown = breakdown_of(per, args.steps)

@@ -5,7 +5,7 @@
 // (softmax_attention/kernels.py:51-67). Each query block attends to a short list of key
 // intervals (the frame window, global rows, anchor frames), so no K/V gather copies exist.
 //
-// Per workgroup: 256 queries of one head (8 waves x 32), key tiles of 64.
+// Per workgroup: 256 queries of one head (8 waves x 32), key tiles of 128.
 //   Sᵀ[key][q] = K · Qᵀ   on v_mfma_f32_32x32x16_bf16 (A = K rows, B = Q rows; Q fragments for
 //                         all 128 channels stay in registers for the whole kernel);
 //   online softmax in the exp2 domain, fp32 running max / sum per query;
@@ -15,8 +15,10 @@
 //                         4g.., 4-7 = keys 8+4g..; measured), so P never leaves registers;
 //                         Vᵀ fragments come from the token-major V tile via ds_read_tr16_b64.
 // K/V tiles stream global -> LDS with buffer_load_dwordx4 ... lds, double-buffered; 16-byte
-// chunk c of tile row r is stored at c ^ (r & 15) (K: row reads) or c ^ 2 (r & 7) (V: the
-// 4-row transpose reads), which keeps both read patterns free of bank conflicts.
+// chunk c of tile row r is stored at c ^ (r & 15) (K: row reads) or c ^ 4 (r & 3) (V: the
+// transpose reads, where the 32 lanes served together touch rows r..r+3 and chunks
+// 4j..4j+3 of each, which the XOR spreads over all 16 chunk positions of the bank space),
+// which keeps both read patterns free of bank conflicts.
 #include "mxfp8_common.h"
 
 #include <math.h>
@@ -58,7 +60,7 @@ __device__ __forceinline__ bf16x4_t lds_read_tr(const uint16_t* p) {
 }
 
 __device__ __forceinline__ int swz_k(int row) { return row & 15; }
-__device__ __forceinline__ int swz_v(int row) { return 2 * (row & 7); }
+__device__ __forceinline__ int swz_v(int row) { return 4 * (row & 3); }
 
 // MXFP8 destination of the output (instead of bf16 rows): codes [rows, kp] and
 // SWIZZLE_32_4_4 scales; head h of query row q fills 128-column chunk chunk0 + h, exactly
@@ -108,8 +110,11 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
   }
   const int h = pid / nblocks;
   const int blk = pid % nblocks;
-  const int q0 = blocks[3 * blk], q1 = blocks[3 * blk + 1], grp = blocks[3 * blk + 2];
-  const int nint = grp_n[grp];
+  // block bounds as wave-uniform scalars, so the per-wave branches below stay scalar
+  const int q0 = __builtin_amdgcn_readfirstlane(blocks[3 * blk]);
+  const int q1 = __builtin_amdgcn_readfirstlane(blocks[3 * blk + 1]);
+  const int grp = __builtin_amdgcn_readfirstlane(blocks[3 * blk + 2]);
+  const int nint = __builtin_amdgcn_readfirstlane(grp_n[grp]);
   const int* kv = grp_kv + grp * kMaxIntervals * 2;
 
   const int tid = threadIdx.x, lane = tid & 63;
