@@ -296,6 +296,48 @@ int vdn_window_attention_mxfp8(const void* q, int64_t q_st, int64_t q_sh, const 
                                int64_t g_st, int64_t g_sh, void* codes, void* scales, int64_t kp,
                                int chunk0, void* stream);
 
+/*
+ * Gate projections of the hybrid block's attention input x [frames * spatial, k] bf16 (row
+ * stride x_st, rows frame-major), one bf16 MFMA pass. w [384, k] bf16 holds the softmax-gate
+ * rows (heads of them, zero rows up to 64), the beta rows (same), the output gate's down rows
+ * (128) and FrameKDAAlpha's down rows (128). Writes
+ *   soft_gate [T, heads] = bf16(sigmoid(bf16(x w_g^T + gate_bias)))   (one Linear with bias),
+ *   beta      [T, heads] = bf16(sigmoid(bf16(x w_b^T))),
+ *   gate_down [T, 128]   = bf16(x w_down^T)                            (all bf16, contiguous),
+ *   partial [frames * ceil(spatial / 128), 128] fp32: sums over each 128-row block of a frame
+ *   of x w_alpha^T (vdn_frame_alpha turns them into the frame mean's projection).
+ * heads even and <= 64, k a multiple of 32; x, w and gate_down 16-byte aligned, soft_gate and
+ * beta 4-byte aligned.
+ * Replaces: the softmax gate, beta and output-gate projections of tp_attention_forward
+ * (src/inference/utils/tensor_parallel.py:194-198; OutputGate, src/models/attention_gates.py:
+ * 52-55) and its frame mean (:198).
+ */
+int vdn_gate_projection(const void* x, int64_t x_st, int64_t k, const void* w, int heads,
+                        int frames, int spatial, const void* gate_bias, void* soft_gate,
+                        void* beta, void* gate_down, float* partial, void* stream);
+
+/*
+ * FrameKDAAlpha from vdn_gate_projection's partial sums: mean[f] = (sum of the frame's
+ * partial rows) / spatial, delta = mean up_w^T + dt_bias, alpha [frames, heads, head_dim] fp32
+ * = exp(-exp(a_log[h]) softplus(delta)) (softplus threshold 20). up_w [heads * head_dim, 128]
+ * bf16, dt_bias [heads * head_dim] fp32, a_log [heads] fp32.
+ * Replaces: FrameKDAAlpha.forward (src/models/linear_attention/layers.py:36-69).
+ */
+int vdn_frame_alpha(const float* partial, int frames, int spatial, const void* up_w,
+                    const float* dt_bias, const float* a_log, int heads, int head_dim,
+                    float* alpha, void* stream);
+
+/*
+ * AdaLN tables out [m, n] bf16 (row stride o_st) = bf16(s w^T + b), s = bf16(SiLU(temb in
+ * fp32)), temb [m, k] bf16 (temb_f32 = 0) or fp32 (row stride t_st), w [n, k] bf16
+ * contiguous and 16-byte aligned, b [n] bf16 or null; k a multiple of 8, at most 16384.
+ * Replaces: the table projection of _project_schedule (src/inference/utils/paper_adaln.py:
+ * 174-188), F.linear(F.silu(temb.float()).to(bf16), weight, bias).
+ */
+int vdn_adaln_tables(const void* temb, int temb_f32, int64_t t_st, int m, int64_t k,
+                     const void* w, const void* b, int64_t n, void* out, int64_t o_st,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

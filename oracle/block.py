@@ -141,7 +141,8 @@ class BlockOracle:
         gw, gb = w["soft_gate_w"][hs], w["soft_gate_b"][hs]
         small = bf16(x1 @ torch.cat((gw, w["beta_w"][hs], w["lgate_down_w"])).double().T)
         n = len(hs)
-        soft_gate = bf16(torch.sigmoid(bf16(small[:, :n] + gb.double())))
+        # the softmax gate is one Linear with bias (OutputGate.up): bias added before rounding
+        soft_gate = bf16(torch.sigmoid(bf16(x1 @ gw.double().T + gb.double())))
         beta = bf16(torch.sigmoid(small[:, n:2 * n]))
         up = bf16(small[:, 2 * n:] @ w["lgate_up_w"][cols].double().T
                   + w["lgate_up_b"][cols].double())

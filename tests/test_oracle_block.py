@@ -77,57 +77,56 @@ def _bf16(x):
     return float(r.reshape(-1)[0]) if np.ndim(x) == 0 else r
 
 
-def _tables_both(tensors, cfg, temb):
-    """AdaLN tables from the oracle and from the product's torch glue (CPU)."""
-    from vdn_amd.block import HybridDiTBlock
-    block = HybridDiTBlock(cfg, BlockWeights(tensors))
-    return ([t.double() for t in ob.BlockOracle(tensors, cfg).tables(temb)],
-            [t.double() for t in block.adaln_tables(temb)])
+def oracle_tables(tensors, cfg, temb):
+    """AdaLN tables of the oracle (float64 after each bf16 rounding)."""
+    return [t.double() for t in ob.BlockOracle(tensors, cfg).tables(temb)]
 
 
-def test_adaln_tables_closed_forms(small):
+def check_adaln_closed_forms(tables_of, w, cfg):
     """AdaLN tables = Linear(bf16(SiLU(temb in fp32))) in the order shift, scale, gate
     (attention), then shift, scale, gate (MLP) (paper_adaln.py:186, 205-212).
     temb = 0 gives SiLU = 0, so every table is its bias; a weight row that is one-hot at
-    column j gives bf16(SiLU(temb_j)) at exactly that row's table and position."""
-    w, _ = small
-    hd = SMALL.hidden
-    temb = torch.linspace(-3, 3, hd)[None]
-    for tables in _tables_both(w.tensors, SMALL, torch.zeros(1, hd)):
-        bias = w.adaln_b.double()
-        for c in range(6):
-            assert torch.equal(tables[c][0], bias[c * hd:(c + 1) * hd]), c
+    column j gives bf16(SiLU(temb_j)) at exactly that row's table and position.
+    `tables_of(tensors, temb)` returns the six tables as float64 CPU tensors."""
+    hd = cfg.hidden
+    temb = torch.linspace(-3, 3, hd)[None].to(torch.bfloat16).float()
+    tables = tables_of(w.tensors, torch.zeros(1, hd))
+    bias = w.adaln_b.double()
+    for c in range(6):
+        assert torch.equal(tables[c][0], bias[c * hd:(c + 1) * hd]), c
     tensors = dict(w.tensors)
     tensors["adaln_w"] = torch.zeros_like(w.adaln_w)
     tensors["adaln_b"] = torch.zeros_like(w.adaln_b)
     picks = {0: (3, 17), 1: (100, 200), 2: (5, 255), 3: (254, 0), 4: (77, 77), 5: (0, 128)}
     for c, (i, j) in picks.items():
         tensors["adaln_w"][c * hd + i, j] = 1.0
-    for tables in _tables_both(tensors, SMALL, temb):
-        for c, (i, j) in picks.items():
-            expect = torch.zeros(hd, dtype=torch.float64)
-            expect[i] = _bf16(_bf16(_silu(float(temb[0, j]))))
-            assert torch.equal(tables[c][0], expect), c
+    tables = tables_of(tensors, temb)
+    for c, (i, j) in picks.items():
+        expect = torch.zeros(hd, dtype=torch.float64)
+        expect[i] = _bf16(_bf16(_silu(float(temb[0, j]))))
+        assert torch.equal(tables[c][0], expect), c
 
 
-def _alpha_both(tensors, cfg, mean):
-    from vdn_amd.block import HybridDiTBlock
+def test_adaln_tables_closed_forms(small):
+    w, _ = small
+    check_adaln_closed_forms(lambda t, temb: oracle_tables(t, SMALL, temb), w, SMALL)
+
+
+def oracle_alpha(tensors, cfg, mean):
     from oracle import vda as ov
-    block = HybridDiTBlock(cfg, BlockWeights(tensors))
-    return (ov.frame_kda_alpha(mean, tensors["alpha_down_w"], tensors["alpha_up_w"],
-                               tensors["dt_bias"], tensors["a_log"], cfg.heads, cfg.head_dim),
-            block.frame_alpha(mean))
+    return ov.frame_kda_alpha(mean, tensors["alpha_down_w"], tensors["alpha_up_w"],
+                              tensors["dt_bias"], tensors["a_log"], cfg.heads, cfg.head_dim)
 
 
-def test_frame_alpha_closed_forms(small):
+def check_alpha_closed_forms(alpha_of, w, cfg):
     """FrameKDAAlpha (layers.py:29-34, 36-69): alpha = exp(-exp(A_log) softplus(up(down(m)) +
     dt_bias)). With zero down/up weights and the fla init dt_bias = dt + log(-expm1(-dt)),
     softplus(dt_bias) = dt exactly, so alpha = exp(-A dt) per head and channel. With
     A_log = 0, dt_bias = 0 and one-hot down/up rows routing frame-mean channel j to output
     (h, c), alpha(h, c) = exp(-softplus(m_j)) = 1 / (1 + e^m_j) and every other channel
-    is exp(-softplus(0)) = 1/2."""
-    w, _ = small
-    nh, d, hd = SMALL.heads, SMALL.head_dim, SMALL.hidden
+    is exp(-softplus(0)) = 1/2. `alpha_of(tensors, mean)` takes per-frame means [F, hidden]
+    (bf16 values) and returns alpha [F, heads, head_dim] fp32 on the CPU."""
+    nh, d, hd = cfg.heads, cfg.head_dim, cfg.hidden
     g = np.random.default_rng(7)
     a = g.uniform(1, 16, nh)
     dt = np.exp(g.uniform(np.log(1e-3), np.log(1e-1), nh * d))
@@ -136,32 +135,41 @@ def test_frame_alpha_closed_forms(small):
     tensors["alpha_up_w"] = torch.zeros_like(w.alpha_up_w)
     tensors["a_log"] = torch.tensor(np.log(a), dtype=torch.float32)
     tensors["dt_bias"] = torch.tensor(dt + np.log(-np.expm1(-dt)), dtype=torch.float32)
-    mean = torch.randn(3, hd)
+    mean = torch.randn(3, hd, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).float()
     expect = np.exp(-a[:, None] * dt.reshape(nh, d))[None].repeat(3, 0)
-    for alpha in _alpha_both(tensors, SMALL, mean):
-        assert alpha.shape == (3, nh, d) and alpha.dtype == torch.float32
-        np.testing.assert_allclose(alpha.numpy(), expect, rtol=3e-6)
+    alpha = alpha_of(tensors, mean)
+    assert alpha.shape == (3, nh, d) and alpha.dtype == torch.float32
+    np.testing.assert_allclose(alpha.numpy(), expect, rtol=3e-6)
     tensors["a_log"] = torch.zeros(nh)
     tensors["dt_bias"] = torch.zeros(nh * d)
     routes = [(11, 4, 1, 127), (200, 9, 0, 0)]      # (mean channel j, latent r, head, channel)
     for j, r, h, c in routes:
         tensors["alpha_down_w"][r, j] = 1.0
         tensors["alpha_up_w"][h * d + c, r] = 1.0
-    mean = torch.linspace(-4, 4, 3 * hd).reshape(3, hd)
+    mean = torch.linspace(-4, 4, 3 * hd).reshape(3, hd).to(torch.bfloat16).float()
     expect = np.full((3, nh, d), 0.5)
     for j, r, h, c in routes:
         expect[:, h, c] = 1.0 / (1.0 + np.exp(mean[:, j].double().numpy()))
-    for alpha in _alpha_both(tensors, SMALL, mean):
-        np.testing.assert_allclose(alpha.numpy(), expect, rtol=2e-6)
+    np.testing.assert_allclose(alpha_of(tensors, mean).numpy(), expect, rtol=2e-6)
 
 
-def test_gate_projections_closed_forms(small):
+def test_frame_alpha_closed_forms(small):
+    w, _ = small
+    check_alpha_closed_forms(lambda t, mean: oracle_alpha(t, SMALL, mean), w, SMALL)
+
+
+def oracle_gates(tensors, cfg, x1):
+    """(soft gate, beta, output gate) of the oracle for x1 [T, hidden] (float64)."""
+    return ob.BlockOracle(tensors, cfg).small_projections(x1)
+
+
+def check_gate_closed_forms(gates_of, w, cfg):
     """The softmax gate sigmoid(x Wg^T + b) per head, beta sigmoid(x Wb^T) and the output
     gate sigmoid(up(down x)) (attention_gates.py:52-55): zero weights give sigmoid(bias)
     (OutputGate's constant init: bias logit(p) gives p), beta 1/2; one-hot rows give
-    sigmoid(x_j + b) at exactly the routed head / channel."""
-    w, _ = small
-    nh, d, hd = SMALL.heads, SMALL.head_dim, SMALL.hidden
+    sigmoid(x_j + b) at exactly the routed head / channel. `gates_of(tensors, x1)` returns
+    float64 CPU tensors."""
+    nh, d, hd = cfg.heads, cfg.head_dim, cfg.hidden
     tensors = dict(w.tensors)
     for name in ("soft_gate_w", "beta_w", "lgate_down_w", "lgate_up_w"):
         tensors[name] = torch.zeros_like(w.tensors[name])
@@ -169,7 +177,7 @@ def test_gate_projections_closed_forms(small):
     tensors["soft_gate_b"] = torch.full((nh,), logit(0.99)).to(torch.bfloat16)
     tensors["lgate_up_b"] = torch.full((nh * d,), logit(0.9)).to(torch.bfloat16)
     x1 = torch.linspace(-2, 2, 5 * hd).reshape(5, hd).to(torch.bfloat16).double()
-    soft, beta, lin = ob.BlockOracle(tensors, SMALL).small_projections(x1)
+    soft, beta, lin = gates_of(tensors, x1)
     sig = lambda v: 1.0 / (1.0 + np.exp(-v))
     assert torch.equal(beta, torch.full((5, nh), 0.5, dtype=torch.float64))
     np.testing.assert_allclose(soft.numpy(), sig(_bf16(logit(0.99))), rtol=2 ** -8)
@@ -180,7 +188,7 @@ def test_gate_projections_closed_forms(small):
     tensors["beta_w"][0, 250] = 1.0
     tensors["lgate_down_w"][7, 3] = 1.0
     tensors["lgate_up_w"][1 * d + 5, 7] = 1.0
-    soft, beta, lin = ob.BlockOracle(tensors, SMALL).small_projections(x1)
+    soft, beta, lin = gates_of(tensors, x1)
     xs = x1.numpy()
     np.testing.assert_allclose(soft[:, 1].numpy(), sig(xs[:, 33]), rtol=2 ** -8)
     np.testing.assert_allclose(soft[:, 0].numpy(), 0.5)
@@ -188,6 +196,11 @@ def test_gate_projections_closed_forms(small):
     np.testing.assert_allclose(lin[:, d + 5].numpy(), sig(xs[:, 3]), rtol=2 ** -8)
     others = np.delete(lin.numpy(), d + 5, axis=1)
     np.testing.assert_allclose(others, 0.5)
+
+
+def test_gate_projections_closed_forms(small):
+    w, _ = small
+    check_gate_closed_forms(lambda t, x1: oracle_gates(t, SMALL, x1), w, SMALL)
 
 
 def test_prenorm_uses_tables_scale_then_shift(small):

@@ -61,6 +61,10 @@ SIGNATURES = {
     "vdn_vda_readout_gated": [_ptr, _i64, _i64, _i64, _i32, _ptr, _ptr, _i32, _f32, _ptr, _i64,
                               _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _ptr, _i64, _i32, _i32,
                               _i32, _i32, _ptr],
+    "vdn_gate_projection": [_ptr, _i64, _i64, _ptr, _i32, _i32, _i32, _ptr, _ptr, _ptr, _ptr,
+                            _ptr, _ptr],
+    "vdn_frame_alpha": [_ptr, _i32, _i32, _ptr, _ptr, _ptr, _i32, _i32, _ptr, _ptr],
+    "vdn_adaln_tables": [_ptr, _i32, _i64, _i32, _i64, _ptr, _ptr, _i64, _ptr, _i64, _ptr],
 }
 
 _LOCK = threading.Lock()

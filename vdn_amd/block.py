@@ -10,6 +10,8 @@ tables; src/inference/utils/lora.py:80-107 LoRA merge):
   qkv    = MXFP8 GEMM(q1, W_qkv + B_lora A_lora)                                  [T, 3H]
   gates  = sigmoid(softmax_gate(x1)), beta = sigmoid(beta_proj(x1)),
            lin_gate = sigmoid(up(down(x1))), alpha = FrameKDAAlpha(frame mean of x1)
+           (one bf16 MFMA pass over x1 for the gate, beta, down and alpha-down columns,
+           vdn_gate_projection; the alpha MLP on per-frame column sums, vdn_frame_alpha)
   soft   = window attention(QK-RMSNorm + 3D RoPE(q, k), v) * gate                 [T, H]
   far    = VDA(raw q, k, v, beta, lin_gate, alpha)                                [T, H]
   h      = h + gate_msa * [O | O_lin]([soft | far])          one K = 2H GEMM, residual fused
@@ -30,9 +32,102 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from . import _lib
 from . import mxfp8 as mx
 from . import vda as vv
 from . import window as vw
+
+GATE_GROUP = 64      # softmax-gate / beta columns of the gate projection (heads <= 64)
+GATE_ROWS = 128      # rows per gate-projection workgroup (per-frame partial sums)
+
+
+def gate_weight(w: "BlockWeights", cfg: "BlockConfig") -> torch.Tensor:
+    """[384, hidden] bf16 operand of vdn_gate_projection: softmax-gate rows, beta rows (each
+    group zero-padded to 64), output-gate down (128) and FrameKDAAlpha down (128)."""
+    if cfg.heads > GATE_GROUP or cfg.heads % 2 or cfg.head_dim != 128 or cfg.hidden % 32:
+        raise NotImplementedError("the gate projection needs an even head count <= 64, "
+                                  "head_dim 128 and hidden % 32 == 0")
+    out = torch.zeros(2 * GATE_GROUP + 256, cfg.hidden, dtype=torch.bfloat16,
+                      device=w.soft_gate_w.device)
+    out[:cfg.heads] = w.soft_gate_w
+    out[GATE_GROUP:GATE_GROUP + cfg.heads] = w.beta_w
+    out[2 * GATE_GROUP:2 * GATE_GROUP + 128] = w.lgate_down_w
+    out[2 * GATE_GROUP + 128:] = w.alpha_down_w
+    return out
+
+
+def gate_projection(x1, weight, gate_bias, heads, frames, spatial):
+    """soft_gate [T, heads], beta [T, heads], gate_down [T, 128] (bf16) and the per-frame
+    column sums of x1 @ alpha_down^T [frames * ceil(spatial / 128), 128] (fp32) of x1
+    [frames * spatial, hidden] bf16 (attention_gates.py:52-55, tensor_parallel.py:194-198)."""
+    t, hd = x1.shape
+    for name, ten in (("x1", x1), ("weight", weight), ("gate_bias", gate_bias)):
+        _lib.require_gpu(ten, name)
+        if ten.dtype != torch.bfloat16 or ten.device != x1.device:
+            raise ValueError(f"{name} must be bf16 on the device of x1")
+    if t != frames * spatial or x1.stride(1) != 1:
+        raise ValueError("x1 must be [frames * spatial, hidden] with unit column stride")
+    if weight.shape != (2 * GATE_GROUP + 256, hd) or not weight.is_contiguous():
+        raise ValueError("weight must be the contiguous [384, hidden] gate_weight operand")
+    if gate_bias.numel() < heads or not gate_bias.is_contiguous():
+        raise ValueError("gate_bias must be contiguous with heads entries")
+    dev = x1.device
+    soft = torch.empty(t, heads, dtype=torch.bfloat16, device=dev)
+    beta = torch.empty(t, heads, dtype=torch.bfloat16, device=dev)
+    down = torch.empty(t, 128, dtype=torch.bfloat16, device=dev)
+    bpf = -(-spatial // GATE_ROWS)
+    partial = torch.empty(frames * bpf, 128, dtype=torch.float32, device=dev)
+    _lib.call("vdn_gate_projection", x1.data_ptr(), x1.stride(0), hd, weight.data_ptr(), heads,
+              frames, spatial, gate_bias.data_ptr(), soft.data_ptr(), beta.data_ptr(),
+              down.data_ptr(), partial.data_ptr(), _lib.stream(dev))
+    return soft, beta, down, partial
+
+
+def frame_alpha(partial, frames, spatial, up_w, dt_bias, a_log, heads, head_dim):
+    """FrameKDAAlpha (layers.py:36-69) from the gate projection's per-frame sums: alpha
+    [frames, heads, head_dim] fp32 = exp(-exp(A_log) softplus(up(mean) + dt_bias))."""
+    for name, t, dt in (("partial", partial, torch.float32), ("up_w", up_w, torch.bfloat16),
+                        ("dt_bias", dt_bias, torch.float32), ("a_log", a_log, torch.float32)):
+        _lib.require_gpu(t, name)
+        if t.dtype != dt or not t.is_contiguous() or t.device != partial.device:
+            raise ValueError(f"{name} must be contiguous {dt} on the device of partial")
+    if partial.shape != (frames * -(-spatial // GATE_ROWS), 128):
+        raise ValueError("partial must be the gate projection's [frames * blocks, 128] sums")
+    if dt_bias.numel() != heads * head_dim or a_log.numel() != heads:
+        raise ValueError("dt_bias must have heads * head_dim entries and a_log heads")
+    if up_w.shape != (heads * head_dim, 128):
+        raise ValueError("up_w must be [heads * head_dim, 128]")
+    alpha = torch.empty(frames, heads, head_dim, dtype=torch.float32, device=partial.device)
+    _lib.call("vdn_frame_alpha", partial.data_ptr(), frames, spatial, up_w.data_ptr(),
+              dt_bias.data_ptr(), a_log.data_ptr(), heads, head_dim, alpha.data_ptr(),
+              _lib.stream(partial.device))
+    return alpha
+
+
+def adaln_tables(temb, weight, bias, hidden):
+    """Six [m, hidden] bf16 tables Linear(bf16(SiLU(temb in fp32)), weight, bias) in the order
+    shift, scale, gate (attention), shift, scale, gate (MLP) (paper_adaln.py:174-188); temb
+    bf16 or fp32."""
+    if temb.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("temb must be bf16 or fp32")
+    _lib.require_gpu(temb, "temb")
+    for name, t in (("weight", weight),) + ((("bias", bias),) if bias is not None else ()):
+        _lib.require_gpu(t, name)
+        if t.dtype != torch.bfloat16 or t.device != temb.device:
+            raise ValueError(f"{name} must be bf16 on the device of temb")
+    if temb.dim() != 2 or temb.stride(1) != 1:
+        raise ValueError("temb must be [m, hidden] with unit column stride")
+    if weight.shape != (6 * hidden, temb.shape[1]) or not weight.is_contiguous():
+        raise ValueError("weight must be contiguous [6 * hidden, hidden]")
+    if bias is not None and (bias.numel() != 6 * hidden or not bias.is_contiguous()):
+        raise ValueError("bias must be contiguous with 6 * hidden entries")
+    m = temb.shape[0]
+    out = torch.empty(m, 6 * hidden, dtype=torch.bfloat16, device=temb.device)
+    _lib.call("vdn_adaln_tables", temb.data_ptr(), int(temb.dtype == torch.float32),
+              temb.stride(0), m, temb.shape[1],
+              weight.data_ptr(), bias.data_ptr() if bias is not None else None, 6 * hidden,
+              out.data_ptr(), out.stride(0), _lib.stream(temb.device))
+    return out.chunk(6, dim=-1)
 
 
 @dataclass(frozen=True)
@@ -154,13 +249,14 @@ class HybridDiTBlock(nn.Module):
         else:
             self.up = mk(w.up_w, w.up_b)
         self.down = mk(w.down_w, w.down_b)
-        # small bf16 projections of the attention input, one GEMM: softmax gate | beta | gate down
-        self.small_w = torch.cat((w.soft_gate_w, w.beta_w, w.lgate_down_w))
+        # softmax gate | beta | output-gate down | alpha down: one pass over x1
+        self.gate_w = gate_weight(w, cfg)
         self.keep = {k: w.tensors[k] for k in (
             "adaln_w", "adaln_b", "norm1", "norm2", "norm3", "norm_q", "norm_k", "soft_gate_b",
             "lgate_up_w", "lgate_up_b", "alpha_down_w", "alpha_up_w", "a_log", "dt_bias",
             "vda_norm", "norm_qc", "norm_kc")}
         self._zero_table = None
+        self._zero_idx = None
         self._side = None
         # The VDA branch runs on a side stream beside RoPE + window attention; False runs it
         # after them on the caller's stream (same kernels, same outputs), which gives each
@@ -171,15 +267,9 @@ class HybridDiTBlock(nn.Module):
     def adaln_tables(self, temb):
         """6 tables [1, H]: shift/scale/gate attention, then MLP (paper_adaln.py:174-188, 205-212)."""
         k = self.keep
-        projected = F.linear(F.silu(temb.float()).to(k["adaln_w"].dtype), k["adaln_w"], k["adaln_b"])
-        return projected.view(-1, 6 * self.cfg.hidden).chunk(6, dim=-1)
-
-    def frame_alpha(self, frame_mean):
-        k, cfg = self.keep, self.cfg
-        delta = F.linear(F.linear(frame_mean.float(), k["alpha_down_w"].float()),
-                         k["alpha_up_w"].float()) + k["dt_bias"]
-        scale = torch.exp(k["a_log"])[:, None]
-        return torch.exp(-scale * F.softplus(delta.view(-1, cfg.heads, cfg.head_dim))).contiguous()
+        if temb.dtype != torch.float32:
+            temb = temb.to(torch.bfloat16)   # SiLU runs in fp32 on either
+        return adaln_tables(temb, k["adaln_w"], k["adaln_b"], self.cfg.hidden)
 
     def _side_stream(self, device):
         """One side stream per device, default priority."""
@@ -191,6 +281,13 @@ class HybridDiTBlock(nn.Module):
         if self._zero_table is None or self._zero_table.device != device:
             self._zero_table = torch.zeros(1, self.cfg.hidden, dtype=torch.bfloat16, device=device)
         return self._zero_table
+
+    def _table_index(self, rows, device):
+        """Row -> table index (all rows use table 0), kept between calls."""
+        z = self._zero_idx
+        if z is None or z.device != device or z.shape[0] < rows:
+            self._zero_idx = z = torch.zeros(rows, dtype=torch.long, device=device)
+        return z[:rows]
 
     # --------------------------------------------------------------- forward ----
     @torch.no_grad()
@@ -207,7 +304,7 @@ class HybridDiTBlock(nn.Module):
         frames, spatial = layout.num_frames, layout.tokens_per_frame
         dev = hidden.device
         shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = self.adaln_tables(temb)
-        idx = torch.zeros(T, dtype=torch.long, device=dev)
+        idx = self._table_index(T, dev)
         parts = {} if return_parts else None
 
         def snap(name, t):
@@ -224,13 +321,13 @@ class HybridDiTBlock(nn.Module):
         raw_q = qkv[:, :inner].view(T, heads, d)
         raw_k = qkv[:, inner:2 * inner].view(T, heads, d)
         value = qkv[:, 2 * inner:].view(T, heads, d)
-        small = F.linear(x1, self.small_w)
-        soft_gate = torch.sigmoid(small[:, :heads] + k["soft_gate_b"])
-        beta = torch.sigmoid(small[:, heads:2 * heads])
+        soft_gate, beta, gate_down, partial = gate_projection(
+            x1, self.gate_w, k["soft_gate_b"], heads, frames, spatial)
         # the low-rank gate sigmoid(up(down(x1))) is formed inside the VDA readout
-        lin_gate = vv.OutputGateProjection(small[:, 2 * heads:], k["lgate_up_w"], k["lgate_up_b"])
-        frame_mean = x1.view(frames, spatial, hd).mean(1, dtype=torch.float32)
-        alpha = self.frame_alpha(frame_mean)
+        lin_gate = vv.OutputGateProjection(gate_down, k["lgate_up_w"], k["lgate_up_b"])
+        alpha = frame_alpha(partial, frames, spatial, k["alpha_up_w"], k["dt_bias"], k["a_log"],
+                            heads, d)
+        del partial
         cos, sin = rope
         # The two branch outputs are the two halves of the [O | O_lin] operand. The kernels
         # quantize them in their epilogues straight into the MXFP8 operand (chunks 0..H-1 for
@@ -254,7 +351,7 @@ class HybridDiTBlock(nn.Module):
                 side.wait_stream(main)
                 with torch.cuda.stream(side):
                     linear_branch()
-                for t in (qkv, small, beta, alpha, qb, sb):
+                for t in (qkv, gate_down, beta, alpha, qb, sb):
                     t.record_stream(side)
             q, kk = vw.paper_qk_rmsnorm_rope(raw_q, raw_k, k["norm_q"], k["norm_k"], cfg.eps,
                                              cos, sin, enabled=True)
@@ -279,7 +376,7 @@ class HybridDiTBlock(nn.Module):
             snap("far", both[:, inner:])
             qb, sb = mx.launch_quantize(both)
             del both
-        del qkv, raw_q, raw_k, value, lin_gate
+        del qkv, raw_q, raw_k, value, lin_gate, gate_down
         # the first residual update writes a fresh tensor (no copy of the input)
         h = torch.empty_like(hidden)
         self.o_cat.forward_quantized(qb, sb, rows=T, out=h, residual=hidden, gate=gate_msa)
