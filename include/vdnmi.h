@@ -265,7 +265,7 @@ int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64_t q_sd,
                         void* stream);
 
 /*
- * Exact softmax attention of query blocks over key intervals (head_dim 128, bf16):
+ * Exact softmax attention of query blocks over key intervals (bf16, head_dim 64, 128 or 256):
  * blocks int32 [nblocks, 3] = (first query, end of its query range, group), <= 256 queries
  * each; grp_kv int32 [groups, 8, 2] key intervals [a, b); grp_n int32 [groups].
  * q, k, v addressed by (token, head) strides with unit channel stride. gate (nullable): bf16
@@ -277,9 +277,9 @@ int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64_t q_sd,
 int vdn_window_attention(const void* q, int64_t q_st, int64_t q_sh, const void* k, int64_t k_st,
                          int64_t k_sh, const void* v, int64_t v_st, int64_t v_sh,
                          const int* blocks, int nblocks, const int* grp_kv, const int* grp_n,
-                         int heads, float scale, const void* gate, int64_t g_st, int64_t g_sh,
-                         void* out, int64_t o_st, int64_t o_sh, float* lse, int64_t l_st,
-                         int64_t l_sh, void* stream);
+                         int heads, int head_dim, float scale, const void* gate, int64_t g_st,
+                         int64_t g_sh, void* out, int64_t o_st, int64_t o_sh, float* lse,
+                         int64_t l_st, int64_t l_sh, void* stream);
 
 /* vdn_window_attention with the output quantized in the epilogue instead of stored as bf16:
  * query row q, head h -> MXFP8 codes[q, 128 (chunk0 + h) .. +128) of a [rows, kp] code

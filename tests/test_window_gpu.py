@@ -271,3 +271,66 @@ def test_mxfp8_output_rejects_bad_destinations(device):
     with pytest.raises(ValueError, match="excludes"):
         vw.paper_window_attention(q, q, q, plan, enabled=True, return_lse=True,
                                   out_mxfp8=(codes, scales, 0))
+
+
+@pytest.mark.parametrize("d", [64, 256])
+@pytest.mark.parametrize("before,after,frames,chunk,radius,anchor",
+                         [(3, 4, 7, 3, 1, "both"), (0, 0, 7, 0, 99, "none"),
+                          (3, 0, 2, 5, 1, "rows"), (0, 4, 1, 0, 0, "columns")])
+@torch.no_grad()
+def test_other_head_dims_dense_fp32_oracle(device, d, before, after, frames, chunk, radius,
+                                           anchor):
+    """head_dim 64 and 256 (paper_window.py:204 accepts 64, 128, 256) against the dense fp32
+    oracle at the reference test's tolerances; strided Q/K/V views, global rows, anchors."""
+    torch.manual_seed(820 + d)
+    layout = vw.SequenceLayout(before + frames * 3 + after, before, frames, 3)
+    bounds = vw.window_bounds(frames, radius, chunk)
+    backing = torch.randn(layout.seq_len + 5, 3, 9, d, device=device, dtype=torch.bfloat16)
+    q, k, v = [backing[:, i, 2:7] for i in range(3)]
+    plan = vw.prepare_paper_window_plan(layout, bounds, anchor, device=device)
+    out, lse = vw.paper_window_attention(q, k, v, plan, enabled=True, return_lse=True)
+    s = layout.seq_len
+    mask = ow.dense_mask(s, before, frames, 3, bounds, anchor)
+    expected, el = ow.attention_dense(q[:s].cpu(), k[:s].cpu(), v[:s].cpu(), mask, d ** -.5)
+    got = out[:s].float().cpu()
+    assert out.shape == q.shape
+    torch.testing.assert_close(got, expected, atol=.009, rtol=.015)
+    assert ((got - expected).norm() / expected.norm()) < .004
+    torch.testing.assert_close(lse[:s].cpu(), el, atol=3e-5, rtol=3e-6)
+    assert out[s:].count_nonzero() == 0
+
+
+@pytest.mark.parametrize("d", [64, 256])
+@torch.no_grad()
+def test_other_head_dims_partial_blocks_tails_and_gate(device, d):
+    """300-token frames: 44-row last query blocks, key intervals ending inside a tile (tiles
+    of 128 keys for d = 64, 64 for d = 256); the fused gate against the separate product."""
+    torch.manual_seed(32 + d)
+    frames, spatial = 3, 300
+    layout = vw.SequenceLayout(frames * spatial, 0, frames, spatial)
+    bounds = vw.window_bounds(frames, 1)
+    q, k, v = [torch.randn(layout.seq_len, 2, d, device=device, dtype=torch.bfloat16)
+               for _ in range(3)]
+    plan = vw.prepare_paper_window_plan(layout, bounds, device=device)
+    out, lse = vw.paper_window_attention(q, k, v, plan, enabled=True, return_lse=True)
+    mask = ow.dense_mask(layout.seq_len, 0, frames, spatial, bounds, "none")
+    expected, el = ow.attention_dense(q.cpu(), k.cpu(), v.cpu(), mask, d ** -.5)
+    torch.testing.assert_close(out.float().cpu(), expected, atol=.009, rtol=.015)
+    torch.testing.assert_close(lse.cpu(), el, atol=3e-5, rtol=3e-6)
+    gate = torch.rand(layout.seq_len, 2, device=device).to(torch.bfloat16)
+    gated = vw.paper_window_attention(q, k, v, plan, enabled=True, gate=gate)
+    assert torch.equal(gated, (out.float() * gate[..., None].float()).to(torch.bfloat16))
+
+
+@torch.no_grad()
+def test_other_head_dims_reject_mxfp8_output(device):
+    from vdn_amd import mxfp8 as vm
+    layout = vw.SequenceLayout(6, 0, 2, 3)
+    plan = vw.prepare_paper_window_plan(layout, vw.window_bounds(2, 1), device=device)
+    q = torch.randn(6, 2, 64, device=device, dtype=torch.bfloat16)
+    codes, scales = vm.empty_activation(6, 256, device)
+    with pytest.raises(ValueError, match="head_dim 128"):
+        vw.paper_window_attention(q, q, q, plan, enabled=True, out_mxfp8=(codes, scales, 0))
+    with pytest.raises(ValueError):
+        bad = torch.randn(6, 2, 96, device=device, dtype=torch.bfloat16)
+        vw.paper_window_attention(bad, bad, bad, plan, enabled=True)

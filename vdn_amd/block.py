@@ -441,8 +441,8 @@ def cross_attention(q, k, v, plan: vw.DevicePlan, scale, out_mxfp8=None):
     _lib.call("vdn_window_attention", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
               k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
               plan.blocks.data_ptr(), plan.nblocks, plan.intervals.data_ptr(),
-              plan.counts.data_ptr(), h, float(scale), None, 0, 0, out.data_ptr(), out.stride(0),
-              out.stride(1), None, 0, 0, _lib.stream(q.device))
+              plan.counts.data_ptr(), h, d, float(scale), None, 0, 0, out.data_ptr(),
+              out.stride(0), out.stride(1), None, 0, 0, _lib.stream(q.device))
     return out
 
 

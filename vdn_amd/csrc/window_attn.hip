@@ -28,9 +28,6 @@
 namespace vdn {
 namespace {
 
-constexpr int kD = 128;
-constexpr int kBN = 128;
-constexpr int kKT = kBN / 32;  // 32-key score accumulators per tile
 constexpr int kMaxIntervals = 8;
 constexpr int kBlockWaves = 8;  // queries per block = 32 * kBlockWaves (must match the plan)
 constexpr float kLog2e = 1.4426950408889634f;
@@ -59,8 +56,19 @@ __device__ __forceinline__ bf16x4_t lds_read_tr(const uint16_t* p) {
       (lds_bf16x4_t*)((__attribute__((address_space(3))) char*)(p)));
 }
 
-__device__ __forceinline__ int swz_k(int row) { return row & 15; }
-__device__ __forceinline__ int swz_v(int row) { return 4 * (row & 3); }
+// Key tile of each head_dim: 128 keys, 64 for D = 256 (whose Q and O fragments take 192
+// registers; the tile buffers then still hold the epilogue's 256 x 256 output block).
+template <int D>
+constexpr int tile_keys() { return D == 256 ? 64 : 128; }
+
+// 16-byte chunk c of tile row r is stored at c ^ swz(r). K rows are read 16 rows per LDS cycle
+// (one chunk each), V rows by the transpose reads 4 rows x 4 chunks per 32 lanes; a 256-byte
+// bank window holds 256 / (2 D) rows, and the XOR spreads each read set over all of its 16
+// chunk positions (D = 64: two rows per window).
+template <int D>
+__device__ __forceinline__ int swz_k(int row) { return D == 64 ? (row >> 1) & 7 : row & 15; }
+template <int D>
+__device__ __forceinline__ int swz_v(int row) { return D == 64 ? 4 * ((row >> 1) & 1) : 4 * (row & 3); }
 
 // MXFP8 destination of the output (instead of bf16 rows): codes [rows, kp] and
 // SWIZZLE_32_4_4 scales; head h of query row q fills 128-column chunk chunk0 + h, exactly
@@ -80,14 +88,19 @@ struct Layout {
 };
 
 // kWaves waves of 32 queries each: a workgroup owns kBM = 32 kWaves queries, and every K/V
-// tile it loads serves all of them.
-template <int kWaves, bool kMx>
+// tile it loads serves all of them. kD is the head dimension (64, 128 or 256).
+template <int kD, int kWaves, bool kMx>
 __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restrict__ grp_kv,
                    const int* __restrict__ grp_n, int nblocks, int heads, float scale_log2,
                    const uint16_t* __restrict__ gate, int64_t g_st, int64_t g_sh,
                    uint16_t* __restrict__ out, int64_t o_st, int64_t o_sh,
                    float* __restrict__ lse, int64_t l_st, int64_t l_sh, MxDst mx) {
+  constexpr int kBN = tile_keys<kD>();
+  constexpr int kKT = kBN / 32;       // 32-key score accumulators per tile
+  constexpr int kChunks = kD / 8;     // 16-byte chunks per tile row
+  constexpr int kSegRows = 64 / kChunks;  // rows per 1 KB DMA segment (one wave instruction)
+  static_assert(!kMx || kD == 128, "the MXFP8 destination holds one head per 128 columns");
   // Separate arrays per buffer: with distinct LDS objects the compiler can tell a tile
   // prefetch into one buffer from reads of the other and does not wait on the prefetch.
   __shared__ __attribute__((aligned(1024))) uint16_t sK0[kBN * kD];
@@ -96,8 +109,8 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
   __shared__ __attribute__((aligned(1024))) uint16_t sV1[kBN * kD];
   constexpr int kBM = 32 * kWaves;
   constexpr int kThreads = 64 * kWaves;
-  constexpr int kSegs = kBN / 4 / kWaves;  // 1 KB (4-row) segments per tensor per wave
-  static_assert(kSegs * kWaves * 4 == kBN && kWaves % 4 == 0, "segment mapping");
+  constexpr int kSegs = kBN / kSegRows / kWaves;  // 1 KB segments per tensor per wave
+  static_assert(kSegs * kWaves * kSegRows == kBN && kWaves % 4 == 0, "segment mapping");
   static_assert(kBM * kD <= 4 * kBN * kD, "the epilogue stages the block in the tile buffers");
 
   // ---- work item: (head, query block); consecutive ids of a head land on one XCD ----
@@ -128,31 +141,31 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
   // waves without a live query still load their share of every tile and meet every barrier,
   // but skip the arithmetic, so the live waves of their SIMDs run at the full MFMA rate.
   const bool wave_live = q0 + wave * 32 < q1;
-  bf16x8 qf[8];
+  bf16x8 qf[kD / 16];
   {
     const uint16_t* src = in.q + static_cast<int64_t>(q_live ? my_q : q0) * in.q_st + h * in.q_sh;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
+    for (int ks = 0; ks < kD / 16; ++ks) {
       const u32x4 w = *reinterpret_cast<const u32x4*>(src + 16 * ks + 8 * g);
       qf[ks] = __builtin_bit_cast(bf16x8, w);
     }
   }
 
-  // lane's share of a tile load: 4 x 1 KB segments (4 rows each) per tensor per wave. The
-  // per-lane byte offsets within a tile are fixed; a tile adds a wave-uniform base, so the
-  // loads take the scalar-base + 32-bit-offset form with no per-tile vector address math.
-  const int seg_row = lane >> 4, phys = lane & 15;
+  // lane's share of a tile load: kSegs 1 KB segments (kSegRows rows each) per tensor per
+  // wave. The per-lane byte offsets within a tile are fixed; a tile adds a wave-uniform base,
+  // so the loads take the scalar-base + 32-bit-offset form with no per-tile vector address math.
+  const int seg_row = lane / kChunks, phys = lane % kChunks;
   uint32_t koff[kSegs], voff[kSegs];
 #pragma unroll
   for (int j = 0; j < kSegs; ++j) {
-    const int row = (j * kWaves + wave) * 4 + seg_row;
-    koff[j] = static_cast<uint32_t>(row * in.k_st * 2 + 16 * (phys ^ swz_k(row)));
-    voff[j] = static_cast<uint32_t>(row * in.v_st * 2 + 16 * (phys ^ swz_v(row)));
+    const int row = (j * kWaves + wave) * kSegRows + seg_row;
+    koff[j] = static_cast<uint32_t>(row * in.k_st * 2 + 16 * (phys ^ swz_k<kD>(row)));
+    voff[j] = static_cast<uint32_t>(row * in.v_st * 2 + 16 * (phys ^ swz_v<kD>(row)));
   }
   const char* k_head = reinterpret_cast<const char*>(in.k + h * in.k_sh);
   const char* v_head = reinterpret_cast<const char*>(in.v + h * in.v_sh);
   // Buffer resources based at the tile's first key row (wave-uniform); the per-lane offsets
-  // stay below 128 rows x stride (the host bounds the strides).
+  // stay below kBN rows x stride (the host bounds the strides).
   auto issue_tile = [&](int a, int b, uint16_t* dk, uint16_t* dv) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t k_rsrc = tile_rsrc(k_head + static_cast<int64_t>(a) * in.k_st * 2);
     const __amdgpu_buffer_rsrc_t v_rsrc = tile_rsrc(v_head + static_cast<int64_t>(a) * in.v_st * 2);
@@ -160,26 +173,27 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
 #pragma unroll
       for (int j = 0; j < kSegs; ++j) {
         const int seg = j * kWaves + wave;
-        load_to_lds16(k_rsrc, koff[j], 0, dk + seg * 4 * kD);
-        load_to_lds16(v_rsrc, voff[j], 0, dv + seg * 4 * kD);
+        load_to_lds16(k_rsrc, koff[j], 0, dk + seg * kSegRows * kD);
+        load_to_lds16(v_rsrc, voff[j], 0, dv + seg * kSegRows * kD);
       }
     } else {  // tail tile: rows past the interval end repeat its last key
 #pragma unroll
       for (int j = 0; j < kSegs; ++j) {
         const int seg = j * kWaves + wave;
-        const int row = seg * 4 + seg_row;
+        const int row = seg * kSegRows + seg_row;
         const int r = min(row, b - a - 1);
-        const uint32_t ko = static_cast<uint32_t>(r * in.k_st * 2 + 16 * (phys ^ swz_k(row)));
-        const uint32_t vo = static_cast<uint32_t>(r * in.v_st * 2 + 16 * (phys ^ swz_v(row)));
-        load_to_lds16(k_rsrc, ko, 0, dk + seg * 4 * kD);
-        load_to_lds16(v_rsrc, vo, 0, dv + seg * 4 * kD);
+        const uint32_t ko = static_cast<uint32_t>(r * in.k_st * 2 + 16 * (phys ^ swz_k<kD>(row)));
+        const uint32_t vo = static_cast<uint32_t>(r * in.v_st * 2 + 16 * (phys ^ swz_v<kD>(row)));
+        load_to_lds16(k_rsrc, ko, 0, dk + seg * kSegRows * kD);
+        load_to_lds16(v_rsrc, vo, 0, dv + seg * kSegRows * kD);
       }
     }
   };
 
-  f32x16 o[4];
+  constexpr int kDB = kD / 32;  // 32-channel output accumulators
+  f32x16 o[kDB];
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+  for (int db = 0; db < kDB; ++db)
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
   float m = -INFINITY, l = 0.f;
@@ -209,7 +223,7 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     const int a = a0 + t * kBN, b = min(a + kBN, b0);
     if (!wave_live) return;
 
-    // ---- Sᵀ = K Qᵀ for the tile's 64 keys (two 32-key accumulators) ----
+    // ---- Sᵀ = K Qᵀ for the tile's kBN keys (kKT 32-key accumulators) ----
     f32x16 s[kKT];
 #pragma unroll
     for (int kt = 0; kt < kKT; ++kt) {
@@ -217,8 +231,8 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
       for (int v = 0; v < 16; ++v) s[kt][v] = 0.f;
       const int row = kt * 32 + col;
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        const int chunk = (2 * ks + g) ^ swz_k(row);
+      for (int ks = 0; ks < kD / 16; ++ks) {
+        const int chunk = (2 * ks + g) ^ swz_k<kD>(row);
         const bf16x8 ka = *reinterpret_cast<const bf16x8*>(tk + row * kD + chunk * 8);
         s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[ks], s[kt], 0, 0, 0);
       }
@@ -245,7 +259,7 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
       const float corr = __builtin_amdgcn_exp2f(m - m_new);
       l *= corr;
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+      for (int db = 0; db < kDB; ++db)
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[db][v] *= corr;
       m = m_new;
@@ -269,18 +283,18 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
 #pragma unroll
       for (int j = 0; j < 8; ++j) pb[j] = static_cast<__bf16>(s[c >> 1][(c & 1) * 8 + j]);
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
+      for (int db = 0; db < kDB; ++db) {
         bf16x4_t lo, hi;
         {
           const int row = 16 * c + tr_row;
           const int e = 32 * db + tr_col;
-          const int chunk = (e >> 3) ^ swz_v(row);
+          const int chunk = (e >> 3) ^ swz_v<kD>(row);
           lo = lds_read_tr(tv + row * kD + chunk * 8 + (e & 7));
         }
         {
           const int row = 16 * c + 8 + tr_row;
           const int e = 32 * db + tr_col;
-          const int chunk = (e >> 3) ^ swz_v(row);
+          const int chunk = (e >> 3) ^ swz_v<kD>(row);
           hi = lds_read_tr(tv + row * kD + chunk * 8 + (e & 7));
         }
         const bf16x8 va{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -289,7 +303,7 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     }
   };
   // ---- key intervals of the group, one after another ----
-  // Each interval is a contiguous key range walked in 64-key tiles; its bounds are read
+  // Each interval is a contiguous key range walked in kBN-key tiles; its bounds are read
   // before its first tile load, so the tile loop itself reads no memory besides the tiles.
   // The online softmax state carries over from one interval to the next.
   for (int i = 0; i < nint; ++i) {
@@ -308,7 +322,7 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
 
   // ---- epilogue: O / l, optional gate, through LDS to coalesced rows ----
   const float inv_l = l > 0.f ? 1.0f / l : 0.f;
-  // [kBM queries][128 channels] bf16 staged across the tile buffers, 64 queries per buffer
+  // [kBM queries][kD channels] bf16 staged across the tile buffers, kBN queries per buffer
   auto stage_rows = [&](int r) -> uint16_t* {
     const int which = r / kBN;  // uniform per wave for both uses below
     return which == 0 ? sK0 : which == 1 ? sK1 : which == 2 ? sV0 : sV1;
@@ -318,7 +332,7 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
   float gv = 1.f;
   if (gate != nullptr && q_live) gv = bf16_bits_to_f32(gate[static_cast<int64_t>(my_q) * g_st + h * g_sh]);
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+  for (int db = 0; db < kDB; ++db)
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int d = 32 * db + (v >> 2) * 8 + g * 4 + (v & 3);
@@ -329,11 +343,11 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
   if (lse != nullptr && q_live && g == 0)
     lse[static_cast<int64_t>(my_q) * l_st + h * l_sh] = (m + log2f(l)) * kLn2;
   __syncthreads();
-  // 16 lanes write one query row (256 bytes, or its 128 MXFP8 codes and 4 scales)
-  for (int r = tid >> 4; r < kBM; r += kThreads / 16) {
+  // kChunks lanes write one query row (2 kD bytes, or its 128 MXFP8 codes and 4 scales)
+  for (int r = tid / kChunks; r < kBM; r += kThreads / kChunks) {
     const int q = q0 + r;
-    if (q >= q1) continue;  // uniform per 16-lane group
-    const int c8 = (tid & 15) * 8;
+    if (q >= q1) continue;  // uniform per kChunks-lane group
+    const int c8 = (tid % kChunks) * 8;
     const uint16_t* src = stage_rows(r);
     const u32x4 row8 = *reinterpret_cast<const u32x4*>(&src[(r % kBN) * kD + c8]);
     if constexpr (kMx) {
@@ -365,13 +379,17 @@ namespace {
 int launch_window(const char* name, const void* q, int64_t q_st, int64_t q_sh, const void* k,
                   int64_t k_st, int64_t k_sh, const void* v, int64_t v_st, int64_t v_sh,
                   const int* blocks, int nblocks, const int* grp_kv, const int* grp_n, int heads,
-                  float scale, const void* gate, int64_t g_st, int64_t g_sh, void* out,
-                  int64_t o_st, int64_t o_sh, float* lse, int64_t l_st, int64_t l_sh,
+                  int head_dim, float scale, const void* gate, int64_t g_st, int64_t g_sh,
+                  void* out, int64_t o_st, int64_t o_sh, float* lse, int64_t l_st, int64_t l_sh,
                   const MxDst* mx, void* stream) {
   if (q == nullptr || k == nullptr || v == nullptr || blocks == nullptr || grp_kv == nullptr ||
       grp_n == nullptr || (mx == nullptr && out == nullptr))
     return set_error(kInvalidArgument, "%s: null pointer", name);
   if (heads <= 0 || nblocks < 0) return set_error(kInvalidArgument, "%s: bad geometry", name);
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return set_error(kInvalidArgument, "%s: head_dim must be 64, 128 or 256", name);
+  if (mx != nullptr && head_dim != 128)
+    return set_error(kUnsupported, "%s: the MXFP8 output takes head_dim 128", name);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || q_st % 8 || q_sh % 8 || k_st % 8 ||
       k_sh % 8 || v_st % 8 || v_sh % 8 ||
       (mx == nullptr && (!aligned16(out) || o_st % 8 || o_sh % 8)))
@@ -396,17 +414,25 @@ int launch_window(const char* name, const void* q, int64_t q_st, int64_t q_sh, c
   if (total > (1ll << 31) - 1) return set_error(kUnsupported, "%s: too many blocks", name);
   const dim3 grid(static_cast<unsigned>(total)), block(kBlockWaves * 64);
   const auto st = static_cast<hipStream_t>(stream);
+  const auto* g16 = static_cast<const uint16_t*>(gate);
+  auto* o16 = static_cast<uint16_t*>(out);
+  const MxDst none{nullptr, nullptr, 0, 0};
   if (mx != nullptr)
-    hipLaunchKernelGGL((window_attn_kernel<kBlockWaves, true>), grid, block, 0, st, in, blocks,
-                       grp_kv, grp_n, nblocks, heads, scale * kLog2e,
-                       static_cast<const uint16_t*>(gate), g_st, g_sh, nullptr, 0, 0, nullptr,
-                       0, 0, *mx);
+    hipLaunchKernelGGL((window_attn_kernel<128, kBlockWaves, true>), grid, block, 0, st, in,
+                       blocks, grp_kv, grp_n, nblocks, heads, scale * kLog2e, g16, g_st, g_sh,
+                       nullptr, 0, 0, nullptr, 0, 0, *mx);
+  else if (head_dim == 128)
+    hipLaunchKernelGGL((window_attn_kernel<128, kBlockWaves, false>), grid, block, 0, st, in,
+                       blocks, grp_kv, grp_n, nblocks, heads, scale * kLog2e, g16, g_st, g_sh,
+                       o16, o_st, o_sh, lse, l_st, l_sh, none);
+  else if (head_dim == 64)
+    hipLaunchKernelGGL((window_attn_kernel<64, kBlockWaves, false>), grid, block, 0, st, in,
+                       blocks, grp_kv, grp_n, nblocks, heads, scale * kLog2e, g16, g_st, g_sh,
+                       o16, o_st, o_sh, lse, l_st, l_sh, none);
   else
-    hipLaunchKernelGGL((window_attn_kernel<kBlockWaves, false>), grid, block, 0, st, in, blocks,
-                       grp_kv, grp_n, nblocks, heads, scale * kLog2e,
-                       static_cast<const uint16_t*>(gate), g_st, g_sh,
-                       static_cast<uint16_t*>(out), o_st, o_sh, lse, l_st, l_sh,
-                       MxDst{nullptr, nullptr, 0, 0});
+    hipLaunchKernelGGL((window_attn_kernel<256, kBlockWaves, false>), grid, block, 0, st, in,
+                       blocks, grp_kv, grp_n, nblocks, heads, scale * kLog2e, g16, g_st, g_sh,
+                       o16, o_st, o_sh, lse, l_st, l_sh, none);
   return check_launch(name);
 }
 
@@ -415,22 +441,23 @@ int launch_window(const char* name, const void* q, int64_t q_st, int64_t q_sh, c
 
 // Reference: paper_window_attention (src/models/softmax_attention/paper_window.py:182-243),
 // window_softmax_reference (window.py:56-111), apply_softmax_gate (kernels.py:51-67).
-// q, k, v: bf16 [rows, heads, 128] (token / head strides, unit channel stride);
+// q, k, v: bf16 [rows, heads, head_dim] (head_dim 64, 128 or 256; token / head strides,
+// unit channel stride);
 // blocks: int32 [nblocks, 3] = (first query, end of its query group, group index), each
 // block at most 256 queries; grp_kv: int32 [groups, 8, 2] key intervals [a, b); grp_n:
 // int32 [groups] interval counts. gate (nullable): bf16 per (token, head) scalar multiplied
-// into the bf16 output. out: bf16 rows of 128 channels; lse (nullable): fp32 natural-log
-// sum of exp of the scaled scores.
+// into the bf16 output. out: bf16 rows of head_dim channels; lse (nullable): fp32
+// natural-log sum of exp of the scaled scores.
 VDN_API int vdn_window_attention(const void* q, int64_t q_st, int64_t q_sh, const void* k,
                                  int64_t k_st, int64_t k_sh, const void* v, int64_t v_st,
                                  int64_t v_sh, const int* blocks, int nblocks, const int* grp_kv,
-                                 const int* grp_n, int heads, float scale, const void* gate,
-                                 int64_t g_st, int64_t g_sh, void* out, int64_t o_st,
-                                 int64_t o_sh, float* lse, int64_t l_st, int64_t l_sh,
-                                 void* stream) {
+                                 const int* grp_n, int heads, int head_dim, float scale,
+                                 const void* gate, int64_t g_st, int64_t g_sh, void* out,
+                                 int64_t o_st, int64_t o_sh, float* lse, int64_t l_st,
+                                 int64_t l_sh, void* stream) {
   return launch_window("vdn_window_attention", q, q_st, q_sh, k, k_st, k_sh, v, v_st, v_sh,
-                       blocks, nblocks, grp_kv, grp_n, heads, scale, gate, g_st, g_sh, out, o_st,
-                       o_sh, lse, l_st, l_sh, nullptr, stream);
+                       blocks, nblocks, grp_kv, grp_n, heads, head_dim, scale, gate, g_st, g_sh,
+                       out, o_st, o_sh, lse, l_st, l_sh, nullptr, stream);
 }
 
 // The same attention with the output quantized in the epilogue: query row q, head h ->
@@ -447,6 +474,6 @@ VDN_API int vdn_window_attention_mxfp8(const void* q, int64_t q_st, int64_t q_sh
                                        void* stream) {
   const MxDst mx{static_cast<uint8_t*>(codes), static_cast<uint8_t*>(scales), kp, chunk0};
   return launch_window("vdn_window_attention_mxfp8", q, q_st, q_sh, k, k_st, k_sh, v, v_st,
-                       v_sh, blocks, nblocks, grp_kv, grp_n, heads, scale, gate, g_st, g_sh,
+                       v_sh, blocks, nblocks, grp_kv, grp_n, heads, 128, scale, gate, g_st, g_sh,
                        nullptr, 0, 0, nullptr, 0, 0, &mx, stream);
 }

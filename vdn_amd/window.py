@@ -330,8 +330,8 @@ def paper_window_attention(query, key, value, plan: PaperWindowPlan, scale=None,
         raise ValueError("native varlen requires BF16/FP16 and unit innermost stride")
     if not query.is_cuda or query.device != plan.device:
         raise ValueError("Q/K/V and prepared plan must be on the same CUDA device")
-    if query.shape[2] != 128 or query.dtype != torch.bfloat16:
-        raise NotImplementedError("the gfx950 window kernel takes bf16 with head_dim 128")
+    if query.dtype != torch.bfloat16:
+        raise NotImplementedError("the gfx950 window kernel takes bf16 activations")
     scale = query.shape[-1] ** -0.5 if scale is None else float(scale)
     if not math.isfinite(scale):
         raise ValueError("scale must be finite")
@@ -339,6 +339,8 @@ def paper_window_attention(query, key, value, plan: PaperWindowPlan, scale=None,
     if out_mxfp8 is not None:
         if out is not None or return_lse:
             raise ValueError("out_mxfp8 excludes out and return_lse")
+        if d != 128:
+            raise ValueError("out_mxfp8 holds one head per 128-column chunk: head_dim 128")
         codes, scales, chunk0 = mxfp8_destination(out_mxfp8, plan.layout.seq_len, h,
                                                   query.device)
         if gate is not None:
@@ -369,7 +371,7 @@ def paper_window_attention(query, key, value, plan: PaperWindowPlan, scale=None,
     _lib.call("vdn_window_attention", query.data_ptr(), query.stride(0), query.stride(1),
               key.data_ptr(), key.stride(0), key.stride(1), value.data_ptr(), value.stride(0),
               value.stride(1), dp.blocks.data_ptr(), dp.nblocks, dp.intervals.data_ptr(),
-              dp.counts.data_ptr(), h, scale, _lib.ptr(gate),
+              dp.counts.data_ptr(), h, d, scale, _lib.ptr(gate),
               0 if gate is None else gate.stride(0), 0 if gate is None else gate.stride(1),
               out.data_ptr(), out.stride(0), out.stride(1), _lib.ptr(lse),
               0 if lse is None else lse.stride(0), 0 if lse is None else lse.stride(1),
