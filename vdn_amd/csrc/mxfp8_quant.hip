@@ -68,17 +68,22 @@ mxfp8_quantize_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t k, i
                       uint8_t* __restrict__ q, uint8_t* __restrict__ s, int64_t kp, int64_t items,
                       uint32_t* __restrict__ nonfinite, uint8_t* __restrict__ finite_tiles) {
   const int lane16 = threadIdx.x & 15;
-  const int64_t ngroups = static_cast<int64_t>(gridDim.x) * (kThreads / 16);
-  const int64_t group = static_cast<int64_t>(blockIdx.x) * (kThreads / 16) + (threadIdx.x >> 4);
-  const int64_t chunks = kp >> 7;
+  // items < 2^31 (the host checks): 32-bit index arithmetic, one division per item
+  const uint32_t ngroups = gridDim.x * (kThreads / 16);
+  const uint32_t group = blockIdx.x * (kThreads / 16) + (threadIdx.x >> 4);
+  const uint32_t chunks = static_cast<uint32_t>(kp >> 7);
   bool bad[kItemsPerGroup];
   float v[kItemsPerGroup][8];
+  int64_t row_of[kItemsPerGroup], chunk_of[kItemsPerGroup];
   // Issue every load of the group's items before any arithmetic.
 #pragma unroll
   for (int j = 0; j < kItemsPerGroup; ++j) {
-    const int64_t item = group + j * ngroups;
-    const int64_t r = item < items ? item / chunks : rows;  // rows => zero fill
-    const int64_t c0 = (item % chunks) * 128 + lane16 * 8;
+    const uint32_t item = group + j * ngroups;
+    const uint32_t rr = item / chunks;
+    row_of[j] = rr;
+    chunk_of[j] = item - rr * chunks;
+    const int64_t r = item < items ? row_of[j] : rows;  // rows => zero fill
+    const int64_t c0 = chunk_of[j] * 128 + lane16 * 8;
     bad[j] = false;
     if (kAct == kActSwiGLU) {
       float g[8];
@@ -93,10 +98,10 @@ mxfp8_quantize_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t k, i
   bool any_bad = false;
 #pragma unroll
   for (int j = 0; j < kItemsPerGroup; ++j) {
-    const int64_t item = group + j * ngroups;
+    const uint32_t item = group + j * ngroups;
     if (item >= items) break;  // uniform across the 16-lane group
-    const int64_t r = item / chunks;
-    const int64_t chunk = item % chunks;
+    const int64_t r = row_of[j];
+    const int64_t chunk = chunk_of[j];
     if (kAct == kActGeluTanh) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[j][i] = round_bf16(gelu_tanh(v[j][i]));
@@ -454,6 +459,9 @@ int launch_quantize(const void* x, int64_t rows, int64_t k, int64_t stride, void
   const int64_t items = rp * (kp / 128);
   const int64_t per_block = (kThreads / 16) * kItemsPerGroup;
   const int64_t blocks = (items + per_block - 1) / per_block;
+  if (items + per_block * 2 > (1ll << 31))  // item indices (plus a grid of slack) fit in 31 bits
+    return set_error(kUnsupported, "%s: %lld x %lld is too large (2^31 128-column items)", name,
+                     static_cast<long long>(rows), static_cast<long long>(k));
   const bool vec = (k % 8 == 0) && (stride % 8 == 0) && aligned16(x) &&
                    (kAct != kActSwiGLU || k % 8 == 0);
   auto* xp = static_cast<const uint16_t*>(x);
