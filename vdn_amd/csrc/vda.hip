@@ -864,14 +864,22 @@ __device__ __forceinline__ void norm_gate_store8(float* y, const float* w, const
 // weights) in LDS once; then each wave walks its token groups without barriers.
 // For a group, lane l (t = l % 16, g = l / 16) loads channels 32 ks + 8 g .. +8 (ks = 0..3)
 // of token t, which is exactly its B operand of v_mfma_f32_16x16x32_bf16 (no LDS round
-// trip for q or for the gate's down rows); the A operand is 16 LDS state rows. The
-// accumulators then hold channels c = 16 mt + 4 g + v (mt = 0..7, v = 0..3) of token t, so
-// the SiLU/L2 of q, the gate's bias and sigmoid, RMSNorm·w·gate and the MXFP8 quantization
-// all run in those registers: a per-token sum or a per-32-block max needs only the four
-// lanes t, t + 16, t + 32, t + 48 (two permlane swaps).
+// trip for q or for the gate's down rows); the A operand is 16 LDS state rows. The LDS rows
+// are permuted (ro_row) so that accumulator mt, element v of lane group g holds output
+// channel 32 (mt / 2) + 8 g + 4 (mt % 2) + v of token t: a lane's accumulators 2j, 2j + 1
+// are the 8 contiguous channels 32 j + 8 g .. +8, read (gate) and written (output) as 16
+// bytes, the same footprint as its q loads. The SiLU/L2 of q, the gate's bias and sigmoid,
+// RMSNorm·w·gate and the MXFP8 quantization all run in those registers: a per-token sum or
+// a per-32-block max needs only the four lanes t, t + 16, t + 32, t + 48 (two permlane
+// swaps), and 32-block b is accumulators 2b, 2b + 1.
 constexpr int kRoWaves = 8;
 constexpr int kRoThreads = 64 * kRoWaves;
 constexpr int kQRow = 136;  // padded bf16 row of the LDS matrices (272 bytes)
+
+// LDS row of output channel c (inverse of the accumulator order above).
+__device__ __forceinline__ int ro_row(int c) {
+  return 16 * (2 * (c >> 5) + ((c >> 2) & 1)) + 4 * ((c >> 3) & 3) + (c & 3);
+}
 
 // The low-rank output gate of the linear branch, formed inside the readout instead of read:
 // gate[t, h*128 + c] = bf16(sigmoid(bf16(down[t] . up_w[h*128 + c] + up_b[h*128 + c]))), with
@@ -901,6 +909,28 @@ __device__ __forceinline__ void rows_times_tokens(const uint16_t* m, const bf16x
     }
 }
 
+// The global operands of one 16-token group in this lane: q channels 32 ks + 8 g .. +8 and,
+// for a read gate, gate channels 32 j + 8 g .. +8, or, for a formed gate, the same channels
+// of the token's down-projection row (its B operands). Zero for tokens past the frame.
+struct RoLoads {
+  u32x4 q[4];
+  u32x4 gt[4];
+};
+
+template <bool kProj>
+__device__ __forceinline__ void ro_load(const View& qv, const View& gv, const GateProj& gp,
+                                        int f, int h, int s, bool valid, int64_t row0, int g,
+                                        RoLoads& L) {
+  const uint16_t* qrow = qv.at(f, h, s) + g * 8;
+  const uint16_t* grow =
+      kProj ? gp.down + (row0 + s) * gp.d_st + g * 8 : gv.at(f, h, s) + g * 8;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    L.q[j] = valid ? *reinterpret_cast<const u32x4*>(qrow + j * 32) : u32x4{0u, 0u, 0u, 0u};
+    L.gt[j] = valid ? *reinterpret_cast<const u32x4*>(grow + j * 32) : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
 // Fused readout: q' = bf16(L2(SiLU(q_raw))) (optional), y = bf16(q' · stateᵀ), then
 // o = bf16(RMSNorm(y)·w·gate) into bf16 out[f*S + s, h*D + c] or, with kMx, MXFP8 codes and
 // scales (token row f*S + s, chunk chunk0 + h). kProj forms the gate from GateProj; else it
@@ -911,9 +941,9 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
                    const void* __restrict__ weight, int weight_f32, float eps, View gv,
                    GateProj gp, uint16_t* __restrict__ out, int64_t o_sf, int64_t o_sh,
                    int64_t o_ss, int spatial, int heads, int parts, MxDst mx) {
-  __shared__ __attribute__((aligned(16))) uint16_t sState[kD * kQRow];     // [c][k]
+  __shared__ __attribute__((aligned(16))) uint16_t sState[kD * kQRow];     // [ro_row(c)][k]
   __shared__ __attribute__((aligned(16))) uint16_t sUp[kProj ? kD * kQRow : 8];
-  __shared__ __attribute__((aligned(16))) float sW[kD];
+  __shared__ __attribute__((aligned(16))) float sW[kD];                    // [ro_row(c)]
   __shared__ __attribute__((aligned(16))) float sB[kD];
   const int logical = xcd_contiguous(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
   const int h = logical % heads;
@@ -924,44 +954,37 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
 
   const uint16_t* st = state + (static_cast<int64_t>(f) * heads + h) * kD * kD;
   for (int idx = tid * 8; idx < kD * kD; idx += kRoThreads * 8)
-    *reinterpret_cast<u32x4*>(&sState[(idx >> 7) * kQRow + (idx & 127)]) =
+    *reinterpret_cast<u32x4*>(&sState[ro_row(idx >> 7) * kQRow + (idx & 127)]) =
         *reinterpret_cast<const u32x4*>(st + idx);
   if constexpr (kProj) {
     const uint16_t* up = gp.up_w + static_cast<int64_t>(h) * kD * kD;
     for (int idx = tid * 8; idx < kD * kD; idx += kRoThreads * 8)
-      *reinterpret_cast<u32x4*>(&sUp[(idx >> 7) * kQRow + (idx & 127)]) =
+      *reinterpret_cast<u32x4*>(&sUp[ro_row(idx >> 7) * kQRow + (idx & 127)]) =
           *reinterpret_cast<const u32x4*>(up + idx);
-    if (tid < kD) sB[tid] = bf16_bits_to_f32(gp.up_b[h * kD + tid]);
+    if (tid < kD) sB[ro_row(tid)] = bf16_bits_to_f32(gp.up_b[h * kD + tid]);
   }
   if (tid < kD)
-    sW[tid] = weight_f32 ? static_cast<const float*>(weight)[tid]
-                         : bf16_bits_to_f32(static_cast<const uint16_t*>(weight)[tid]);
+    sW[ro_row(tid)] = weight_f32 ? static_cast<const float*>(weight)[tid]
+                                 : bf16_bits_to_f32(static_cast<const uint16_t*>(weight)[tid]);
   __syncthreads();
 
   const int groups = (spatial + 15) >> 4;
   const int per = (groups + parts - 1) / parts;
   const int g_end = min(groups, (part + 1) * per);
   const int64_t row0 = static_cast<int64_t>(f) * spatial;
-  for (int grp = part * per + wave; grp < g_end; grp += kRoWaves) {
+  int grp = part * per + wave;
+  RoLoads cur;
+  if (grp < g_end)
+    ro_load<kProj>(qv, gv, gp, f, h, grp * 16 + t16, grp * 16 + t16 < spatial, row0, g, cur);
+  for (; grp < g_end; grp += kRoWaves) {
     const int s = grp * 16 + t16;
     const bool valid = s < spatial;
-    // ---- q' as B operands ----
-    u32x4 qraw[4];
-    const uint16_t* qrow = qv.at(f, h, s) + g * 8;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      qraw[ks] = valid ? *reinterpret_cast<const u32x4*>(qrow + ks * 32) : u32x4{0u, 0u, 0u, 0u};
     // ---- gate (bf16 pairs in the accumulator layout) ----
     uint32_t gate_pk[8][2];
     if constexpr (kProj) {
-      u32x4 draw[4];
-      const uint16_t* drow = gp.down + (row0 + s) * gp.d_st + g * 8;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        draw[ks] = valid ? *reinterpret_cast<const u32x4*>(drow + ks * 32) : u32x4{0u, 0u, 0u, 0u};
       bf16x8 db[4];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) db[ks] = __builtin_bit_cast(bf16x8, draw[ks]);
+      for (int ks = 0; ks < 4; ++ks) db[ks] = __builtin_bit_cast(bf16x8, cur.gt[ks]);
       f32x4 ag[8];
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) ag[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -981,19 +1004,17 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
         gate_pk[mt][1] = pack_bf16x2(gv4[2], gv4[3]);
       }
     } else {
-      const uint16_t* grow = gv.at(f, h, s) + g * 4;
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) {
-        const u32x2 w2 = valid ? *reinterpret_cast<const u32x2*>(grow + mt * 16) : u32x2{0u, 0u};
-        gate_pk[mt][0] = w2[0];
-        gate_pk[mt][1] = w2[1];
+        gate_pk[mt][0] = cur.gt[mt >> 1][2 * (mt & 1)];
+        gate_pk[mt][1] = cur.gt[mt >> 1][2 * (mt & 1) + 1];
       }
     }
     bf16x8 qb[4];
     {
       float qf[4][8];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) unpack8(qraw[ks], qf[ks]);
+      for (int ks = 0; ks < 4; ++ks) unpack8(cur.q[ks], qf[ks]);
       if (activate_q) {
         // paper_sglang.py:235-238: y = silu(x); y / sqrt(max(sum y^2, 1e-12))
         float ss = 0.f;
@@ -1039,9 +1060,10 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
       }
     }
     if constexpr (kMx) {
-      // 32-block b of the head's 128 channels = accumulator groups mt = 2b, 2b + 1
+      // 32-block b of the head's 128 channels = accumulators 2b, 2b + 1; this lane's 8 codes
+      // of it are channels 32 b + 8 g .. +8
       const int64_t row = row0 + s;
-      uint8_t* crow = mx.codes + row * mx.kp + (mx.chunk0 + h) * 128 + g * 4;
+      uint8_t* crow = mx.codes + row * mx.kp + (mx.chunk0 + h) * 128 + g * 8;
       uint32_t word = 0;
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
@@ -1053,27 +1075,37 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
         amax = max_quad_rows(amax);
         float sinv;
         word |= e8m0_from_amax(amax, &sinv) << (8 * b);
+        u32x2 c2;
 #pragma unroll
-        for (int m = 2 * b; m < 2 * b + 2; ++m) {
+        for (int m = 0; m < 2; ++m) {
           int c = 0;
-          c = __builtin_amdgcn_cvt_pk_fp8_f32(ay[m][0] * sinv, ay[m][1] * sinv, c, false);
-          c = __builtin_amdgcn_cvt_pk_fp8_f32(ay[m][2] * sinv, ay[m][3] * sinv, c, true);
-          if (valid) *reinterpret_cast<uint32_t*>(crow + m * 16) = static_cast<uint32_t>(c);
+          const f32x4& y4 = ay[2 * b + m];
+          c = __builtin_amdgcn_cvt_pk_fp8_f32(y4[0] * sinv, y4[1] * sinv, c, false);
+          c = __builtin_amdgcn_cvt_pk_fp8_f32(y4[2] * sinv, y4[3] * sinv, c, true);
+          c2[m] = static_cast<uint32_t>(c);
         }
+        if (valid) *reinterpret_cast<u32x2*>(crow + b * 32) = c2;
       }
       if (valid && g == 0)
         *reinterpret_cast<uint32_t*>(
             mx.scales + swizzled_scale_offset(row, (mx.chunk0 + h) * 4, mx.kp >> 7)) = word;
     } else if (valid) {
-      uint16_t* orow = out + f * o_sf + h * o_sh + s * o_ss + g * 4;
+      uint16_t* orow = out + f * o_sf + h * o_sh + s * o_ss + g * 8;
 #pragma unroll
-      for (int mt = 0; mt < 8; ++mt) {
-        u32x2 o2;
-        o2[0] = pack_bf16x2(ay[mt][0], ay[mt][1]);
-        o2[1] = pack_bf16x2(ay[mt][2], ay[mt][3]);
-        *reinterpret_cast<u32x2*>(orow + mt * 16) = o2;
+      for (int j = 0; j < 4; ++j) {
+        u32x4 o4;
+        o4[0] = pack_bf16x2(ay[2 * j][0], ay[2 * j][1]);
+        o4[1] = pack_bf16x2(ay[2 * j][2], ay[2 * j][3]);
+        o4[2] = pack_bf16x2(ay[2 * j + 1][0], ay[2 * j + 1][1]);
+        o4[3] = pack_bf16x2(ay[2 * j + 1][2], ay[2 * j + 1][3]);
+        *reinterpret_cast<u32x4*>(orow + j * 32) = o4;
       }
     }
+    // the next group's loads (a copy into a second register set held across the MFMAs
+    // would not fit the 128-VGPR budget)
+    if (grp + kRoWaves < g_end)
+      ro_load<kProj>(qv, gv, gp, f, h, s + 16 * kRoWaves, s + 16 * kRoWaves < spatial, row0, g,
+                     cur);
   }
 }
 
