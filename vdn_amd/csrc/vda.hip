@@ -199,14 +199,18 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
       activate8_f32(kf, true);
       activate8_f32(vf, false);
     }
-    const u32x4 kw = pack8(kf);  // k' (bf16)
+    // The packed words are made opaque so that the values are taken back out of them (one
+    // shift or mask each) rather than rounded again one by one.
+    u32x4 kw = pack8(kf);  // k' (bf16)
+    asm volatile("" : "+v"(kw));
     unpack8(kw, kf);
     const float b = braw;
     const float b16 = round_bf16(b);
     float prod[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) prod[i] = b * kf[i];  // exact for bf16 beta
-    const u32x4 hw = pack8(prod);                       // hi = bf16(prod)
+    u32x4 hw = pack8(prod);                             // hi = bf16(prod)
+    asm volatile("" : "+v"(hw));
     float hi[8];
     unpack8(hw, hi);
 #pragma unroll
@@ -225,7 +229,8 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
       *reinterpret_cast<u32x4*>(row + 2 * kTile) = mw;
       *reinterpret_cast<u32x4*>(row + 3 * kTile) = pack8(prod);
     }
-    const u32x4 vw = pack8(vf);  // v' (bf16)
+    u32x4 vw = pack8(vf);  // v' (bf16)
+    asm volatile("" : "+v"(vw));
     unpack8(vw, vf);
 #pragma unroll
     for (int i = 0; i < 8; ++i) vf[i] *= b16;
