@@ -435,7 +435,9 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
 //         is then done reading buffer s % 2 and buffer (s+1) % 2 is complete;
 //   tail  A groups mt >= kHead in N order: after the MFMAs of B fragment nt, fragment nt of
 //         step s+1 is read into the same registers; step s+2's tiles are DMA'd into buffer
-//         s % 2 between the MFMA groups.
+//         s % 2, one segment after the first and one after the third MFMA of each column
+//         (a DMA issue stalls while the CU's address unit is busy; issued in the shadow of
+//         queued MFMAs it costs less than in bursts).
 // So the next step starts with its B fragments and first A fragment already in registers,
 // and a tile's epilogue (straight from the accumulators: 8-byte bf16 or 4-byte MXFP8 stores)
 // runs while the next tile's first steps are in flight.
@@ -514,7 +516,7 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
                              int64_t mp, int64_t np, int64_t kp, Epilogue ep, int64_t out_rows,
                              int64_t n, int tiles_m, int tiles_n, int group_m) {
   constexpr int TM = 8, TN = 8;
-  static_assert(kHead >= 1 && kHead < TM, "head groups");
+  static_assert(kHead >= 1 && kHead + 2 < TM, "head groups");
   // after the two step buffers: the bf16 modes' staging strips, or the producer's SwiGLU
   // hand-over slots (2 wave pairs x 64 lanes x 32 fp32)
   __shared__ __attribute__((aligned(1024))) uint8_t
@@ -922,15 +924,22 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
         // step s+1's scale words are read late: the current ones are mostly dead by then
         if (nt == TN - 2) read_scales(nxt);
         __builtin_amdgcn_sched_barrier(0);
+        // the column's two DMA segments go out after its first and third MFMA, each in the
+        // shadow of the MFMAs that follow it
 #pragma unroll
-        for (int mt = kHead; mt < TM; ++mt)
+        for (int mt = kHead; mt < TM; ++mt) {
           acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
               bfrag[nt], af[mt], acc[mt][nt], 0, 0, 0, static_cast<int>(sb[nt]), 0,
               static_cast<int>(sa[mt]));
+          if (mt == kHead || mt == kHead + 2) {
+            asm volatile("" ::"a"(acc[mt][nt]) : "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            dma_segment(cur, 2 * nt + (mt == kHead ? 0 : 1));
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
         pin_column_from<kHead>(acc, nt);
         bfrag[nt] = frag(nxt + kPTile * kBK, wn * 128 + nt * 16 + frag_row);
-        dma_segment(cur, 2 * nt);
-        dma_segment(cur, 2 * nt + 1);
       }
       __builtin_amdgcn_sched_barrier(0);
       dma_advance();
@@ -953,12 +962,15 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
 // Tile order of the persistent kernel: bands of 4 tile rows, so the 32 tiles an XCD runs
 // at once are 4 A row panels x 8 W column panels and the next 32 reuse the same A panels.
 // Measured against bands of 2, 6, 8, 16 and 32 rows at the block's shapes: 4 is fastest
-// (2-4% over 8 on QKV; 16 and 32 lose 7-25%). The head of a K step takes 3 of the 8 A row
-// groups (measured against 4 and 5: 3 is 1-2% faster on the K = 10240 / 13824 launches).
+// (2-4% over 8 on QKV; 16 and 32 lose 7-25%). The head of a K step takes 2 of the 8 A row
+// groups: with the DMA segments spread over the tail's MFMAs, 2 takes 3.5-4.5% fewer cycles
+// per K step than 3 with the segments issued in pairs after each column (QKV, [O | O_lin]
+// and FFN-down shapes); 3 with the spread segments was in between, and 1 or 2 with paired
+// segments no better than 3.
 constexpr int kPGroupM = 4;
 
 #ifndef VDN_GEMM_HEAD
-#define VDN_GEMM_HEAD 3
+#define VDN_GEMM_HEAD 2
 #endif
 
 int cu_count() {
