@@ -104,4 +104,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// a, b = round_bf16(a), round_bf16(b) through one packed conversion (each half is rounded on
+// its own, so the values are those of round_bf16). The packed word is opaque to the
+// compiler: the values come back out of it with one shift or mask each, instead of being
+// rounded again one conversion per value.
+__device__ __forceinline__ void round_bf16_pair(float& a, float& b) {
+  uint32_t p = pack_bf16x2(a, b);
+  asm volatile("" : "+v"(p));
+  a = __uint_as_float(p << 16);
+  b = __uint_as_float(p & 0xffff0000u);
+}
+
 }  // namespace vdn

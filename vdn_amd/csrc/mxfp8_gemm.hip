@@ -657,6 +657,8 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
     }
     const int64_t chunk128 = swiglu ? n0 >> 8 : (n0 + wn * 128) >> 7;
     const bool chunk_in = chunk128 < (ep.kp_out >> 7);
+    // every row and column of the tile inside the output: no per-value bounds selects
+    const bool interior = m0 + kPTile <= out_rows && n0 + kPTile <= n;
     // A rolled loop over the 8 row groups keeps one copy of the code; the accumulators
     // (registers) are picked by a uniform branch chain, not indexed.
 #pragma nounroll
@@ -670,11 +672,13 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
         for (int nt = 0; nt < TN; ++nt) {
           f32x4 a = acc[m][nt];
           // the copy is opaque: the rounding below stays in this branch instead of being
-          // hoisted (for all 256 accumulators at once) out of the loop
+          // hoisted (for all 256 accumulators at once) out of the loop; so is the packed
+          // pair, which is then unpacked rather than each value converted on its own
           asm volatile("" : "+v"(a));
           u32x2 p;
           p[0] = pack_bf16x2(a[0], a[1]);
           p[1] = pack_bf16x2(a[2], a[3]);
+          asm volatile("" : "+v"(p));
           unpack4(p, y[nt]);
         }
       }
@@ -686,7 +690,12 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
           for (int nt = 0; nt < TN; ++nt) {
             f32x4 gs;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) gs[v] = swiglu_gate(round_bf16(y[nt][v] + bias4[nt][v]));
+            for (int v = 0; v < 4; v += 2) {
+              float g0 = y[nt][v] + bias4[nt][v], g1 = y[nt][v + 1] + bias4[nt][v + 1];
+              round_bf16_pair(g0, g1);
+              gs[v] = swiglu_gate(g0);
+              gs[v + 1] = swiglu_gate(g1);
+            }
             *reinterpret_cast<f32x4*>(pass_slot + nt * 4) = gs;
           }
         }
@@ -696,28 +705,64 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
           for (int nt = 0; nt < TN; ++nt) {
             const f32x4 gs = *reinterpret_cast<const f32x4*>(pass_slot + nt * 4);
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              const float val = round_bf16(round_bf16(y[nt][v] + bias4[nt][v]) * gs[v]);
-              if (ep.nonfinite != nullptr) bad = bad || !(fabsf(val) < INFINITY);
-              const bool in = row < out_rows && ocol0 + nt * 16 + v < n;
-              y[nt][v] = in ? val : 0.f;
+            for (int v = 0; v < 4; v += 2) {
+              float a0 = y[nt][v] + bias4[nt][v], a1 = y[nt][v + 1] + bias4[nt][v + 1];
+              round_bf16_pair(a0, a1);
+              a0 *= gs[v];
+              a1 *= gs[v + 1];
+              round_bf16_pair(a0, a1);
+              y[nt][v] = a0;
+              y[nt][v + 1] = a1;
             }
           }
+          if (ep.nonfinite != nullptr) {
+#pragma unroll
+            for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+              for (int v = 0; v < 4; ++v) bad = bad || !(fabsf(y[nt][v]) < INFINITY);
+          }
+#pragma unroll
+          for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const bool in = row < out_rows && ocol0 + nt * 16 + v < n;
+              y[nt][v] = in ? y[nt][v] : 0.f;
+            }
         }
         __syncthreads();   // the slot is free for the next row group
         if (wn == 1) continue;   // the a wave quantizes and stores the chunk
       } else {
-        // bias, activation and bf16 rounding; rows >= out_rows and columns >= n are zero
+        // bias, activation and bf16 rounding, two values at a time; rows >= out_rows and
+        // columns >= n are zero (tested only on tiles that reach past the output)
 #pragma unroll
         for (int nt = 0; nt < TN; ++nt)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            float val = round_bf16(y[nt][v] + bias4[nt][v]);
-            if (ep.act == 1) val = round_bf16(gelu_tanh(val));
-            if (ep.nonfinite != nullptr) bad = bad || !(fabsf(val) < INFINITY);
-            const bool in = row < out_rows && col0 + nt * 16 + v < n;
-            y[nt][v] = in ? val : 0.f;
+          for (int v = 0; v < 4; v += 2) {
+            float a = y[nt][v] + bias4[nt][v], b = y[nt][v + 1] + bias4[nt][v + 1];
+            round_bf16_pair(a, b);
+            if (ep.act == 1) {
+              a = gelu_tanh(a);
+              b = gelu_tanh(b);
+              round_bf16_pair(a, b);
+            }
+            y[nt][v] = a;
+            y[nt][v + 1] = b;
           }
+        if (ep.nonfinite != nullptr) {
+#pragma unroll
+          for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) bad = bad || !(fabsf(y[nt][v]) < INFINITY);
+        }
+        if (!interior) {
+#pragma unroll
+          for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const bool in = row < out_rows && col0 + nt * 16 + v < n;
+              y[nt][v] = in ? y[nt][v] : 0.f;
+            }
+        }
       }
       // every lane takes part in the block maxima; only the stores are predicated
       const bool store = chunk_in && row < mp;
