@@ -876,15 +876,18 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
           u32x4 packed;
 #pragma unroll
           for (int e = 0; e < 8; e += 2) {
-            // the last rounding of each value is the one of the packing conversion
-            float yy[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-              float v = y[e + h] + bias8[e + h];
-              if constexpr (kMode == 1) v = r[e + h] + round_bf16(gate8[e + h] * round_bf16(v));
-              yy[h] = v;
+            // the last rounding of each value is the one of the packing conversion; the
+            // residual form r + bf16(gate * bf16(v)) rounds two values at a time
+            float v0 = y[e] + bias8[e], v1 = y[e + 1] + bias8[e + 1];
+            if constexpr (kMode == 1) {
+              round_bf16_pair(v0, v1);
+              v0 *= gate8[e];
+              v1 *= gate8[e + 1];
+              round_bf16_pair(v0, v1);
+              v0 += r[e];
+              v1 += r[e + 1];
             }
-            packed[e / 2] = pack_bf16x2(yy[0], yy[1]);
+            packed[e / 2] = pack_bf16x2(v0, v1);
           }
           // streaming store: the output is not read again here, and in L2 it would only evict
           // the A / W panels the next tiles need
