@@ -632,10 +632,11 @@ def _counter_rows(path, counter):
 GEMM_KERNEL = re.compile(r"mxfp8_gemm_(persistent_)?kernel")
 
 
-def summarize_traffic(fetch_csv, write_csv):
+def summarize_traffic(fetch_csv, write_csv, command=""):
     """Markdown summary of the HBM traffic per MXFP8 GEMM launch from a FETCH_SIZE pass and a
     WRITE_SIZE pass (each run with --calibrate-copy). Each counter is scaled by the factor
-    that maps its reading for the calibration kernel onto the kernel's known 1 GiB."""
+    that maps its reading for the calibration kernel onto the kernel's known 1 GiB.
+    `command` (the passes' command lines) replaces the default ones in the summary."""
     passes = {}
     for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
         rows = _counter_rows(path, counter)
@@ -660,14 +661,23 @@ def summarize_traffic(fetch_csv, write_csv):
         lines.append(f"| {len(lines)} | `{kname}{tile}` | {fk * fetch_factor / 2**20:.3f} | "
                      f"{wk * write_factor / 2**20:.3f} | {nbytes / 1e9:.3f} |")
     per_launch = total / len(fetch)
+    if command:
+        cmd_lines = ["Commands (from the repository root, on one MI355X):", "",
+                     *["    " + c.strip()
+                       for c in command.replace(" ;; ", "\n").strip().splitlines()], "",
+                     "    python3 bench.py --summarize-traffic "
+                     f"{fetch_csv} {write_csv}", ""]
+    else:
+        cmd_lines = [
+            "Commands (from the repository root, on one MI355X; one block forward, no warmup):", "",
+            "    rocprofv3 --pmc FETCH_SIZE -d gpurun_out/pmc_fetch -o f --output-format csv -- "
+            "python3 bench.py --steps 1 --warmup 0 --isolated-steps 0 --no-cpu-baseline --calibrate-copy",
+            "    rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_write -o w --output-format csv -- "
+            "python3 bench.py --steps 1 --warmup 0 --isolated-steps 0 --no-cpu-baseline --calibrate-copy",
+            "    python3 bench.py --summarize-traffic gpurun_out/pmc_fetch/f_counter_collection.csv "
+            "gpurun_out/pmc_write/w_counter_collection.csv", ""]
     out = ["# HBM traffic per MXFP8 GEMM launch, hybrid DiT block at 108,000 tokens", "",
-           "Commands (from the repository root, on one MI355X; one block forward, no warmup):", "",
-           "    rocprofv3 --pmc FETCH_SIZE -d gpurun_out/pmc_fetch -o f --output-format csv -- "
-           "python3 bench.py --steps 1 --warmup 0 --isolated-steps 0 --no-cpu-baseline --calibrate-copy",
-           "    rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_write -o w --output-format csv -- "
-           "python3 bench.py --steps 1 --warmup 0 --isolated-steps 0 --no-cpu-baseline --calibrate-copy",
-           "    python3 bench.py --summarize-traffic gpurun_out/pmc_fetch/f_counter_collection.csv "
-           "gpurun_out/pmc_write/w_counter_collection.csv", "",
+           *cmd_lines,
            "Calibration: `torch.neg` over 2^29 bf16 values (1 GiB read, 1 GiB written) reads "
            f"FETCH_SIZE x{fetch_factor:.4f} and WRITE_SIZE x{write_factor:.4f} of its true bytes; "
            "each GEMM reading below is scaled by that factor.", "",
@@ -737,7 +747,7 @@ def main():
         summarize_counters(args.summarize_counters, args.command)
         return
     if args.summarize_traffic:
-        summarize_traffic(*args.summarize_traffic)
+        summarize_traffic(*args.summarize_traffic, command=args.command)
         return
     if args.summarize_trace:
         summarize_trace(*args.summarize_trace)
