@@ -318,10 +318,56 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
       if (t + 1 < ntiles) process(t + 1, ntiles, a0, b0, std::integral_constant<int, 1>{});
     }
   }
+  const float inv_l = l > 0.f ? 1.0f / l : 0.f;
+  if constexpr (kMx) {
+    // ---- MXFP8 epilogue straight from the accumulators ----
+    // Lane (col, g) holds channels 32 db + 8 j + 4 g + i (v = 4 j + i) of query my_q: 16 of
+    // the 32 channels of MXFP8 block db; lane ^ 32 holds the other 16. y = bf16(bf16(o / l)
+    // * gate) as in the bf16 form; the block's amax takes one exchange, and each group of 4
+    // channels leaves as one 4-byte store of codes.
+    float gv = 1.f;
+    if (gate != nullptr && q_live) gv = bf16_bits_to_f32(gate[static_cast<int64_t>(my_q) * g_st + h * g_sh]);
+    uint8_t* crow = mx.codes + static_cast<int64_t>(my_q) * mx.kp + (mx.chunk0 + h) * 128 + 4 * g;
+    uint32_t word = 0;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) {
+      float y[16];
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        float a = o[db][v] * inv_l, b = o[db][v + 1] * inv_l;
+        round_bf16_pair(a, b);
+        if (gate != nullptr) {
+          a *= gv;
+          b *= gv;
+          round_bf16_pair(a, b);
+        }
+        y[v] = a;
+        y[v + 1] = b;
+      }
+      float amax = 0.f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) amax = fmaxf(amax, fabsf(y[v]));
+      amax = fmaxf(amax, __shfl_xor(amax, 32));
+      float sinv;
+      word |= e8m0_from_amax(amax, &sinv) << (8 * db);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int c = 0;
+        c = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * j] * sinv, y[4 * j + 1] * sinv, c, false);
+        c = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * j + 2] * sinv, y[4 * j + 3] * sinv, c, true);
+        if (q_live) *reinterpret_cast<uint32_t*>(crow + 32 * db + 8 * j) = static_cast<uint32_t>(c);
+      }
+    }
+    if (q_live && g == 0)
+      *reinterpret_cast<uint32_t*>(
+          mx.scales + swizzled_scale_offset(my_q, (mx.chunk0 + h) * 4, mx.kp >> 7)) = word;
+    if (lse != nullptr && q_live && g == 0)
+      lse[static_cast<int64_t>(my_q) * l_st + h * l_sh] = (m + log2f(l)) * kLn2;
+    return;
+  }
   __syncthreads();  // the epilogue reuses the K buffers
 
   // ---- epilogue: O / l, optional gate, through LDS to coalesced rows ----
-  const float inv_l = l > 0.f ? 1.0f / l : 0.f;
   // [kBM queries][kD channels] bf16 staged across the tile buffers, kBN queries per buffer
   auto stage_rows = [&](int r) -> uint16_t* {
     const int which = r / kBN;  // uniform per wave for both uses below
@@ -350,17 +396,7 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     const int c8 = (tid % kChunks) * 8;
     const uint16_t* src = stage_rows(r);
     const u32x4 row8 = *reinterpret_cast<const u32x4*>(&src[(r % kBN) * kD + c8]);
-    if constexpr (kMx) {
-      float y[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        y[2 * i] = bf16_bits_to_f32(static_cast<uint16_t>(row8[i] & 0xffff));
-        y[2 * i + 1] = bf16_bits_to_f32(static_cast<uint16_t>(row8[i] >> 16));
-      }
-      quantize_store8(y, tid & 15, q, mx.chunk0 + h, mx.kp, mx.codes, mx.scales);
-    } else {
-      *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(q) * o_st + h * o_sh + c8) = row8;
-    }
+    *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(q) * o_st + h * o_sh + c8) = row8;
   }
 }
 
