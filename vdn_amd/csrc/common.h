@@ -115,4 +115,12 @@ __device__ __forceinline__ void round_bf16_pair(float& a, float& b) {
   b = __uint_as_float(p & 0xffff0000u);
 }
 
+// The four values of v rounded to bf16, two per conversion (as round_bf16_pair).
+__device__ __forceinline__ void round_bf16_x4(f32x4& v) {
+  float a = v[0], b = v[1], c = v[2], d = v[3];
+  round_bf16_pair(a, b);
+  round_bf16_pair(c, d);
+  v = f32x4{a, b, c, d};
+}
+
 }  // namespace vdn

@@ -999,11 +999,14 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
         const f32x4 b = *reinterpret_cast<const f32x4*>(&sB[mt * 16 + g * 4]);
         float gv4[4];
 #pragma unroll
+        for (int v = 0; v < 4; ++v) gv4[v] = ag[mt][v] + b[v];
+        round_bf16_pair(gv4[0], gv4[1]);
+        round_bf16_pair(gv4[2], gv4[3]);
+#pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const float z = round_bf16(ag[mt][v] + b[v]);
           // sigmoid by the hardware exp2 and reciprocal: a few fp32 ulp from 1 / (1 + exp(-z)),
           // below the bf16 rounding that follows
-          gv4[v] = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z * -1.4426950408889634f));
+          gv4[v] = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gv4[v] * -1.4426950408889634f));
         }
         gate_pk[mt][0] = pack_bf16x2(gv4[0], gv4[1]);
         gate_pk[mt][1] = pack_bf16x2(gv4[2], gv4[3]);
@@ -1045,14 +1048,14 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
     for (int mt = 0; mt < 8; ++mt) ay[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     rows_times_tokens(sState, qb, t16, g, ay);
     // ---- RMSNorm(y)·w·gate (paper_sglang.py:398-403), rounded to bf16 ----
+    // (two values per rounding conversion)
     float ss = 0.f;
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
+    for (int mt = 0; mt < 8; ++mt) {
+      round_bf16_x4(ay[mt]);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        ay[mt][v] = round_bf16(ay[mt][v]);
-        ss += ay[mt][v] * ay[mt][v];
-      }
+      for (int v = 0; v < 4; ++v) ss += ay[mt][v] * ay[mt][v];
+    }
     const float inv = 1.0f / sqrtf(sum_quad_rows(ss) / static_cast<float>(kD) + eps);
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
@@ -1061,8 +1064,9 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
       for (int v = 0; v < 4; ++v) {
         const uint32_t pk = gate_pk[mt][v >> 1];
         const float gt = __uint_as_float(v & 1 ? pk & 0xffff0000u : pk << 16);
-        ay[mt][v] = round_bf16(ay[mt][v] * inv * w[v] * gt);
+        ay[mt][v] = ay[mt][v] * inv * w[v] * gt;
       }
+      round_bf16_x4(ay[mt]);
     }
     if constexpr (kMx) {
       // 32-block b of the head's 128 channels = accumulators 2b, 2b + 1; this lane's 8 codes
