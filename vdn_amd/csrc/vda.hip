@@ -171,22 +171,27 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
   const int r = tid >> 4;
   const int steps = (spatial + kTS - 1) / kTS;
 
-  // The next step's raw rows load while this step's MFMAs run; they are activated and
-  // stored to the other LDS buffer at the step's end.
+  // Raw rows of one step in registers: activated and stored to the other LDS buffer at the
+  // end of the step before the one that reads them.
+  // beta's raw bits (fp32 for kSplit 3, the beta_f32 launch; else bf16 in the low half), turned
+  // into a float only when the step is activated, so no wait follows the loads
+  (void)beta_f32;
   u32x4 kraw, vraw;
-  float braw;
-  auto load_step = [&](int step, u32x4& kr, u32x4& vr, float& br) __attribute__((always_inline)) {
+  uint32_t braw;
+  auto load_step = [&](int step, u32x4& kr, u32x4& vr, uint32_t& br) __attribute__((always_inline)) {
     const int s = step * kTS + r;
     if (s < spatial) {
       kr = *reinterpret_cast<const u32x4*>(kv.at(f, h, s) + c8);
       vr = *reinterpret_cast<const u32x4*>(vv.at(f, h, s) + c8);
       const int64_t bo = f * b_sf + h * b_sh + s * b_ss;
-      br = beta_f32 ? static_cast<const float*>(beta)[bo]
-                    : bf16_bits_to_f32(static_cast<const uint16_t*>(beta)[bo]);
+      if constexpr (kSplit == 3)
+        br = static_cast<const uint32_t*>(beta)[bo];
+      else
+        br = static_cast<const uint16_t*>(beta)[bo];
     } else {
       kr = u32x4{0, 0, 0, 0};
       vr = u32x4{0, 0, 0, 0};
-      br = 0.f;
+      br = 0u;
     }
   };
   // Each rounding to bf16 is the packing conversion (RNE); the packed words are the LDS
@@ -204,7 +209,7 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
     u32x4 kw = pack8(kf);  // k' (bf16)
     asm volatile("" : "+v"(kw));
     unpack8(kw, kf);
-    const float b = braw;
+    const float b = __uint_as_float(kSplit == 3 ? braw : braw << 16);
     const float b16 = round_bf16(b);
     float prod[8];
 #pragma unroll
@@ -258,13 +263,15 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
     return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   };
 
+  // The raw rows of step s + 1 were loaded at the end of step s - 1 (right after step s's rows
+  // were activated), so their latency is covered by a whole step, not only its MFMAs.
   load_step(0, kraw, vraw, braw);
   store_step(0);
+  if (steps > 1) load_step(1, kraw, vraw, braw);
   __syncthreads();
   for (int step = 0; step < steps; ++step) {
     const int buf = step & 1;
     const bool more = step + 1 < steps;
-    if (more) load_step(step + 1, kraw, vraw, braw);
     const uint16_t* tk = lds[buf][0];
     const uint16_t* tv = lds[buf][1 + kSplit];
     bf16x8 kn[2], pn[kSplit][2];
@@ -287,6 +294,7 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
       }
     }
     if (more) store_step(buf ^ 1);
+    if (step + 2 < steps) load_step(step + 2, kraw, vraw, braw);
     __syncthreads();
   }
 
