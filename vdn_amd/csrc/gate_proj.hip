@@ -138,22 +138,40 @@ gate_projection_kernel(const uint16_t* __restrict__ x, int64_t x_st, int k,
       for (int nb = 0; nb < 3; ++nb) fr.w[j][nb] = *reinterpret_cast<const bf16x8*>(tW + w_off[nb][j]);
     }
   };
-  auto mfmas = [&](const Frags& fr) __attribute__((always_inline)) {
+  // The 12 MFMAs of one stage, with the stage's 4 DMAs (x1 stage sa into slot sla, W stage sw
+  // into slot slw) issued after MFMAs 0, 3, 6 and 9: a DMA issue can stall while the CU's
+  // address unit is busy, and in the shadow of queued MFMAs the stall costs less than a burst.
+  auto mfmas = [&](const Frags& fr, int sa, int sla, int sw, int slw) __attribute__((always_inline)) {
+    const int64_t woff = static_cast<int64_t>(sw) * kGK * 2;
+    uint16_t* dw = sW + slw * (kGCols * kGK);
+    int n = 0;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int nb = 0; nb < 3; ++nb)
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+        for (int mb = 0; mb < 2; ++mb) {
           acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr.a[j][mb], fr.w[j][nb], acc[mb][nb], 0, 0, 0);
+          if (n % 3 == 0) {
+            asm volatile("" ::"v"(acc[mb][nb]) : "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            if (n == 0)
+              issue_a(sa, sla);
+            else
+              g_load_lds16(w_src[n / 3 - 1] + woff, dw + 64 * (3 * wave + n / 3 - 1) * 8);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          ++n;
+        }
   };
 
   // ---- K loop. Stage s lives in x1 slot s % 6 and W slot s % 4. The prologue issues x1
-  // stages 0-4, then W stages 0-2; iteration s (after its barrier) issues one batch, x1 stage
-  // s + 5 and W stage s + 3, into the slots of stage s - 1 (whose fragments every wave read
-  // in iteration s - 2 and consumed in iteration s - 1), reads the fragments of stage s + 1
-  // into registers and runs the MFMAs of stage s from the registers read one iteration
-  // earlier, so the LDS reads of one stage overlap the MFMAs of the previous. Past the last
+  // stages 0-4, then W stages 0-2; iteration s (after its barrier) reads the fragments of
+  // stage s + 1 into registers, then runs the MFMAs of stage s from the registers read one
+  // iteration earlier and, among them, issues one batch, x1 stage s + 5 and W stage s + 3,
+  // into the slots of stage s - 1 (whose fragments every wave read in iteration s - 2 and
+  // consumed in iteration s - 1), so the LDS reads of one stage overlap the MFMAs of the
+  // previous. Past the last
   // stage a batch loads the last stage again (into those free slots), so every batch is 4
   // DMAs per wave and the waits are exact: stage s + 1 must have landed before the barrier
   // of iteration s; its W came with batch s - 2 (the prologue for s < 2), its x1 earlier, so
@@ -179,12 +197,11 @@ gate_projection_kernel(const uint16_t* __restrict__ x, int64_t x_st, int k,
         asm volatile("s_waitcnt vmcnt(3)\n\ts_barrier" ::: "memory");
       else
         asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
-      issue_a(min(si + kARing - 1, stages - 1), aslot == 0 ? kARing - 1 : aslot - 1);
-      issue_w(min(si + kWRing - 1, stages - 1), wslot == 0 ? kWRing - 1 : wslot - 1);
       const int an = aslot == kARing - 1 ? 0 : aslot + 1;
       const int wn2 = wslot == kWRing - 1 ? 0 : wslot + 1;
       if (si + 1 < stages) read_frags(fr[1 - h], sA + an * (kGRows * kGK), sW + wn2 * (kGCols * kGK));
-      mfmas(fr[h]);
+      mfmas(fr[h], min(si + kARing - 1, stages - 1), aslot == 0 ? kARing - 1 : aslot - 1,
+            min(si + kWRing - 1, stages - 1), wslot == 0 ? kWRing - 1 : wslot - 1);
       aslot = an;
       wslot = wn2;
     }
