@@ -65,6 +65,17 @@ def test_quantize_strided_and_unaligned_rows(device):
     check_quantized(base[:, 256:512], q, s)
 
 
+def test_quantize_ragged_k_on_a_wider_row(device):
+    """K = 520 (a multiple of 8, not of 128) as a view of 1040-wide rows, 200 rows: the last
+    128-column chunk holds 8 real columns; the 120 past K must quantize as zero although the
+    memory there holds the next columns of the row."""
+    torch.manual_seed(7)
+    base = torch.randn(200, 1040, dtype=torch.bfloat16) * 5
+    view = base.to(device)[:, :520]
+    q, s = vm.quantize_activation(view)
+    check_quantized(base[:, :520].contiguous(), q, s)
+
+
 @pytest.mark.parametrize("arrangement", ["sorted", "perm0", "perm1", "perm2"])
 def test_quantize_every_bf16_value(device, arrangement):
     """All 63k finite bf16 patterns, packed into blocks two different ways."""
