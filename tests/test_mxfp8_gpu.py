@@ -145,6 +145,59 @@ def test_prenorm_quantize(device, rows, k, weight_f32, tables_f32):
     assert torch.equal(q2, q) and torch.equal(s2, s)
 
 
+@pytest.mark.parametrize("rows,k,pattern,f32", [(300, 5120, "shared", False),
+                                                 (300, 5120, "groups", False),
+                                                 (129, 1024, "shared", True),
+                                                 (77, 2048, "groups", True),
+                                                 (260, 4096, "mixed", False)])
+def test_prenorm_quantize_full_rows(device, rows, k, pattern, f32):
+    """Row widths of 1024, 2048, 4096 and 5120 columns, whose kernel stages a table row shared
+    by a workgroup's rows in LDS: one table row for every row ("shared"), one per 8-row group
+    ("groups": each group shared, the groups differing) and per-row indices ("mixed")."""
+    g = torch.Generator().manual_seed(k + rows)
+    x = torch.randn(rows, k, generator=g).to(torch.bfloat16) * 2
+    w = (torch.rand(k, generator=g) + 0.5).to(torch.float32 if f32 else torch.bfloat16)
+    tdt = torch.float32 if f32 else torch.bfloat16
+    scale = (torch.randn(3, k, generator=g) * 0.2).to(tdt)
+    shift = (torch.randn(3, k, generator=g) * 0.2).to(tdt)
+    if pattern == "shared":
+        idx = torch.full((rows,), 2, dtype=torch.long)
+    elif pattern == "groups":
+        idx = (torch.arange(rows) // 8 + 1) % 3
+    else:
+        idx = torch.randint(0, 3, (rows,), generator=g)
+    y, q, s, finite = vm.launch_prenorm_quantize(x.to(device), w.to(device), 1e-6,
+                                                 scale.to(device), shift.to(device),
+                                                 idx.to(device), write_bf16=True)
+    ref, mag = om.prenorm(x.float().numpy(), w.float().numpy(), 1e-6, scale.float().numpy(),
+                          shift.float().numpy(), idx.numpy(), return_magnitude=True)
+    yc = y.float().cpu().numpy()
+    ulps = bf16_ulps(yc, ref)
+    assert ((ulps <= 1) | (np.abs(yc - ref) <= 2.0 ** -21 * mag)).all()
+    assert (ulps == 0).mean() > 0.999
+    check_quantized(y.cpu(), q, s)
+    assert bool(finite.all())
+    _, q2, s2, f2 = vm.launch_prenorm_quantize(x.to(device), w.to(device), 1e-6, scale.to(device),
+                                               shift.to(device), idx.to(device), write_bf16=False)
+    assert torch.equal(q2, q) and torch.equal(s2, s) and torch.equal(f2, finite)
+
+
+def test_prenorm_full_rows_finite_flags(device):
+    x = torch.randn(20, 5120, dtype=torch.bfloat16)
+    x[3, 4000] = float("inf")
+    x[17, 11] = float("nan")
+    w = torch.ones(5120, dtype=torch.bfloat16)
+    t = torch.zeros(1, 5120, dtype=torch.bfloat16)
+    idx = torch.zeros(20, dtype=torch.long, device=device)
+    for write_bf16 in (True, False):
+        _, _, _, finite = vm.launch_prenorm_quantize(x.to(device), w.to(device), 1e-6, t.to(device),
+                                                     t.to(device), idx, write_bf16=write_bf16)
+        assert finite.shape == (128,)
+        expect = [True] * 128
+        expect[3] = expect[17] = False
+        assert finite.cpu().tolist() == expect
+
+
 def test_prenorm_finite_flags(device):
     x = torch.randn(5, 256, dtype=torch.bfloat16)
     x[2, 7] = float("inf")

@@ -72,18 +72,40 @@ __device__ __forceinline__ float swiglu_gate(float g) {
 __device__ __forceinline__ float silu_mul(float a, float g) { return a * swiglu_gate(g); }
 #pragma clang fp contract(on)
 
-// Quantizes the 8 values a lane holds (one quarter of a 32-block), stores the 8 codes
-// and, from lane 0 of each 16-lane group, the chunk's 4 scale bytes. A group is one DPP
-// row (lanes 16k .. 16k + 15) whose lanes are all active: the amax and the scale bytes move
-// between its lanes by DPP.
-__device__ __forceinline__ void quantize_store8(const float* v, int lane16, int64_t r, int64_t chunk,
-                                                int64_t kp, uint8_t* __restrict__ q,
-                                                uint8_t* __restrict__ s) {
+// The maximum of `amax` over lanes l, l ^ 1, l ^ 2, l ^ 3 (the 4 lanes of a 32-block) for an
+// amax that is non-negative and never NaN (a running fmaxf from 0 ignores NaN). Such floats
+// order as their bit patterns do, so the steps are unsigned maxima, which take the DPP
+// operand directly.
+__device__ __forceinline__ float block_amax4(float amax) {
+  uint32_t b = __float_as_uint(amax);
+  b = max(b, static_cast<uint32_t>(
+                 __builtin_amdgcn_update_dpp(0, static_cast<int>(b), 0xB1, 0xf, 0xf, true)));
+  b = max(b, static_cast<uint32_t>(
+                 __builtin_amdgcn_update_dpp(0, static_cast<int>(b), 0x4E, 0xf, 0xf, true)));
+  return __uint_as_float(b);
+}
+
+// The 4 scale bytes of a 16-lane group (byte i from lane 4 i of the DPP row), complete in
+// the group's lane 0: lanes 0 and 8 first pair their byte with lane + 4's, then lane 0 takes
+// lane 8's pair as its upper half.
+__device__ __forceinline__ uint32_t scale_word16(uint32_t scale) {
+  const uint32_t pair =
+      scale | (static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+                   0, static_cast<int>(scale), 0x104, 0xf, 0xf, true)) << 8);  // row_shl 4
+  return pair | (static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+                     0, static_cast<int>(pair), 0x108, 0xf, 0xf, true)) << 16);  // row_shl 8
+}
+
+// Quantizes the 8 values a lane holds (one quarter of a 32-block), stores the 8 codes at
+// `qdst` and, from the lanes with `scale_lane` set (lane 0 of each 16-lane group), the
+// chunk's 4 scale bytes at `sdst`. A group is one DPP row (lanes 16k .. 16k + 15) whose lanes
+// are all active: the amax and the scale bytes move between its lanes by DPP.
+__device__ __forceinline__ void quantize_store8_at(const float* v, uint8_t* __restrict__ qdst,
+                                                   uint8_t* __restrict__ sdst, bool scale_lane) {
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  amax = fmaxf(amax, dpp_f32<0xB1>(amax));  // lane ^ 1
-  amax = fmaxf(amax, dpp_f32<0x4E>(amax));  // lane ^ 2
+  amax = block_amax4(amax);
   float inv;
   const uint32_t scale = e8m0_from_amax(amax, &inv);
   float scaled[8];
@@ -91,14 +113,17 @@ __device__ __forceinline__ void quantize_store8(const float* v, int lane16, int6
   for (int i = 0; i < 8; ++i) scaled[i] = v[i] * inv;
   const u32x2 codes = e4m3x8(scaled);
   // 16 lanes write the chunk's 128 contiguous bytes: a streaming store of whole lines
-  __builtin_nontemporal_store(codes, reinterpret_cast<u32x2*>(q + r * kp + chunk * 128 + lane16 * 8));
-  const uint32_t s1 = dpp_u32<0x104>(scale);  // lane + 4 of the 16-lane row
-  const uint32_t s2 = dpp_u32<0x108>(scale);
-  const uint32_t s3 = dpp_u32<0x10C>(scale);
-  if (lane16 == 0) {
-    const uint32_t word = scale | (s1 << 8) | (s2 << 16) | (s3 << 24);
-    *reinterpret_cast<uint32_t*>(s + swizzled_scale_offset(r, chunk * 4, kp >> 7)) = word;
-  }
+  __builtin_nontemporal_store(codes, reinterpret_cast<u32x2*>(qdst));
+  const uint32_t word = scale_word16(scale);
+  if (scale_lane) *reinterpret_cast<uint32_t*>(sdst) = word;
+}
+
+// quantize_store8_at for lane `lane16` of the group holding row r, 128-column chunk `chunk`.
+__device__ __forceinline__ void quantize_store8(const float* v, int lane16, int64_t r, int64_t chunk,
+                                                int64_t kp, uint8_t* __restrict__ q,
+                                                uint8_t* __restrict__ s) {
+  quantize_store8_at(v, q + r * kp + chunk * 128 + lane16 * 8,
+                     s + swizzled_scale_offset(r, chunk * 4, kp >> 7), lane16 == 0);
 }
 
 }  // namespace vdn

@@ -184,8 +184,7 @@ mxfp8_quantize32_kernel(const uint16_t* __restrict__ x, int rows, int k, int str
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    amax = fmaxf(amax, dpp_f32<0xB1>(amax));  // lane ^ 1
-    amax = fmaxf(amax, dpp_f32<0x4E>(amax));  // lane ^ 2
+    amax = block_amax4(amax);
     float inv;
     const uint32_t scale = e8m0_from_amax(amax, &inv);
     float scaled[8];
@@ -194,11 +193,8 @@ mxfp8_quantize32_kernel(const uint16_t* __restrict__ x, int rows, int k, int str
     const u32x2 codes = e4m3x8(scaled);
     __builtin_nontemporal_store(
         codes, reinterpret_cast<u32x2*>(q + (r * static_cast<uint32_t>(kp) + chunk * 128 + lane16 * 8)));
-    const uint32_t s1 = dpp_u32<0x104>(scale);  // lane + 4 of the 16-lane row
-    const uint32_t s2 = dpp_u32<0x108>(scale);
-    const uint32_t s3 = dpp_u32<0x10C>(scale);
+    const uint32_t word = scale_word16(scale);
     if (lane16 == 0) {
-      const uint32_t word = scale | (s1 << 8) | (s2 << 16) | (s3 << 24);
       // swizzled_scale_offset(r, 4 chunk, kp / 128) in 32 bits
       const uint32_t off = ((r >> 7) * chunks + chunk) * 512 + (r & 31) * 16 + ((r & 127) >> 5) * 4;
       *reinterpret_cast<uint32_t*>(s + off) = word;
@@ -249,26 +245,86 @@ __device__ __forceinline__ void unpack_bf16x8(const u32x4 w, float* f) {
 constexpr int kPrenormRows = 16;
 constexpr int kPrenormThreads = 64 * kPrenormRows;
 
-// One row of kCols = 512 kS columns (every slice real) whose weight, 1 + scale and shift
-// rows are staged in `tab`: the arithmetic and rounding of the general path below in
-// straight-line code. The bf16 results stay packed (the rounding conversion is the
-// packing); a bf16 is nonfinite iff its magnitude bits reach 0x7f80, so one packed max per
-// word tests two of them.
+// Rows of exactly kCols = 512 kS columns (every slice real), eight rows per workgroup, two
+// workgroups per CU (60 KB of LDS and at most 128 VGPRs each), so one's table staging and
+// load latency overlap the other's arithmetic; each wave issues its row's loads before the
+// table row is staged. The row index is wave-uniform, so every address is a scalar row base
+// plus a per-lane offset. The arithmetic is that of the general path in straight-line code.
+// The bf16 results stay packed (the rounding conversion is the packing); a bf16 is nonfinite
+// iff its magnitude bits reach 0x7f80, so one packed max per word tests two of them. (At
+// [108000, 5120]: 354 us without the bf16 output and 518 us with it, against 429 and 548 us
+// for sixteen rows per workgroup at one workgroup per CU, whose staging and arithmetic left
+// the CU without loads in flight.)
+constexpr int kFullRows = 8;
+constexpr int kFullThreads = 64 * kFullRows;
+
 template <int kS>
-__device__ __forceinline__ void prenorm_row_straight(const uint16_t* __restrict__ xrow,
-                                                     const float (*tab)[64 * kS * 8], float eps,
-                                                     int64_t r, int64_t kp,
-                                                     uint16_t* __restrict__ y,
-                                                     uint8_t* __restrict__ q,
-                                                     uint8_t* __restrict__ s,
-                                                     uint8_t* __restrict__ finite) {
+__global__ void __launch_bounds__(kFullThreads) __attribute__((amdgpu_waves_per_eu(4)))
+prenorm_quantize_full_rows_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t stride,
+                                  const void* __restrict__ weight, int weight_f32, float eps,
+                                  const void* __restrict__ scale, int64_t scale_stride,
+                                  const void* __restrict__ shift, int64_t shift_stride,
+                                  int tables_f32, const int64_t* __restrict__ indices,
+                                  uint16_t* __restrict__ y, uint8_t* __restrict__ q,
+                                  uint8_t* __restrict__ s, uint8_t* __restrict__ finite,
+                                  int64_t rp) {
 #pragma clang fp contract(off)
   constexpr int kCols = 64 * kS * 8;
-  const int lane = threadIdx.x & 63;
+  constexpr int64_t kChunks = kCols / 128;
+  __shared__ __attribute__((aligned(16))) float tab[3][kCols];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kFullRows;
+  const int64_t r = r0 + wave;
+  const bool in_row = r < rows;  // wave-uniform
+  const int64_t idx0 = r0 < rows ? indices[r0] : 0;
+  int same = 1;
+  if (tid < kFullRows && r0 + tid < rows) same = indices[r0 + tid] == idx0;
   u32x4 raw[kS];
 #pragma unroll
-  for (int j = 0; j < kS; ++j)
-    raw[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xrow + (lane + 64 * j) * 8));
+  for (int j = 0; j < kS; ++j) raw[j] = u32x4{0u, 0u, 0u, 0u};
+  if (in_row) {
+    const uint16_t* xrow = x + r * stride + lane * 8;
+#pragma unroll
+    for (int j = 0; j < kS; ++j)
+      raw[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xrow + 512 * j));
+  }
+  // one table row for the whole workgroup?
+  const bool shared_row = __syncthreads_and(same) != 0;
+  if (shared_row) {
+    for (int c0 = tid * 8; c0 < kCols; c0 += kFullThreads * 8) {
+      float t[8];
+      load_table8(weight, weight_f32, c0, t);
+      *reinterpret_cast<f32x4*>(&tab[0][c0]) = f32x4{t[0], t[1], t[2], t[3]};
+      *reinterpret_cast<f32x4*>(&tab[0][c0 + 4]) = f32x4{t[4], t[5], t[6], t[7]};
+      load_table8(scale, tables_f32, idx0 * scale_stride + c0, t);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) t[i] = 1.0f + t[i];  // the (1 + scale) factor, formed once
+      *reinterpret_cast<f32x4*>(&tab[1][c0]) = f32x4{t[0], t[1], t[2], t[3]};
+      *reinterpret_cast<f32x4*>(&tab[1][c0 + 4]) = f32x4{t[4], t[5], t[6], t[7]};
+      load_table8(shift, tables_f32, idx0 * shift_stride + c0, t);
+      *reinterpret_cast<f32x4*>(&tab[2][c0]) = f32x4{t[0], t[1], t[2], t[3]};
+      *reinterpret_cast<f32x4*>(&tab[2][c0 + 4]) = f32x4{t[4], t[5], t[6], t[7]};
+    }
+  }
+  __syncthreads();
+  if (r >= rp) return;  // whole wave (no barrier follows)
+  // slice j of this lane: columns 8 (lane + 64 j) .. + 8, i.e. 128-column chunk 4 j + lane / 16;
+  // its codes sit at row base + 8 lane + 512 j and its group's scale word at the row's
+  // swizzled base + 512 (lane / 16) + 2048 j
+  uint8_t* const qlane = q + r * kCols + lane * 8;
+  uint8_t* const slane = s + swizzled_scale_offset(r, 0, kChunks) + (lane >> 4) * 512;
+  const bool scale_lane = (lane & 15) == 0;
+  if (!in_row) {  // a padding row: zero codes, the zero scale, finite
+#pragma unroll
+    for (int j = 0; j < kS; ++j) {
+      float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      quantize_store8_at(v, qlane + 512 * j, slane + 2048 * j, scale_lane);
+    }
+    if (lane == 0) finite[r] = 1;
+    return;
+  }
+  const int64_t table_row = shared_row ? idx0 : indices[r];
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < kS; ++j) {
@@ -281,23 +337,32 @@ __device__ __forceinline__ void prenorm_row_straight(const uint16_t* __restrict_
   for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
   const float ms = ss / static_cast<float>(kCols) + eps;
   const float inv_rms = static_cast<float>(1.0 / sqrt(static_cast<double>(ms)));
+  uint16_t* const ylane = y == nullptr ? nullptr : y + r * kCols + lane * 8;
   u16x2 mag = {0, 0};
 #pragma unroll
   for (int j = 0; j < kS; ++j) {
     const int c0 = (lane + 64 * j) * 8;
     float xv[8], w[8], u[8], sh[8];
     unpack_bf16x8(raw[j], xv);
+    if (shared_row) {
 #pragma unroll
-    for (int i = 0; i < 8; i += 4) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(&tab[0][c0 + i]);
-      const f32x4 b = *reinterpret_cast<const f32x4*>(&tab[1][c0 + i]);
-      const f32x4 c = *reinterpret_cast<const f32x4*>(&tab[2][c0 + i]);
+      for (int i = 0; i < 8; i += 4) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(&tab[0][c0 + i]);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(&tab[1][c0 + i]);
+        const f32x4 c = *reinterpret_cast<const f32x4*>(&tab[2][c0 + i]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        w[i + e] = a[e];
-        u[i + e] = b[e];
-        sh[i + e] = c[e];
+        for (int e = 0; e < 4; ++e) {
+          w[i + e] = a[e];
+          u[i + e] = b[e];
+          sh[i + e] = c[e];
+        }
       }
+    } else {
+      load_table8(weight, weight_f32, c0, w);
+      load_table8(scale, tables_f32, table_row * scale_stride + c0, u);
+      load_table8(shift, tables_f32, table_row * shift_stride + c0, sh);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) u[i] = 1.0f + u[i];
     }
     u32x4 packed;
 #pragma unroll
@@ -307,15 +372,16 @@ __device__ __forceinline__ void prenorm_row_straight(const uint16_t* __restrict_
       packed[i] = pack_bf16x2(t0 * u[2 * i] + sh[2 * i], t1 * u[2 * i + 1] + sh[2 * i + 1]);
       mag = __builtin_elementwise_max(mag, __builtin_bit_cast(u16x2, packed[i] & 0x7fff7fffu));
     }
-    if (y != nullptr) __builtin_nontemporal_store(packed, reinterpret_cast<u32x4*>(y + r * kCols + c0));
+    if (y != nullptr) __builtin_nontemporal_store(packed, reinterpret_cast<u32x4*>(ylane + 512 * j));
     float v[8];
     unpack_bf16x8(packed, v);
-    quantize_store8(v, lane & 15, r, 4 * j + (lane >> 4), kp, q, s);
+    quantize_store8_at(v, qlane + 512 * j, slane + 2048 * j, scale_lane);
   }
   const bool any_bad = __ballot(mag[0] >= 0x7f80 || mag[1] >= 0x7f80) != 0;
   if (lane == 0) finite[r] = any_bad ? 0 : 1;
 }
 
+// Rows of other widths (K up to 512 kS columns, the last slices partial or padding).
 template <int kS>
 __global__ void __launch_bounds__(kPrenormThreads)
 prenorm_quantize_rows_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t k,
@@ -363,10 +429,6 @@ prenorm_quantize_rows_kernel(const uint16_t* __restrict__ x, int64_t rows, int64
     const int64_t r = r0 + wave;
     if (r >= rp) return;  // whole wave (no barrier follows)
     const bool in_row = r < rows;
-    if (__builtin_amdgcn_readfirstlane(shared_row && in_row && k == kCols)) {  // wave-uniform
-      prenorm_row_straight<kS>(x + r * stride, tab, eps, r, kp, y, q, s, finite);
-      return;
-    }
     const int64_t table_row = in_row ? indices[r] : 0;
     // the row stays in registers as packed bf16 (kS x 4 VGPRs) and is unpacked where used
     u32x4 raw[kS];
@@ -644,6 +706,20 @@ VDN_API int vdn_mxfp8_prenorm_quantize(const void* x, int64_t rows, int64_t k, i
                        scale_stride % tab_align == 0 && shift_stride % tab_align == 0;
   if (wave_ok && slices <= 64 * 10) {
     const dim3 grid(static_cast<unsigned>((rp + kPrenormRows - 1) / kPrenormRows));
+#define VDN_PRENORM_FULL(S)                                                                    \
+    if (k == 512 * (S)) {                                                                      \
+      hipLaunchKernelGGL((prenorm_quantize_full_rows_kernel<S>),                             \
+                         dim3(static_cast<unsigned>((rp + kFullRows - 1) / kFullRows)),        \
+                         dim3(kFullThreads), 0, st, xp, rows, row_stride, weight, wf, eps,     \
+                         scale, scale_stride,                                                  \
+                         shift, shift_stride, tf, indices, yp, qp, sp, finite, rp);            \
+      return check_launch(name);                                                               \
+    }
+    VDN_PRENORM_FULL(2)
+    VDN_PRENORM_FULL(4)
+    VDN_PRENORM_FULL(8)
+    VDN_PRENORM_FULL(10)
+#undef VDN_PRENORM_FULL
 #define VDN_PRENORM_WAVE(S)                                                                   \
     hipLaunchKernelGGL((prenorm_quantize_rows_kernel<S>), grid, dim3(kPrenormThreads), 0, st, xp, rows, \
                        k, row_stride, weight, wf, eps, scale, scale_stride, shift,              \
