@@ -183,6 +183,35 @@ def test_rope_independent_oracle_strided_inputs(device, layout, r):
     assert outputs[0].data_ptr() != outputs[1].data_ptr()
 
 
+@pytest.mark.parametrize("heads,tables", [(7, torch.float32), (40, torch.bfloat16),
+                                          (2, torch.bfloat16)])
+@torch.no_grad()
+def test_rope_full_width_fast_form_matches_general_form(device, heads, tables):
+    """D = R = 128 on 16-byte rows takes the per-token fast form; the same values behind a
+    channel stride of 2 take the general per-row form. Both round the same way, so their
+    outputs are bit-identical (head counts below, at and above a multiple of 4)."""
+    g = torch.Generator().manual_seed(heads)
+    t = 37
+    storage = (torch.randn(t, 3 * heads * 128, generator=g) * 3).bfloat16()
+    q = storage[:, :heads * 128].view(t, heads, 128)
+    k = storage[:, heads * 128:2 * heads * 128].view(t, heads, 128)
+    qw = (torch.rand(128, generator=g) + 0.5).bfloat16()
+    kw = (torch.rand(128, generator=g) + 0.5).float()
+    angles = torch.randn(t, 128, generator=g) * 4
+    c, s = angles.cos().to(tables), angles.sin().to(tables)
+    args = (qw.to(device), kw.to(device), 1e-6, c.to(device), s.to(device))
+    fast = vw.paper_qk_rmsnorm_rope(q.to(device), k.to(device), *args, enabled=True)
+    wide = torch.zeros(t, heads, 256, dtype=torch.bfloat16)
+    wide2 = torch.zeros(t, heads, 256, dtype=torch.bfloat16)
+    wide[:, :, ::2], wide2[:, :, ::2] = q, k
+    general = vw.paper_qk_rmsnorm_rope(wide.to(device)[:, :, ::2], wide2.to(device)[:, :, ::2],
+                                       *args, enabled=True)
+    for a, b, raw, w in zip(fast, general, (q, k), (qw, kw)):
+        assert torch.equal(a, b)
+        torch.testing.assert_close(a.cpu(), ow.qk_rope(raw, w, 1e-6, c.float(), s.float()),
+                                   atol=.032, rtol=.02)
+
+
 @torch.no_grad()
 def test_rope_bf16_intermediate_round_trap(device):
     g = torch.Generator().manual_seed(715)

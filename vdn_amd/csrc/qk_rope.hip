@@ -8,7 +8,7 @@
 //   channels i >= R pass n through.
 // A row is held by D/8 lanes (8 channels each); the rotate partner is exchanged through a
 // per-row LDS line, which keeps arbitrary even R <= D exact (qk_rope_kernel), or, for the
-// common D = R = 128, through a DPP lane rotation (qk_rope_row128_kernel).
+// common D = 128, through a DPP lane rotation (qk_rope_row128_kernel, qk_rope_token128_kernel).
 #include "common.h"
 
 #include <math.h>
@@ -152,16 +152,21 @@ qk_rope_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float eps,
   }
 }
 
-// Fast form for 128-channel heads rotated over the full width (R = 128) or not rotated
-// (R = 0), with unit channel strides and 16-byte rows: the rotate-half partner of a lane's 8
-// channels is 8 lanes away in the same 16-lane row, so a DPP row rotation by 8 exchanges it
-// (no LDS line, no barrier), and a workgroup walks kGroups groups of 16 rows. Arithmetic and
+// Fast forms for 128-channel heads with unit channel strides and 16-byte rows. Arithmetic and
 // rounding are those of qk_rope_kernel.
+//
+// qk_rope_row128_kernel: rotated over the full width (R = 128) or not rotated (R = 0); a
+// 16-lane group per row, a workgroup walking kRopeGroups groups of 16 rows. The rotate-half
+// partner of a lane's 8 channels is 8 lanes away in the same 16-lane row, so a DPP row
+// rotation by 8 exchanges it (no LDS line, no barrier). The launcher takes it for R = 0 (the
+// QK norm alone), where it streams at about 5.9 TB/s.
 constexpr int kRopeGroups = 8;
 
+// Lane l of a 16-lane row reads lane (l + 8) mod 16 (every source lane exists, so the bound
+// control only lets the rotation fold into the instruction that consumes it).
 __device__ __forceinline__ float row_ror8(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                               0x128, 0xf, 0xf, false));
+                                                               0x128, 0xf, 0xf, true));
 }
 
 __global__ void __launch_bounds__(256)
@@ -210,6 +215,64 @@ qk_rope_row128_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float e
 #pragma unroll
     for (int i = 0; i < 4; ++i) packed[i] = pack_bf16x2(o[2 * i], o[2 * i + 1]);
     __builtin_nontemporal_store(packed, reinterpret_cast<u32x4*>(a.out + row * kD + sub * 8));
+  }
+}
+
+// qk_rope_token128_kernel: R = 128. A wave takes one token and walks its heads four at a
+// time (a 16-lane group, 8 channels per lane, per head; every row load is one contiguous 1 KB
+// span); the weights and the token's cos / sin row (rounded to bf16) are loaded once per
+// token instead of once per row, and the partner's sign (-n_{c+64} for the first 64
+// channels) is folded into the lane's sin values: (-p) s and p (-s) are the same product,
+// rounding included. At [108000 tokens, 40 heads] for q and k of a fused QKV row: 1010 us for
+// the row walk above, 800 us for this form; holding 2, 4 or 8 heads' loads in flight per
+// group was slower (820-915 us), the registers costing more occupancy than the loads gain.
+__global__ void __launch_bounds__(256)
+qk_rope_token128_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float eps,
+                        const void* __restrict__ cos_t, const void* __restrict__ sin_t,
+                        int64_t c_st, int64_t s_st, int table_f32) {
+#pragma clang fp contract(off)
+  constexpr int kD = 128;
+  const int lane = threadIdx.x & 63, sub = lane & 15, g = lane >> 4;
+  const RopeArgs& a = blockIdx.y == 0 ? q : k;
+  const int64_t t =
+      static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (t >= tokens) return;  // whole wave
+  float wv[8], cvv[8], svv[8];
+  load8(a.w, a.w_f32, sub * 8, false, wv);
+  load8(cos_t, table_f32, t * c_st + sub * 8, true, cvv);
+  load8(sin_t, table_f32, t * s_st + sub * 8, true, svv);
+  if (sub < 8) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) svv[i] = -svv[i];
+  }
+  const uint16_t* const xt = a.x + t * a.st + g * a.sh + sub * 8;
+  uint16_t* const ot = a.out + (t * heads + g) * kD + sub * 8;
+  for (int h0 = 0; h0 < heads; h0 += 4) {
+    if (h0 + g >= heads) break;  // the whole 16-lane group (its DPP steps stay in it)
+    const u32x4 raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xt + h0 * a.sh));
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(raw[i] << 16);
+      v[2 * i + 1] = __uint_as_float(raw[i] & 0xffff0000u);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+    ss = sum16(ss);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(kD) + eps);
+    u32x4 packed;
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      float n0 = (v[i] * inv) * wv[i], n1 = (v[i + 1] * inv) * wv[i + 1];
+      round_bf16_pair(n0, n1);
+      float c0 = n0 * cvv[i], c1 = n1 * cvv[i + 1];
+      round_bf16_pair(c0, c1);
+      float s0 = row_ror8(n0) * svv[i], s1 = row_ror8(n1) * svv[i + 1];
+      round_bf16_pair(s0, s1);
+      packed[i / 2] = pack_bf16x2(c0 + s0, c1 + s1);
+    }
+    __builtin_nontemporal_store(packed, reinterpret_cast<u32x4*>(ot + h0 * kD));
   }
 }
 
@@ -266,7 +329,12 @@ VDN_API int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64
                           q_only ? 1 : 2),                                                      \
                      dim3(256), 0, st, qa, ka, tokens, heads, eps, cos_t, sin_t, c_st, c_sd,    \
                      s_st, s_sd, tf, r);
-  if (head_dim == 128 && vec && (r == 0 || r == 128)) {
+  if (head_dim == 128 && vec && r == 128) {
+    hipLaunchKernelGGL(qk_rope_token128_kernel,
+                       dim3(static_cast<unsigned>((tokens + 3) / 4), q_only ? 1 : 2),
+                       dim3(256), 0, st, qa, ka, tokens, heads, eps, cos_t, sin_t, c_st, s_st,
+                       tf);
+  } else if (head_dim == 128 && vec && r == 0) {
     const int64_t per_block = 16 * kRopeGroups;
     hipLaunchKernelGGL(qk_rope_row128_kernel,
                        dim3(static_cast<unsigned>((rows + per_block - 1) / per_block),
