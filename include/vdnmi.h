@@ -196,14 +196,17 @@ int vdn_vda_gather(const float* prefix, const float* suffix, const float* logp, 
  * activate_q, then out = bf16(y * (1/sqrt(mean(y^2) + eps)) * weight * gate).
  * q, gate, out: bf16 addressed (f, h, s); state: bf16 [frames, heads, 128, 128] ([v][k]);
  * weight: [128] bf16 or fp32 (weight_f32).
+ * head_dim (16, 32, 64 or 128) is the number of channels that carry data: rows are always
+ * 128 wide, channels past head_dim are zero in q, state and weight, and the norm's mean is
+ * over head_dim channels (the reference's branch body at d < 128, delta_rule.py:45-60).
  * Replaces: the readout matmul and vdn_linear_epilogue of paper_readout
  * (src/models/linear_attention/paper_stack.py:317-318, paper_sglang.py:377-437).
  */
 int vdn_vda_readout(const void* q, int64_t q_sf, int64_t q_sh, int64_t q_ss, int activate_q,
                     const void* state, const void* weight, int weight_f32, float eps,
                     const void* gate, int64_t g_sf, int64_t g_sh, int64_t g_ss, void* out,
-                    int64_t o_sf, int64_t o_sh, int64_t o_ss, int frames, int heads, int spatial,
-                    void* stream);
+                    int64_t o_sf, int64_t o_sh, int64_t o_ss, int head_dim, int frames,
+                    int heads, int spatial, void* stream);
 
 /* vdn_vda_readout with the output quantized in the epilogue instead of stored as bf16: token
  * row f * spatial + s, head h -> MXFP8 codes[row, 128 (chunk0 + h) .. +128) of a [rows, kp]
@@ -235,13 +238,14 @@ int vdn_vda_readout_gated(const void* q, int64_t q_sf, int64_t q_sh, int64_t q_s
                           int heads, int spatial, void* stream);
 
 /*
- * RMSNorm(128) * weight * gate of a frame-major readout [frames, heads, spatial, 128] bf16.
+ * RMSNorm(head_dim) * weight * gate of a frame-major readout [frames, heads, spatial, 128]
+ * bf16; head_dim as in vdn_vda_readout (channels past it are zero).
  * Replaces: vdn_linear_epilogue (src/models/linear_attention/paper_sglang.py:406-437).
  */
 int vdn_vda_epilogue(const void* readout, const void* weight, int weight_f32, float eps,
                      const void* gate, int64_t g_sf, int64_t g_sh, int64_t g_ss, void* out,
-                     int64_t o_sf, int64_t o_sh, int64_t o_ss, int frames, int heads, int spatial,
-                     void* stream);
+                     int64_t o_sf, int64_t o_sh, int64_t o_ss, int head_dim, int frames,
+                     int heads, int spatial, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Frame-window softmax branch.

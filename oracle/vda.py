@@ -240,7 +240,7 @@ def paper_branch(q_raw, k_raw, v_raw, beta, gate, alpha, bounds, frames, spatial
     state = gather(prefix, suffix, alpha, bounds, seed, bridge)
     state = bf16(state.float()).double()
     readout = bf16((q @ state.transpose(-1, -2)).float()).double()
-    out = epilogue(readout, weight, gate.reshape(frames * spatial, h, D), eps)
+    out = epilogue(readout, weight, gate.reshape(frames * spatial, h, q_raw.shape[2]), eps)
     return out, dict(A=A, B=B, T=T, J=J, prefix=prefix, suffix=suffix, state=state,
                      readout=readout, seed=seed)
 

@@ -34,7 +34,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     lib = _lib.load()
     for name in declared_functions():
         assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
-    assert lib.vdn_abi_version() == 3
+    assert lib.vdn_abi_version() == 4
     assert lib.vdn_last_error() is not None
 
 
@@ -69,3 +69,17 @@ def test_short_conv_and_swiglu_entry_points_validate_before_launching():
     assert lib.vdn_mxfp8_gemm_act_quantize(fake, fake, 2048, fake, fake, 1280, 256, None, 3, fake,
                                            fake, 2048, 640, None, None) != 0
     assert b"unknown activation" in lib.vdn_last_error()
+
+
+def test_vda_readout_and_epilogue_validate_head_dim():
+    """head_dim (ABI 4) must be 16, 32, 64 or 128; checked before any HIP call (fake, never
+    dereferenced, aligned addresses)."""
+    lib = _lib.load()
+    fake = 1 << 20
+    args = (fake, 1024, 512, 128, 1, fake, fake, 0, 1e-6, fake, 1024, 512, 128, fake, 1024, 128,
+            512)
+    assert lib.vdn_vda_readout(*args, 48, 2, 4, 8, None) != 0
+    assert b"head_dim" in lib.vdn_last_error()
+    assert lib.vdn_vda_epilogue(fake, fake, 0, 1e-6, fake, 1024, 512, 128, fake, 1024, 128, 512,
+                                256, 2, 4, 8, None) != 0
+    assert b"head_dim" in lib.vdn_last_error()

@@ -237,3 +237,22 @@ def test_short_conv_temporal_loop_of_the_reference_test():
     expected = F.silu(acc).reshape(frames, fh * fw, h, d).permute(0, 2, 1, 3)
     got = ov.short_conv_prepare(tokens.bfloat16().double(), frames, fh, fw, w_sp, w_tm, False)
     torch.testing.assert_close(got, expected, atol=1e-12, rtol=1e-12)
+
+
+@pytest.mark.parametrize("d", [16, 64])
+def test_paper_branch_oracle_small_head_dim_matches_eager(d):
+    """The bf16-path oracle at head dims below 128 (the reference's eager body takes any d,
+    delta_rule.py:45-60) against the float64 eager body on the same bf16 inputs."""
+    frames, spatial, h = 4, 9, 2
+    g = torch.Generator().manual_seed(d)
+    raw = [ov.bf16(torch.randn(frames * spatial, h, d, generator=g)) for _ in range(3)]
+    beta = ov.bf16(torch.rand(frames * spatial, h, generator=g))
+    gate = ov.bf16(torch.rand(frames * spatial, h, d, generator=g))
+    alpha = torch.rand(frames, h, d, generator=g) * 0.2 + 0.8
+    w = torch.rand(d, generator=g) + 0.5
+    bounds = ov.window_bounds(frames, 1)
+    out, _ = ov.paper_branch(*raw, beta, gate, alpha, bounds, frames, spatial, w, 1e-6)
+    ref = ov.eager_branch_fp64(*raw, beta, gate, alpha, bounds, frames, spatial, w)
+    assert out.shape == (frames * spatial, h * d)
+    rel = (out - ref).norm() / ref.norm()
+    assert rel < 4e-3, rel.item()

@@ -44,9 +44,9 @@ SIGNATURES = {
     "vdn_vda_gather": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i32, _i32,
                        _i32, _i32, _ptr, _ptr],
     "vdn_vda_readout": [_ptr, _i64, _i64, _i64, _i32, _ptr, _ptr, _i32, _f32, _ptr, _i64, _i64,
-                        _i64, _ptr, _i64, _i64, _i64, _i32, _i32, _i32, _ptr],
+                        _i64, _ptr, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _ptr],
     "vdn_vda_epilogue": [_ptr, _ptr, _i32, _f32, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64,
-                         _i32, _i32, _i32, _ptr],
+                         _i32, _i32, _i32, _i32, _ptr],
     "vdn_qk_rmsnorm_rope": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _ptr,
                             _i64, _f32, _ptr, _i64, _i64, _ptr, _i64, _i64, _i32, _i32, _i64,
                             _i32, _i32, _ptr, _ptr, _ptr],

@@ -851,13 +851,15 @@ struct MxDst {
 };
 
 // RMSNorm(y)·w·gate of one lane's 8 values, rounded to bf16 (as stored by the bf16 form).
+// inv_dim = 1 / head_dim, a power of two: rows are 128 wide, channels past head_dim hold
+// zeros, and the mean of squares is over head_dim channels.
 __device__ __forceinline__ void norm_gate8(const float* y, const float* w, const u32x4 graw,
-                                           float eps, float* o) {
+                                           float eps, float inv_dim, float* o) {
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) ss += y[i] * y[i];
   ss = sum16(ss);
-  const float inv = 1.0f / sqrtf(ss / static_cast<float>(kD) + eps);
+  const float inv = 1.0f / sqrtf(ss * inv_dim + eps);
   float gv[8];
   unpack8(graw, gv);
 #pragma unroll
@@ -865,9 +867,9 @@ __device__ __forceinline__ void norm_gate8(const float* y, const float* w, const
 }
 
 __device__ __forceinline__ void norm_gate_store8(float* y, const float* w, const uint16_t* gsrc,
-                                                 uint16_t* dst, float eps) {
+                                                 uint16_t* dst, float eps, float inv_dim) {
   float o[8];
-  norm_gate8(y, w, *reinterpret_cast<const u32x4*>(gsrc), eps, o);
+  norm_gate8(y, w, *reinterpret_cast<const u32x4*>(gsrc), eps, inv_dim, o);
   *reinterpret_cast<u32x4*>(dst) = pack8(o);
 }
 
@@ -951,7 +953,8 @@ __device__ __forceinline__ void ro_load(const View& qv, const View& gv, const Ga
 template <bool kMx, bool kProj>
 __global__ void __launch_bounds__(kRoThreads) __attribute__((amdgpu_waves_per_eu(4)))
 vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
-                   const void* __restrict__ weight, int weight_f32, float eps, View gv,
+                   const void* __restrict__ weight, int weight_f32, float eps, float inv_dim,
+                   View gv,
                    GateProj gp, uint16_t* __restrict__ out, int64_t o_sf, int64_t o_sh,
                    int64_t o_ss, int spatial, int heads, int parts, MxDst mx) {
   __shared__ __attribute__((aligned(16))) uint16_t sState[kD * kQRow];     // [ro_row(c)][k]
@@ -1064,7 +1067,7 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
 #pragma unroll
       for (int v = 0; v < 4; ++v) ss += ay[mt][v] * ay[mt][v];
     }
-    const float inv = 1.0f / sqrtf(sum_quad_rows(ss) / static_cast<float>(kD) + eps);
+    const float inv = 1.0f / sqrtf(sum_quad_rows(ss) * inv_dim + eps);
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
       const f32x4 w = *reinterpret_cast<const f32x4*>(&sW[mt * 16 + g * 4]);
@@ -1129,7 +1132,8 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
 // Epilogue alone (vdn_linear_epilogue): readout [F, H, S, D] bf16 -> out [F*S, H*D].
 __global__ void __launch_bounds__(256)
 vda_epilogue_kernel(const uint16_t* __restrict__ readout, const void* __restrict__ weight,
-                    int weight_f32, float eps, View gv, uint16_t* __restrict__ out,
+                    int weight_f32, float eps, float inv_dim, View gv,
+                    uint16_t* __restrict__ out,
                     int64_t o_sf, int64_t o_sh, int64_t o_ss, int frames, int heads,
                     int spatial) {
   const int lane16 = threadIdx.x & 15;
@@ -1145,10 +1149,11 @@ vda_epilogue_kernel(const uint16_t* __restrict__ readout, const void* __restrict
     w[i] = weight_f32 ? static_cast<const float*>(weight)[lane16 * 8 + i]
                       : bf16_bits_to_f32(static_cast<const uint16_t*>(weight)[lane16 * 8 + i]);
   norm_gate_store8(y, w, gv.at(f, h, s) + lane16 * 8,
-                   out + f * o_sf + h * o_sh + s * o_ss + lane16 * 8, eps);
+                   out + f * o_sf + h * o_sh + s * o_ss + lane16 * 8, eps, inv_dim);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+bool valid_head_dim(int d) { return d == 16 || d == 32 || d == 64 || d == 128; }
 bool stride8(int64_t s) { return s % 8 == 0; }
 
 }  // namespace
@@ -1331,7 +1336,9 @@ VDN_API int vdn_vda_gather(const float* prefix, const float* suffix, const float
 // Fused readout (paper_stack.py:317 torch.matmul + paper_sglang.py:377-437 epilogue), with
 // the q activation of paper_prepare applied in registers when activate_q = 1.
 // q: (f, h, s, c) at q + f*q_sf + h*q_sh + s*q_ss + c; gate likewise; out likewise.
-// state: bf16 [F, H, 128, 128] ([v][k]); weight [128] bf16 or fp32.
+// state: bf16 [F, H, 128, 128] ([v][k]); weight [128] bf16 or fp32. head_dim < 128 (16, 32,
+// 64): rows stay 128 wide with zeros past head_dim in q and state (and in the weight, so
+// those output channels are zero), and the norm's mean is over head_dim channels.
 namespace vdn {
 namespace {
 
@@ -1339,12 +1346,17 @@ int launch_readout(const char* name, const void* q, int64_t q_sf, int64_t q_sh, 
                    int activate_q, const void* state, const void* weight, int weight_f32,
                    float eps, const void* gate, int64_t g_sf, int64_t g_sh, int64_t g_ss,
                    const GateProj* gp, void* out, int64_t o_sf, int64_t o_sh, int64_t o_ss,
-                   const MxDst* mx, int frames, int heads, int spatial, void* stream) {
+                   const MxDst* mx, int head_dim, int frames, int heads, int spatial,
+                   void* stream) {
   if (q == nullptr || state == nullptr || weight == nullptr ||
       (gp == nullptr && gate == nullptr) || (mx == nullptr && out == nullptr))
     return set_error(kInvalidArgument, "%s: null pointer", name);
   if (frames <= 0 || heads <= 0 || spatial <= 0)
     return set_error(kInvalidArgument, "%s: bad geometry", name);
+  if (!valid_head_dim(head_dim) || ((gp != nullptr || mx != nullptr) && head_dim != kD))
+    return set_error(kInvalidArgument,
+                     "%s: head_dim must be 16, 32, 64 or 128 (128 with an MXFP8 destination "
+                     "or a formed gate)", name);
   if (!aligned16(q) || !aligned16(state) || !stride8(q_sf) || !stride8(q_sh) ||
       !stride8(q_ss) ||
       (gp == nullptr &&
@@ -1385,7 +1397,8 @@ int launch_readout(const char* name, const void* q, int64_t q_sf, int64_t q_sh, 
   auto* op = static_cast<uint16_t*>(out);
 #define VDN_READOUT(MX, PROJ)                                                                  \
   hipLaunchKernelGGL((vda_readout_kernel<MX, PROJ>), grid, block, 0, st, qv, activate_q, sp,   \
-                     weight, weight_f32, eps, gv, g, op, o_sf, o_sh, o_ss, spatial, heads,      \
+                     weight, weight_f32, eps, 1.0f / head_dim, gv, g, op, o_sf, o_sh, o_ss,     \
+                     spatial, heads,                                                            \
                      parts, m)
   if (mx != nullptr && gp != nullptr)
     VDN_READOUT(true, true);
@@ -1405,11 +1418,11 @@ int launch_readout(const char* name, const void* q, int64_t q_sf, int64_t q_sh, 
 VDN_API int vdn_vda_readout(const void* q, int64_t q_sf, int64_t q_sh, int64_t q_ss,
                             int activate_q, const void* state, const void* weight, int weight_f32,
                             float eps, const void* gate, int64_t g_sf, int64_t g_sh, int64_t g_ss,
-                            void* out, int64_t o_sf, int64_t o_sh, int64_t o_ss, int frames,
-                            int heads, int spatial, void* stream) {
+                            void* out, int64_t o_sf, int64_t o_sh, int64_t o_ss, int head_dim,
+                            int frames, int heads, int spatial, void* stream) {
   return launch_readout("vdn_vda_readout", q, q_sf, q_sh, q_ss, activate_q, state, weight,
                         weight_f32, eps, gate, g_sf, g_sh, g_ss, nullptr, out, o_sf, o_sh, o_ss,
-                        nullptr, frames, heads, spatial, stream);
+                        nullptr, head_dim, frames, heads, spatial, stream);
 }
 
 // The same readout with the output quantized in the epilogue: token row f * S + s, head h ->
@@ -1426,7 +1439,7 @@ VDN_API int vdn_vda_readout_mxfp8(const void* q, int64_t q_sf, int64_t q_sh, int
   const MxDst mx{static_cast<uint8_t*>(codes), static_cast<uint8_t*>(scales), kp, chunk0};
   return launch_readout("vdn_vda_readout_mxfp8", q, q_sf, q_sh, q_ss, activate_q, state,
                         weight, weight_f32, eps, gate, g_sf, g_sh, g_ss, nullptr, nullptr, 0, 0,
-                        0, &mx, frames, heads, spatial, stream);
+                        0, &mx, kD, frames, heads, spatial, stream);
 }
 
 // The readout with the linear branch's low-rank output gate formed in the kernel:
@@ -1451,25 +1464,28 @@ VDN_API int vdn_vda_readout_gated(const void* q, int64_t q_sf, int64_t q_sh, int
   const MxDst mx{static_cast<uint8_t*>(codes), static_cast<uint8_t*>(scales), kp, chunk0};
   return launch_readout("vdn_vda_readout_gated", q, q_sf, q_sh, q_ss, activate_q, state,
                         weight, weight_f32, eps, nullptr, 0, 0, 0, &gp, out, o_sf, o_sh, o_ss,
-                        codes != nullptr ? &mx : nullptr, frames, heads, spatial, stream);
+                        codes != nullptr ? &mx : nullptr, kD, frames, heads, spatial, stream);
 }
 
 // Reference: paper_sglang.py:377-437 (_linear_epilogue_kernel / vdn_linear_epilogue):
 // readout [F, H, S, 128] bf16 contiguous -> RMSNorm(d)·w·gate -> out.
 VDN_API int vdn_vda_epilogue(const void* readout, const void* weight, int weight_f32, float eps,
                              const void* gate, int64_t g_sf, int64_t g_sh, int64_t g_ss,
-                             void* out, int64_t o_sf, int64_t o_sh, int64_t o_ss, int frames,
-                             int heads, int spatial, void* stream) {
+                             void* out, int64_t o_sf, int64_t o_sh, int64_t o_ss, int head_dim,
+                             int frames, int heads, int spatial, void* stream) {
   const char* name = "vdn_vda_epilogue";
   if (readout == nullptr || weight == nullptr || gate == nullptr || out == nullptr)
     return set_error(kInvalidArgument, "%s: null pointer", name);
   if (frames <= 0 || heads <= 0 || spatial <= 0)
     return set_error(kInvalidArgument, "%s: bad geometry", name);
+  if (!valid_head_dim(head_dim))
+    return set_error(kInvalidArgument, "%s: head_dim must be 16, 32, 64 or 128", name);
   const int64_t items = static_cast<int64_t>(frames) * heads * spatial;
   const View gv{static_cast<const uint16_t*>(gate), g_sf, g_sh, g_ss};
   hipLaunchKernelGGL(vda_epilogue_kernel, dim3(static_cast<unsigned>((items + 15) / 16)),
                      dim3(256), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t*>(readout), weight, weight_f32, eps, gv,
+                     static_cast<const uint16_t*>(readout), weight, weight_f32, eps,
+                     1.0f / head_dim, gv,
                      static_cast<uint16_t*>(out), o_sf, o_sh, o_ss, frames, heads, spatial);
   return check_launch(name);
 }

@@ -23,6 +23,38 @@ from . import _lib
 from .mxfp8 import mxfp8_destination
 
 HEAD_DIM = 128
+# Head dims the branch accepts. The kernels work on 128-wide rows; a smaller head dim runs
+# with its channels zero-padded to 128, which is exact: SiLU(0) = 0 and zeros add nothing to
+# the L2 norms, to A = Kᵀ diag(β) K and B = (vβ)ᵀ K (whose padded rows and columns are zero,
+# so (I + A)⁻¹ is block diagonal with an identity block), to the scans and gathers (the
+# state's padded rows and columns stay zero), and to the readout, whose RMSNorm takes its
+# mean over the true head dim.
+HEAD_DIMS = (16, 32, 64, 128)
+
+
+def _check_head_dim(d):
+    if d not in HEAD_DIMS:
+        raise ValueError(f"head_dim must be one of {HEAD_DIMS}, got {d}")
+
+
+def _pad_channels(x, value=0.0):
+    """[..., d] -> [..., 128] with `value` in the added channels (x itself when d = 128)."""
+    d = x.shape[-1]
+    if d == HEAD_DIM:
+        return x
+    out = x.new_full((*x.shape[:-1], HEAD_DIM), value)
+    out[..., :d] = x
+    return out
+
+
+def _pad_square(x):
+    """[..., d, d] -> [..., 128, 128] zero-padded (x itself when d = 128)."""
+    d = x.shape[-1]
+    if d == HEAD_DIM:
+        return x
+    out = x.new_zeros((*x.shape[:-2], HEAD_DIM, HEAD_DIM))
+    out[..., :d, :d] = x
+    return out
 
 
 def _cuda(t, name, dtype=None):
@@ -99,12 +131,14 @@ def paper_prepare(tokens, *, frames, spatial, l2norm, conv=None, proj=None, fram
     if tokens.ndim != 3 or tokens.shape[0] != frames * spatial or min(frames, spatial) < 1:
         raise ValueError("tokens must be [frames*spatial, heads, dim] with positive sizes")
     n, h, d = tokens.shape
-    if d != HEAD_DIM:
-        raise ValueError("head_dim 128 required")
+    _check_head_dim(d)
     if conv is not None and proj in getattr(conv, "projs", ()):
+        if d != HEAD_DIM:
+            raise NotImplementedError("the gfx950 short-conv kernel takes head_dim 128")
         return _conv_prepare(tokens, frames, spatial, l2norm, conv, proj, frame_size)
     if d != HEAD_DIM:
-        raise ValueError("head_dim 128 required")
+        out = paper_prepare(_pad_channels(tokens), frames=frames, spatial=spatial, l2norm=l2norm)
+        return out[..., :d].contiguous()
     if tokens.stride(-1) != 1:
         tokens = tokens.contiguous()
     out = torch.empty((frames, h, spatial, d), dtype=tokens.dtype, device=tokens.device)
@@ -143,8 +177,11 @@ def paper_statistics(key, value, beta):
     f, h, s, d = key.shape
     if min(f, h, s) < 1 or d not in (16, 32, 64, 128):
         raise ValueError("positive F,H,S and D in 16,32,64,128 required")
-    if d != HEAD_DIM or key.dtype != torch.bfloat16:
-        raise NotImplementedError("the gfx950 statistics kernel takes bf16 K/V with D = 128")
+    if key.dtype != torch.bfloat16:
+        raise NotImplementedError("the gfx950 statistics kernel takes bf16 K/V")
+    if d != HEAD_DIM:
+        a, b = paper_statistics(_pad_channels(key), _pad_channels(value), beta)
+        return a[..., :d, :d].contiguous(), b[..., :d, :d].contiguous()
     ks = (h * s * d, s * d, d)
     bs = (h * s, s, 1)
     return _stats_call(key, ks, value, ks, beta, bs, f, h, s, 0)
@@ -291,8 +328,6 @@ def paper_boundary_scan(transitions, injections, plan, text_state=None):
     f, h, d, dk = transitions.shape
     if f != plan.frames or d != dk or d not in (16, 32, 64, 128) or h < 1:
         raise ValueError("factor geometry incompatible with boundary plan")
-    if d != HEAD_DIM:
-        raise NotImplementedError("the gfx950 scan kernel takes D = 128")
     if plan.starts.device != transitions.device:
         raise ValueError("plan and factors must share a device")
     if text_state is not None:
@@ -300,6 +335,10 @@ def paper_boundary_scan(transitions, injections, plan, text_state=None):
         if text_state.shape != (h, d, d) or text_state.device != transitions.device:
             raise ValueError("text_state must be head-local H,D,D")
         text_state = text_state.contiguous()
+    if d != HEAD_DIM:
+        bank = paper_boundary_scan(_pad_square(transitions), _pad_square(injections), plan,
+                                   None if text_state is None else _pad_square(text_state))
+        return bank[..., :d, :d].contiguous()
     shape = (2, plan.chunks, h, d, d)
     bank = transitions.new_empty(shape)
     stream = _stream(transitions)
@@ -331,13 +370,17 @@ def paper_gather(bank, alpha, plan, text_state=None, out_dtype=torch.bfloat16, b
             or alpha.device != bank.device or plan.starts.device != bank.device
             or out_dtype not in (torch.bfloat16, torch.float32)):
         raise ValueError("gather geometry/device/dtype mismatch")
-    if d != HEAD_DIM:
-        raise NotImplementedError("the gfx950 gather kernel takes D = 128")
     if text_state is not None:
         _cuda(text_state, "text_state", torch.float32)
         if text_state.shape != (h, d, d) or text_state.device != bank.device:
             raise ValueError("text_state geometry/device mismatch")
         text_state = text_state.contiguous()
+    if d != HEAD_DIM:
+        _check_head_dim(d)
+        out = paper_gather(_pad_square(bank), _pad_channels(alpha, 1.0), plan,
+                           None if text_state is None else _pad_square(text_state), out_dtype,
+                           bridge)
+        return out[..., :d, :d].contiguous()
     alpha = alpha.contiguous()
     stream = _stream(bank)
     logp = None
@@ -357,8 +400,17 @@ def paper_gather(bank, alpha, plan, text_state=None, out_dtype=torch.bfloat16, b
 
 def _weight_flag(w):
     if w.dtype not in (torch.bfloat16, torch.float32) or w.shape != (HEAD_DIM,):
-        raise ValueError("norm weight must be [128] bf16 or fp32")
+        raise ValueError("norm weight must be [head_dim] bf16 or fp32")
     return int(w.dtype == torch.float32)
+
+
+def _norm_weight(norm_weight, d, device):
+    """The norm weight as the kernels read it: [128] on `device`, zero past the head dim (so
+    the padded output channels are zero)."""
+    w = norm_weight.to(device=device)
+    if w.shape != (d,):
+        raise ValueError("norm weight must be [head_dim] bf16 or fp32")
+    return _pad_channels(w).contiguous()
 
 
 def vdn_linear_epilogue(readout, norm_weight, gate, eps):
@@ -366,18 +418,20 @@ def vdn_linear_epilogue(readout, norm_weight, gate, eps):
     (paper_sglang.py:406-437)."""
     _cuda(readout, "readout", torch.bfloat16)
     f, h, s, d = readout.shape
-    if d != HEAD_DIM:
-        raise ValueError("head_dim 128 required")
-    readout = readout.contiguous()
+    _check_head_dim(d)
     gate = gate.reshape(f * s, h, d).to(readout.dtype)
+    w = _norm_weight(norm_weight, d, readout.device)
+    readout = _pad_channels(readout).contiguous()
+    gate = _pad_channels(gate)
     if gate.stride(-1) != 1:
         gate = gate.contiguous()
-    w = norm_weight.to(device=readout.device).contiguous()
-    out = torch.empty((f * s, h * d), dtype=readout.dtype, device=readout.device)
+    out = torch.empty((f * s, h * HEAD_DIM), dtype=readout.dtype, device=readout.device)
     gs = (s * gate.stride(0), gate.stride(1), gate.stride(0))
-    os_ = (s * out.stride(0), d, out.stride(0))
+    os_ = (s * out.stride(0), HEAD_DIM, out.stride(0))
     _lib.call("vdn_vda_epilogue", readout.data_ptr(), w.data_ptr(), _weight_flag(w), float(eps),
-              gate.data_ptr(), *gs, out.data_ptr(), *os_, f, h, s, _stream(readout))
+              gate.data_ptr(), *gs, out.data_ptr(), *os_, d, f, h, s, _stream(readout))
+    if d != HEAD_DIM:
+        out = out.view(f * s, h, HEAD_DIM)[..., :d].reshape(f * s, h * d)
     return out
 
 
@@ -425,7 +479,7 @@ def _q_view(q, frames, spatial):
 
 
 def linear_readout(q, state, norm_weight, gate, eps, frames, spatial, *, activate_q=True,
-                   out=None, out_mxfp8=None):
+                   out=None, out_mxfp8=None, head_dim=HEAD_DIM):
     """Fused q activation + readout + epilogue.
 
     q: raw [F*S, H, D] bf16 (any row/head stride), or prepared q (token-major, or frame-major
@@ -433,6 +487,9 @@ def linear_readout(q, state, norm_weight, gate, eps, frames, spatial, *, activat
     state: [F, H, D, D] bf16 from paper_gather; gate [F*S, H, D] bf16, or an
     OutputGateProjection, which the kernel turns into that gate itself.
     Returns (or writes into `out`) [F*S, H*D] bf16 = RMSNorm(bf16(q'·stateᵀ))·w·gate.
+    D may be 16, 32, 64 or 128 (a smaller D runs zero-padded to 128 with an explicit gate
+    and a bf16 destination). `head_dim` is internal: with 128-wide operands whose channels
+    past it are zero, it sets the norm's mean to that many channels.
     `out_mxfp8` = (codes, scales, chunk0) instead quantizes the result in the kernel: head h of
     row r becomes chunk chunk0 + h of row r of an MXFP8 activation (empty_activation),
     byte-identical to quantize_activation of the bf16 result; returns None then.
@@ -441,8 +498,11 @@ def linear_readout(q, state, norm_weight, gate, eps, frames, spatial, *, activat
     _cuda(state, "state", torch.bfloat16)
     q, qs = _q_view(q, frames, spatial)
     n, h, d = frames * spatial, q.shape[-3] if q.ndim == 4 else q.shape[1], q.shape[-1]
-    if d != HEAD_DIM or state.shape != (frames, h, d, d):
+    if d not in HEAD_DIMS or state.shape != (frames, h, d, d):
         raise ValueError("readout geometry mismatch")
+    if d != HEAD_DIM:
+        return _padded_readout(q, state, norm_weight, gate, eps, frames, spatial, activate_q,
+                               out, out_mxfp8)
     if isinstance(gate, OutputGateProjection):
         return _gated_readout(q, state, norm_weight, gate, eps, frames, spatial, activate_q,
                               out, out_mxfp8)
@@ -468,7 +528,29 @@ def linear_readout(q, state, norm_weight, gate, eps, frames, spatial, *, activat
     os_ = (spatial * out.stride(0), d, out.stride(0))
     _lib.call("vdn_vda_readout", q.data_ptr(), *qs, int(bool(activate_q)), state.data_ptr(),
               w.data_ptr(), _weight_flag(w), float(eps), gate.data_ptr(), *gs, out.data_ptr(),
-              *os_, frames, h, spatial, _stream(q))
+              *os_, head_dim, frames, h, spatial, _stream(q))
+    return out
+
+
+def _padded_readout(q, state, norm_weight, gate, eps, frames, spatial, activate_q, out,
+                    out_mxfp8):
+    """linear_readout at head_dim d < 128: q, state, gate and the norm weight zero-padded to
+    the kernel's 128 channels, the norm's mean over d, the output's first d channels kept."""
+    n, h, d = frames * spatial, state.shape[1], state.shape[-1]
+    if isinstance(gate, OutputGateProjection) or out_mxfp8 is not None:
+        raise ValueError("the formed output gate and the MXFP8 destination take head_dim 128")
+    _cuda(gate, "gate", torch.bfloat16)
+    if gate.shape != (n, h, d):
+        raise ValueError("readout geometry mismatch")
+    if out is not None and (out.shape != (n, h * d) or out.dtype != torch.bfloat16):
+        raise ValueError("out must be bf16 [F*S, H*D]")
+    w = _norm_weight(norm_weight, d, q.device)
+    full = linear_readout(_pad_channels(q), _pad_square(state), w, _pad_channels(gate), eps,
+                          frames, spatial, activate_q=activate_q, head_dim=d)
+    full = full.view(n, h, HEAD_DIM)[..., :d].reshape(n, h * d)
+    if out is None:
+        return full
+    out.copy_(full)
     return out
 
 
@@ -501,7 +583,7 @@ def _gated_readout(q, state, norm_weight, gp, eps, frames, spatial, activate_q, 
 
 def vda_forward(q_raw, k_raw, v_raw, beta, gate, alpha, bounds, num_frames, tokens_per_frame,
                 norm_weight, eps, *, chunk_size=8, bridge=True, text=None, out=None,
-                out_mxfp8=None, conv=None, frame_size=None):
+                out_mxfp8=None, conv=None, frame_size=None, _head_dim=HEAD_DIM):
     """The paper VDA branch body on raw projections (paper_stack.py:266-318).
 
     q_raw/k_raw/v_raw: [F*S, H, 128] bf16 raw projections; beta [F*S, H]; gate [F*S, H, 128]
@@ -510,7 +592,34 @@ def vda_forward(q_raw, k_raw, v_raw, beta, gate, alpha, bounds, num_frames, toke
     both scans). `conv` (a LinearAttentionSepConv, frame_size = (H_f, W_f)) convolves the
     projections it lists before their activation; the prompt's tokens are not convolved.
     `out` / `out_mxfp8` as in linear_readout.
+    A head dim of 16, 32 or 64 (the reference's eager body, delta_rule.py:45-60) runs with
+    every operand's channels zero-padded to 128 (alpha padded with ones), which is exact; it
+    takes an explicit gate, a bf16 destination and no short conv.
     """
+    d = q_raw.shape[-1]
+    if d != HEAD_DIM:
+        _check_head_dim(d)
+        n, h = q_raw.shape[:2]
+        if (k_raw.shape[-1] != d or v_raw.shape[-1] != d or alpha.shape[-1] != d
+                or (not isinstance(gate, OutputGateProjection) and gate.shape[-1] != d)):
+            raise ValueError("q, k, v, gate and alpha must share the head dim")
+        if isinstance(gate, OutputGateProjection) or out_mxfp8 is not None or conv is not None:
+            raise ValueError("head_dim < 128 takes an explicit gate, a bf16 destination and no "
+                             "short conv")
+        if out is not None and (out.shape != (n, h * d) or out.dtype != torch.bfloat16):
+            raise ValueError("out must be bf16 [F*S, H*D]")
+        if text is not None:
+            text = (_pad_channels(text[0]), _pad_channels(text[1]), text[2])
+        w = _norm_weight(norm_weight, d, q_raw.device)
+        full = vda_forward(_pad_channels(q_raw), _pad_channels(k_raw), _pad_channels(v_raw),
+                           beta, _pad_channels(gate), _pad_channels(alpha, 1.0).contiguous(),
+                           bounds, num_frames, tokens_per_frame, w, eps, chunk_size=chunk_size,
+                           bridge=bridge, text=text, _head_dim=d)
+        full = full.view(n, h, HEAD_DIM)[..., :d].reshape(n, h * d)
+        if out is None:
+            return full
+        out.copy_(full)
+        return out
     f, s = num_frames, tokens_per_frame
     h = q_raw.shape[1]
     device = q_raw.device
@@ -552,7 +661,7 @@ def vda_forward(q_raw, k_raw, v_raw, beta, gate, alpha, bounds, num_frames, toke
         return linear_readout(q, state, norm_weight, gate, eps, f, s, activate_q=False, out=out,
                               out_mxfp8=out_mxfp8)
     return linear_readout(q_raw, state, norm_weight, gate, eps, f, s, out=out,
-                          out_mxfp8=out_mxfp8)
+                          out_mxfp8=out_mxfp8, head_dim=_head_dim)
 
 
 def paper_readout(branch, xv, num_frames, tokens_per_frame, bounds, qkv_raw, frame_size=None,
