@@ -290,6 +290,10 @@ int vdn_window_attention(const void* q, int64_t q_st, int64_t q_sh, const void* 
  * matrix and the four E8M0 scales of that chunk in its SWIZZLE_32_4_4 scale array; the same
  * bytes vdn_mxfp8_quantize writes for the bf16 output. Rows without a query are not written.
  * codes 16-byte aligned, kp a multiple of 128 with (chunk0 + heads) * 128 <= kp.
+ * q_norm_w (nullable, 16-byte aligned): [128] bf16 weight of an RMSNorm applied to each
+ * (query, head) row as it is loaded, n = bf16((x * (1 / sqrt(mean(x^2) + q_norm_eps))) * w),
+ * bit-identical to vdn_qk_rmsnorm_rope's norm of the queries (the QK norm of
+ * src/models/softmax_attention/paper_qk_rope.py:82-95) followed by this entry point.
  * Replaces: paper_window_attention (src/models/softmax_attention/paper_window.py:182-243)
  * followed by quantize_activation (src/models/ops/mxfp8_quant.py:77-90) of its output.
  */
@@ -297,7 +301,8 @@ int vdn_window_attention_mxfp8(const void* q, int64_t q_st, int64_t q_sh, const 
                                int64_t k_st, int64_t k_sh, const void* v, int64_t v_st,
                                int64_t v_sh, const int* blocks, int nblocks, const int* grp_kv,
                                const int* grp_n, int heads, float scale, const void* gate,
-                               int64_t g_st, int64_t g_sh, void* codes, void* scales, int64_t kp,
+                               int64_t g_st, int64_t g_sh, const void* q_norm_w,
+                               float q_norm_eps, void* codes, void* scales, int64_t kp,
                                int chunk0, void* stream);
 
 /*

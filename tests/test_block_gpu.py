@@ -156,3 +156,28 @@ def test_rope_tables_match_the_oracle_restatement():
     oc, os_ = ow.rope_tables_3d(3, 5, 7)
     assert torch.allclose(cos.cpu().double(), oc, atol=1e-6)
     assert torch.allclose(sin.cpu().double(), os_, atol=1e-6)
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("w_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("rows", [300, 1037])
+def test_cross_attention_query_norm_in_kernel_equals_norm_pass(w_dtype, rows):
+    """The queries' RMSNorm fused into the MXFP8-output attention gives the same codes and
+    scales as qk_rmsnorm followed by the attention (partial last query blocks included)."""
+    from vdn_amd import mxfp8 as vm
+    from vdn_amd.block import cross_attention
+    g = torch.Generator().manual_seed(rows)
+    heads, d, ctx = 3, 128, 77
+    q = (torch.randn(rows, heads, d, generator=g) * 3).bfloat16().cuda()
+    k = torch.randn(ctx, heads, d, generator=g).bfloat16().cuda()
+    v = torch.randn(ctx, heads, d, generator=g).bfloat16().cuda()
+    w = (torch.rand(d, generator=g) + 0.5).to(w_dtype).cuda()
+    plan = cross_attention_plan(rows, ctx, "cuda")
+    qa, sa = vm.empty_activation(rows, heads * d, "cuda")
+    qb, sb = vm.empty_activation(rows, heads * d, "cuda")
+    cross_attention(q, k, v, plan, d ** -0.5, out_mxfp8=(qa, sa, 0), q_norm=(w, 1e-6))
+    cross_attention(vw.qk_rmsnorm(q, w, 1e-6), k, v, plan, d ** -0.5, out_mxfp8=(qb, sb, 0))
+    torch.cuda.synchronize()
+    assert torch.equal(qa, qb) and torch.equal(sa, sb)
+    with pytest.raises(ValueError, match="MXFP8-output form"):
+        cross_attention(q, k, v, plan, d ** -0.5, q_norm=(w, 1e-6))

@@ -54,8 +54,8 @@ SIGNATURES = {
                              _ptr, _ptr, _i32, _i32, _f32, _ptr, _i64, _i64, _ptr, _i64, _i64,
                              _ptr, _i64, _i64, _ptr],
     "vdn_window_attention_mxfp8": [_ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr,
-                                   _i32, _ptr, _ptr, _i32, _f32, _ptr, _i64, _i64, _ptr, _ptr,
-                                   _i64, _i32, _ptr],
+                                   _i32, _ptr, _ptr, _i32, _f32, _ptr, _i64, _i64, _ptr, _f32,
+                                   _ptr, _ptr, _i64, _i32, _ptr],
     "vdn_vda_readout_mxfp8": [_ptr, _i64, _i64, _i64, _i32, _ptr, _ptr, _i32, _f32, _ptr, _i64,
                               _i64, _i64, _ptr, _ptr, _i64, _i32, _i32, _i32, _i32, _ptr],
     "vdn_vda_readout_gated": [_ptr, _i64, _i64, _i64, _i32, _ptr, _ptr, _i32, _f32, _ptr, _i64,

@@ -392,12 +392,14 @@ class HybridDiTBlock(nn.Module):
         L = context.shape[0]
         ck = self.ck.forward_quantized(cx, csx, rows=L).view(L, heads, d)
         cv = self.cv.forward_quantized(cx, csx, rows=L).view(L, heads, d)
-        cq = vw.qk_rmsnorm(cq, k["norm_qc"], cfg.eps)
         ck = vw.qk_rmsnorm(ck, k["norm_kc"], cfg.eps)
         if parts is None:
+            # the queries' RMSNorm runs in the attention kernel as it loads them
             qo, so = mx.empty_activation(T, inner, dev)
-            cross_attention(cq, ck, cv, cross_plan, d ** -0.5, out_mxfp8=(qo, so, 0))
+            cross_attention(cq, ck, cv, cross_plan, d ** -0.5, out_mxfp8=(qo, so, 0),
+                            q_norm=(k["norm_qc"], cfg.eps))
         else:
+            cq = vw.qk_rmsnorm(cq, k["norm_qc"], cfg.eps)
             co = cross_attention(cq, ck, cv, cross_plan, d ** -0.5)
             snap("co", co.view(T, inner))
             qo, so = mx.launch_quantize(co.view(T, inner))
@@ -423,19 +425,30 @@ def cross_attention_plan(num_queries: int, num_keys: int, device) -> vw.DevicePl
     return vw._device_plan([(((0, num_queries),), ((0, num_keys),))], torch.device(device))
 
 
-def cross_attention(q, k, v, plan: vw.DevicePlan, scale, out_mxfp8=None):
+def cross_attention(q, k, v, plan: vw.DevicePlan, scale, out_mxfp8=None, q_norm=None):
     """Unmasked attention of q [T, H, D] over context k, v [L, H, D] on the window kernel.
     `out_mxfp8` = (codes, scales, chunk0): quantize the output in the kernel (head h -> chunk
-    chunk0 + h) instead of returning bf16 [T, H, D]."""
+    chunk0 + h) instead of returning bf16 [T, H, D]. With it, `q_norm` = (weight [D], eps)
+    applies the queries' RMSNorm (vw.qk_rmsnorm) first, in the kernel as it loads them for a
+    bf16 weight (the same bits as the separate pass), else as that pass."""
     from . import _lib
     T, h, d = q.shape
+    if q_norm is not None and out_mxfp8 is None:
+        raise ValueError("q_norm is fused into the MXFP8-output form only")
     if out_mxfp8 is not None:
         codes, scales, chunk0 = mx.mxfp8_destination(out_mxfp8, T, h, q.device)
+        qw, qeps = (None, 0.0) if q_norm is None else q_norm
+        if qw is not None:
+            if qw.shape != (d,) or qw.device != q.device:
+                raise ValueError("q_norm weight must be a [head_dim] tensor on q's device")
+            if qw.dtype != torch.bfloat16 or qw.data_ptr() % 16:
+                q, qw = vw.qk_rmsnorm(q, qw, qeps), None
         _lib.call("vdn_window_attention_mxfp8", q.data_ptr(), q.stride(0), q.stride(1),
                   k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
                   plan.blocks.data_ptr(), plan.nblocks, plan.intervals.data_ptr(),
-                  plan.counts.data_ptr(), h, float(scale), None, 0, 0, codes.data_ptr(),
-                  scales.data_ptr(), codes.shape[1], chunk0, _lib.stream(q.device))
+                  plan.counts.data_ptr(), h, float(scale), None, 0, 0, _lib.ptr(qw),
+                  float(qeps), codes.data_ptr(), scales.data_ptr(), codes.shape[1], chunk0,
+                  _lib.stream(q.device))
         return None
     out = torch.empty_like(q)
     _lib.call("vdn_window_attention", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),

@@ -80,6 +80,57 @@ struct MxDst {
   int chunk0;
 };
 
+// RMSNorm of the queries applied as they are loaded (w == nullptr: none): n = bf16((x * (1 /
+// sqrt(sum(x^2) / 128 + eps))) * w) per (query, head) row, w [128] bf16.
+struct QNorm {
+  const uint16_t* w;
+  float eps;
+};
+
+// The query RMSNorm of qk_rope_row128_kernel (the QK norm of paper_qk_rope.py:82-95, D = 128)
+// on this kernel's Q fragments, bit for bit: lane (col, g) holds the 8-channel chunks
+// c = 2 ks + g of its query row and lane ^ 32 the chunks of the other parity. Each chunk's sum
+// of squares runs in channel order as one lane of the norm kernel does; the pair of chunks
+// (2 ks, 2 ks + 1) is added across the two lanes and the pair sums in the same balanced tree
+// as that kernel's 16-lane DPP reduction, so the sum, and every output, has the same bits.
+__device__ __forceinline__ void rms_norm_q128(bf16x8 (&qf)[8], const QNorm& qn, int g) {
+#pragma clang fp contract(off)
+  // the lane's weights (channels 16 ks + 8 g .. +8) as 16-byte loads, issued first
+  u32x4 wr[8];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) wr[ks] = *reinterpret_cast<const u32x4*>(qn.w + 16 * ks + 8 * g);
+  float part[8];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    part[ks] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = static_cast<float>(qf[ks][i]);
+      part[ks] += x * x;
+    }
+  }
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) part[ks] += __shfl_xor(part[ks], 32);
+  const float ss = ((part[0] + part[1]) + (part[2] + part[3])) +
+                   ((part[4] + part[5]) + (part[6] + part[7]));
+  const float inv = 1.0f / sqrtf(ss / 128.0f + qn.eps);
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    float w[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[2 * i] = __uint_as_float(wr[ks][i] << 16);
+      w[2 * i + 1] = __uint_as_float(wr[ks][i] & 0xffff0000u);
+    }
+    u32x4 packed;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      packed[i] = pack_bf16x2((static_cast<float>(qf[ks][2 * i]) * inv) * w[2 * i],
+                              (static_cast<float>(qf[ks][2 * i + 1]) * inv) * w[2 * i + 1]);
+    qf[ks] = __builtin_bit_cast(bf16x8, packed);
+  }
+}
+
 struct Layout {
   const uint16_t* q;
   const uint16_t* k;
@@ -95,7 +146,7 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
                    const int* __restrict__ grp_n, int nblocks, int heads, float scale_log2,
                    const uint16_t* __restrict__ gate, int64_t g_st, int64_t g_sh,
                    uint16_t* __restrict__ out, int64_t o_st, int64_t o_sh,
-                   float* __restrict__ lse, int64_t l_st, int64_t l_sh, MxDst mx) {
+                   float* __restrict__ lse, int64_t l_st, int64_t l_sh, MxDst mx, QNorm qn) {
   constexpr int kBN = tile_keys<kD>();
   constexpr int kKT = kBN / 32;       // 32-key score accumulators per tile
   constexpr int kChunks = kD / 8;     // 16-byte chunks per tile row
@@ -306,13 +357,30 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
   // Each interval is a contiguous key range walked in kBN-key tiles; its bounds are read
   // before its first tile load, so the tile loop itself reads no memory besides the tiles.
   // The online softmax state carries over from one interval to the next.
+  // With a query norm, the first non-empty interval's first tile goes out before the norm
+  // runs, so that the tile's latency covers it.
+  int pre_issued = -1;
+  if constexpr (kMx) {
+    if (qn.w != nullptr) {
+      for (int i = 0; i < nint; ++i) {
+        const int a0 = __builtin_amdgcn_readfirstlane(kv[2 * i]);
+        const int b0 = __builtin_amdgcn_readfirstlane(kv[2 * i + 1]);
+        if (b0 > a0) {
+          issue_tile(a0, min(a0 + kBN, b0), sK0, sV0);
+          pre_issued = i;
+          break;
+        }
+      }
+      rms_norm_q128(qf, qn, g);
+    }
+  }
   for (int i = 0; i < nint; ++i) {
     const int a0 = __builtin_amdgcn_readfirstlane(kv[2 * i]);
     const int b0 = __builtin_amdgcn_readfirstlane(kv[2 * i + 1]);
     const int ntiles = (b0 - a0 + kBN - 1) / kBN;
     if (ntiles <= 0) continue;
     __syncthreads();  // every wave is done reading the buffers of the previous interval
-    issue_tile(a0, min(a0 + kBN, b0), sK0, sV0);
+    if (i != pre_issued) issue_tile(a0, min(a0 + kBN, b0), sK0, sV0);
     for (int t = 0; t < ntiles; t += 2) {
       process(t, ntiles, a0, b0, std::integral_constant<int, 0>{});
       if (t + 1 < ntiles) process(t + 1, ntiles, a0, b0, std::integral_constant<int, 1>{});
@@ -417,7 +485,7 @@ int launch_window(const char* name, const void* q, int64_t q_st, int64_t q_sh, c
                   const int* blocks, int nblocks, const int* grp_kv, const int* grp_n, int heads,
                   int head_dim, float scale, const void* gate, int64_t g_st, int64_t g_sh,
                   void* out, int64_t o_st, int64_t o_sh, float* lse, int64_t l_st, int64_t l_sh,
-                  const MxDst* mx, void* stream) {
+                  const MxDst* mx, QNorm qn, void* stream) {
   if (q == nullptr || k == nullptr || v == nullptr || blocks == nullptr || grp_kv == nullptr ||
       grp_n == nullptr || (mx == nullptr && out == nullptr))
     return set_error(kInvalidArgument, "%s: null pointer", name);
@@ -441,6 +509,12 @@ int launch_window(const char* name, const void* q, int64_t q_st, int64_t q_sh, c
                        "chunks [chunk0, chunk0 + heads), scales 4-byte alignment", name);
   }
   if (!(scale > 0.f) || !isfinite(scale)) return set_error(kInvalidArgument, "%s: bad scale", name);
+  if (qn.w != nullptr && (mx == nullptr || !(qn.eps > 0.f) || !isfinite(qn.eps)))
+    return set_error(kInvalidArgument,
+                     "%s: the query norm needs the MXFP8 output and a finite positive eps", name);
+  if (qn.w != nullptr && !aligned16(qn.w))
+    return set_error(kInvalidArgument, "%s: the query norm weight needs 16-byte alignment",
+                     name);
   if (k_st <= 0 || v_st <= 0 || k_st > (1 << 22) || v_st > (1 << 22))
     return set_error(kUnsupported, "%s: K/V token strides must be in (0, 2^22] elements", name);
   if (nblocks == 0) return kOk;
@@ -456,19 +530,19 @@ int launch_window(const char* name, const void* q, int64_t q_st, int64_t q_sh, c
   if (mx != nullptr)
     hipLaunchKernelGGL((window_attn_kernel<128, kBlockWaves, true>), grid, block, 0, st, in,
                        blocks, grp_kv, grp_n, nblocks, heads, scale * kLog2e, g16, g_st, g_sh,
-                       nullptr, 0, 0, nullptr, 0, 0, *mx);
+                       nullptr, 0, 0, nullptr, 0, 0, *mx, qn);
   else if (head_dim == 128)
     hipLaunchKernelGGL((window_attn_kernel<128, kBlockWaves, false>), grid, block, 0, st, in,
                        blocks, grp_kv, grp_n, nblocks, heads, scale * kLog2e, g16, g_st, g_sh,
-                       o16, o_st, o_sh, lse, l_st, l_sh, none);
+                       o16, o_st, o_sh, lse, l_st, l_sh, none, QNorm{nullptr, 0.f});
   else if (head_dim == 64)
     hipLaunchKernelGGL((window_attn_kernel<64, kBlockWaves, false>), grid, block, 0, st, in,
                        blocks, grp_kv, grp_n, nblocks, heads, scale * kLog2e, g16, g_st, g_sh,
-                       o16, o_st, o_sh, lse, l_st, l_sh, none);
+                       o16, o_st, o_sh, lse, l_st, l_sh, none, QNorm{nullptr, 0.f});
   else
     hipLaunchKernelGGL((window_attn_kernel<256, kBlockWaves, false>), grid, block, 0, st, in,
                        blocks, grp_kv, grp_n, nblocks, heads, scale * kLog2e, g16, g_st, g_sh,
-                       o16, o_st, o_sh, lse, l_st, l_sh, none);
+                       o16, o_st, o_sh, lse, l_st, l_sh, none, QNorm{nullptr, 0.f});
   return check_launch(name);
 }
 
@@ -493,7 +567,8 @@ VDN_API int vdn_window_attention(const void* q, int64_t q_st, int64_t q_sh, cons
                                  int64_t l_sh, void* stream) {
   return launch_window("vdn_window_attention", q, q_st, q_sh, k, k_st, k_sh, v, v_st, v_sh,
                        blocks, nblocks, grp_kv, grp_n, heads, head_dim, scale, gate, g_st, g_sh,
-                       out, o_st, o_sh, lse, l_st, l_sh, nullptr, stream);
+                       out, o_st, o_sh, lse, l_st, l_sh, nullptr, QNorm{nullptr, 0.f},
+                       stream);
 }
 
 // The same attention with the output quantized in the epilogue: query row q, head h ->
@@ -506,10 +581,12 @@ VDN_API int vdn_window_attention_mxfp8(const void* q, int64_t q_st, int64_t q_sh
                                        int64_t v_sh, const int* blocks, int nblocks,
                                        const int* grp_kv, const int* grp_n, int heads,
                                        float scale, const void* gate, int64_t g_st, int64_t g_sh,
+                                       const void* q_norm_w, float q_norm_eps,
                                        void* codes, void* scales, int64_t kp, int chunk0,
                                        void* stream) {
   const MxDst mx{static_cast<uint8_t*>(codes), static_cast<uint8_t*>(scales), kp, chunk0};
   return launch_window("vdn_window_attention_mxfp8", q, q_st, q_sh, k, k_st, k_sh, v, v_st,
                        v_sh, blocks, nblocks, grp_kv, grp_n, heads, 128, scale, gate, g_st, g_sh,
-                       nullptr, 0, 0, nullptr, 0, 0, &mx, stream);
+                       nullptr, 0, 0, nullptr, 0, 0, &mx,
+                       QNorm{static_cast<const uint16_t*>(q_norm_w), q_norm_eps}, stream);
 }

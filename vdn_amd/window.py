@@ -351,8 +351,8 @@ def paper_window_attention(query, key, value, plan: PaperWindowPlan, scale=None,
                   value.data_ptr(), value.stride(0), value.stride(1), dp.blocks.data_ptr(),
                   dp.nblocks, dp.intervals.data_ptr(), dp.counts.data_ptr(), h, scale,
                   _lib.ptr(gate), 0 if gate is None else gate.stride(0),
-                  0 if gate is None else gate.stride(1), codes.data_ptr(), scales.data_ptr(),
-                  codes.shape[1], chunk0, _lib.stream(query.device))
+                  0 if gate is None else gate.stride(1), None, 0.0, codes.data_ptr(),
+                  scales.data_ptr(), codes.shape[1], chunk0, _lib.stream(query.device))
         return None
     if out is None:
         out = torch.empty((rows, h, d), dtype=query.dtype, device=query.device)
