@@ -98,8 +98,8 @@ def work(name, a, plans):
     if name == "vdn_vda_gather":
         f, h, out_f32 = a[10], a[11], a[13]
         return 0.0, 2 * f * h * D * D * 4 + f * h * D * D * (4 if out_f32 else 2)
-    if name == "vdn_vda_readout":
-        f, h, s = a[17], a[18], a[19]
+    if name == "vdn_vda_readout":   # (..., o_ss, head_dim, frames, heads, spatial, stream)
+        f, h, s = a[18], a[19], a[20]
         return 2.0 * f * s * h * D * D, 3 * f * s * h * D * 2 + f * h * D * D * 2
     if name == "vdn_vda_readout_mxfp8":   # q, gate read (bf16); codes + scales written
         f, h, s = a[17], a[18], a[19]
