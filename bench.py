@@ -428,6 +428,64 @@ def c3_vda(steps, frames=30):
             "passes": breakdown_of(per, steps)}
 
 
+def c1_vda(steps):
+    """C1, the reference's CPU-runnable case: one VDA layer at 4 frames x 16x16 tokens, 8 heads,
+    head_dim 64; q, k, v ~ N(0,1) with q and k L2-normalised, beta = sigmoid(N(0,1)),
+    alpha = exp(-A_h dt_c) (A ~ U(1,16), dt log-uniform in [1e-3, 1e-1]), gate and norm
+    weight 1, +-1 frame window. The GPU path (bf16 operands, head dim zero-padded to the
+    kernels' 128) is timed per call; beside it the reference's eager fp32 body on the host
+    cores (the oracle's restatement of branch.py:404-482), whose output the GPU result is
+    compared with. At this size a call is bound by its 15 launches, not by the GPU."""
+    if steps <= 0:
+        return None
+    import torch
+    import torch.nn.functional as F
+    from oracle import vda as ov
+    from vdn_amd import vda as vv
+    frames, spatial, heads, d = 4, 256, 8, 64
+    g = torch.Generator().manual_seed(0)
+    q = F.normalize(torch.randn(frames * spatial, heads, d, generator=g), dim=-1)
+    k = F.normalize(torch.randn(frames * spatial, heads, d, generator=g), dim=-1)
+    v = torch.randn(frames * spatial, heads, d, generator=g)
+    beta = torch.sigmoid(torch.randn(frames * spatial, heads, generator=g))
+    a = torch.empty(heads).uniform_(1, 16, generator=g)
+    dt = torch.exp(torch.rand(heads * d, generator=g) * (math.log(0.1) - math.log(1e-3))
+                   + math.log(1e-3))
+    alpha = torch.exp(-a[:, None] * dt.view(heads, d)).expand(frames, heads, d).contiguous()
+    gate, w = torch.ones(frames * spatial, heads, d), torch.ones(d)
+    bounds = [(max(f - 1, 0), min(f + 1, frames - 1)) for f in range(frames)]
+    dev = [x.cuda() for x in (q.bfloat16(), k.bfloat16(), v.bfloat16(), beta, gate.bfloat16(),
+                              alpha, w)]
+    reps = 10 * steps
+
+    def run():
+        return vv.vda_forward(*dev[:6], bounds, frames, spatial, dev[6], 1e-6)
+
+    with torch.no_grad():
+        out = run()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            run()
+        end.record()
+        torch.cuda.synchronize()
+    gpu_ms = start.elapsed_time(end) / reps
+    threads = host_threads()
+    torch.set_num_threads(threads)
+    t0 = time.perf_counter()
+    ref = ov.eager_branch_fp32(q, k, v, beta, gate, alpha, bounds, frames, spatial, w)
+    cpu_ms = (time.perf_counter() - t0) * 1e3
+    rel = float((out.float().cpu() - ref).norm() / ref.norm())
+    log(f"C1: VDA layer {gpu_ms:.3f} ms on the GPU, {cpu_ms:.1f} ms eager fp32 on {threads} "
+        f"host threads, rel-L2 {rel:.1e}")
+    return {"workload": f"VDA layer, {frames} frames x {spatial} tokens, {heads}x{d} heads",
+            "ms": round(gpu_ms, 4), "tokens_per_s": round(frames * spatial / gpu_ms * 1e3),
+            "rel_l2_vs_cpu_eager_fp32": float(f"{rel:.3g}"),
+            "cpu_baseline": {"ms": round(cpu_ms, 2), "cores": threads, "kind": "port",
+                             "sample": "the whole layer, eager fp32 body on the host"}}
+
+
 def c4_window(steps, frames=30):
     """The frame-window softmax branch alone: 30 frames x 3600 tokens, 40 heads x 128, bf16
     q, k, v ~ N(0,1)/sqrt(128); QK RMSNorm (weight 1) + 3D RoPE (t, h, w split 44/42/42,
@@ -734,10 +792,11 @@ def main():
     p.add_argument("--cpu-sample-frames", type=int, default=6)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--config-steps", type=int, default=5,
-                   help="timed repeats of the stand-alone config measurements (C2 quantize + "
-                        "GEMMs, C3 VDA branch, C4 RoPE + window attention); 0 skips them")
+                   help="timed repeats of the stand-alone config measurements (C1 VDA layer "
+                        "at head_dim 64, C2 quantize + GEMMs, C3 VDA branch, C4 RoPE + window "
+                        "attention); 0 skips them")
     p.add_argument("--configs-only", action="store_true",
-                   help="run only the stand-alone config measurements (C2, C3, C4) and print "
+                   help="run only the stand-alone config measurements (C1, C2, C3, C4) and print "
                         "them as one JSON line (for profiling their kernels apart from the block)")
     p.add_argument("--isolated-steps", type=int, default=2,
                    help="untimed-for-value steps with the VDA branch after the window attention "
@@ -769,7 +828,8 @@ def main():
     frames = args.frames
     if args.configs_only:
         steps = max(args.config_steps, 1)
-        print(json.dumps({"configs": {"C2": c2_quantize_gemm(steps), "C3": c3_vda(steps, frames),
+        print(json.dumps({"configs": {"C1": c1_vda(steps), "C2": c2_quantize_gemm(steps),
+                                      "C3": c3_vda(steps, frames),
                                       "C4": c4_window(steps, frames)}}), flush=True)
         if args.calibrate_copy:
             calibrate_copy()
@@ -842,7 +902,8 @@ def main():
                   lambda p, c, f, s, t, l: {p.device_plan.intervals.data_ptr():
                                             visible_pairs(f, s, cfg.radius),
                                             c.intervals.data_ptr(): t * l})
-    configs = {"C2": c2_quantize_gemm(args.config_steps),
+    configs = {"C1": c1_vda(args.config_steps),
+               "C2": c2_quantize_gemm(args.config_steps),
                "C3": c3_vda(args.config_steps, frames),
                "C4": c4_window(args.config_steps, frames)}
     traffic = traffic_per_launch()
