@@ -148,3 +148,49 @@ def test_small_head_dim_rejections(device):
     with pytest.raises(ValueError, match="128"):
         vv.paper_delta_factors(torch.zeros(1, d, d, device=device),
                                torch.zeros(1, d, d, device=device))
+
+
+class _Branch(torch.nn.Module):
+    """The attributes paper_readout reads from the reference's linear branch
+    (paper_stack.py:266-318): beta_proj, alpha(frame_mean, heads=), output_gate, norm, bridge,
+    paper_vda_chunk_size."""
+
+    def __init__(self, hidden, heads, d, g):
+        super().__init__()
+        self.heads, self.d = heads, d
+        self.beta_proj = torch.nn.Linear(hidden, heads, bias=False)
+        self.gate_proj = torch.nn.Linear(hidden, heads * d)
+        for p in (self.beta_proj.weight, self.gate_proj.weight, self.gate_proj.bias):
+            p.data.copy_(torch.randn(p.shape, generator=g) * 0.05)
+        self.decay = torch.rand(heads, d, generator=g) * 0.1 + 0.85
+        self.norm = torch.nn.RMSNorm(d, eps=1e-6)
+        self.bridge = "alpha"
+        self.paper_vda_chunk_size = 2
+
+    def alpha(self, frame_mean, heads=None):
+        return self.decay.to(frame_mean.device).expand(frame_mean.shape[0], -1, -1)
+
+    def output_gate(self, xv):
+        return torch.sigmoid(self.gate_proj(xv))
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("d", [64, 128])
+def test_paper_readout_signature_matches_vda_forward(device, d):
+    """paper_readout (the reference's signature) forms beta, alpha and the output gate from
+    the branch and runs the same kernels as vda_forward given them: identical bytes."""
+    frames, spatial, h, hidden = 5, 12, 2, 96
+    g = torch.Generator().manual_seed(d)
+    br = _Branch(hidden, h, d, g).to(device).to(torch.bfloat16)
+    br.decay = br.decay.float()
+    xv = torch.randn(frames * spatial, hidden, generator=g).bfloat16().to(device)
+    qkv = [torch.randn(frames * spatial, h, d, generator=g).bfloat16().to(device)
+           for _ in range(3)]
+    bounds = ov.window_bounds(frames, 1)
+    got = vv.paper_readout(br, xv, frames, spatial, bounds, qkv, heads=h)
+    beta = torch.sigmoid(br.beta_proj(xv))
+    gate = br.output_gate(xv).reshape(-1, h, d)
+    alpha = br.decay.to(device).expand(frames, -1, -1).float().contiguous()
+    want = vv.vda_forward(*qkv, beta, gate, alpha, bounds, frames, spatial, br.norm.weight, 1e-6,
+                          chunk_size=2)
+    assert got.shape == (frames * spatial, h * d) and torch.equal(got, want)

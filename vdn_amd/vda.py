@@ -684,24 +684,26 @@ def paper_readout(branch, xv, num_frames, tokens_per_frame, bounds, qkv_raw, fra
         if text_beta is None:
             text_beta = torch.sigmoid(branch.beta_proj(text_x))
         text = (text_qkv_raw[1], text_qkv_raw[2], text_beta.reshape(-1, h))
+    d = q.shape[-1]
     if gate is None:
-        gate = _output_gate(branch.output_gate, xv, h)
+        gate = _output_gate(branch.output_gate, xv, h, d)
     else:
-        gate = gate.reshape(-1, h, HEAD_DIM)
+        gate = gate.reshape(-1, h, d)
     return vda_forward(q, k, v, beta.reshape(-1, h), gate, alpha, bounds,
                        num_frames, tokens_per_frame, branch.norm.weight, branch.norm.eps,
                        chunk_size=branch.paper_vda_chunk_size, bridge=branch.bridge == "alpha",
                        text=text, conv=conv, frame_size=frame_size)
 
 
-def _output_gate(module, xv, heads):
+def _output_gate(module, xv, heads, head_dim=HEAD_DIM):
     """OutputGate(xv) of the linear branch: a bottleneck-128 gate in bf16 goes to the readout
     kernel as its projection operands (only down(xv) is formed here); any other gate is
     evaluated by the module itself."""
     down, up = getattr(module, "down", None), getattr(module, "up", None)
-    if (down is not None and up is not None and down.out_features == HEAD_DIM
+    if (head_dim == HEAD_DIM and down is not None and up is not None
+            and down.out_features == HEAD_DIM
             and up.in_features == HEAD_DIM and up.out_features == heads * HEAD_DIM
             and up.bias is not None and xv.dtype == torch.bfloat16
             and all(p.dtype == torch.bfloat16 for p in (down.weight, up.weight, up.bias))):
         return OutputGateProjection(down(xv), up.weight, up.bias)
-    return module(xv).reshape(-1, heads, HEAD_DIM)
+    return module(xv).reshape(-1, heads, head_dim)
