@@ -6,9 +6,11 @@ attention, cross-attention to 512 context rows, gated residuals) over 30 latent 
 45 x 80 = 108,000 tokens, bf16 activations, MXFP8 projections. Random-init weights N(0, 0.02),
 hidden/temb/context N(0, 1), all resident in HBM before timing.
 
-Prints one JSON line: value = ms per block forward (lower is better), the MXFP8 GEMM roofline
-(algorithmic FLOP / measured launch time, HIP events on the launch stream), the VDA passes'
-algorithmic GB/s, a per-entry-point breakdown, and the CPU fp32 path timed on a bounded sample.
+Prints one JSON line: value = the median ms per block forward over the timed steps (one event
+pair per step, lower is better), the MXFP8 GEMM roofline (algorithmic FLOP / measured launch
+time, HIP events on the launch stream, from separate instrumented steps), the VDA passes'
+algorithmic GB/s, a per-entry-point breakdown, the caller stream's idle time per block, and the
+CPU fp32 path timed on a bounded sample.
 
   python bench.py [--steps K] [--warmup W] [--frames F] [--no-cpu-baseline]
 """
@@ -19,6 +21,7 @@ import json
 import math
 import os
 import re
+import statistics
 import sys
 import time
 
@@ -533,6 +536,22 @@ def c4_window(steps, frames=30):
             "qk_rope_gbs": round(rope_bytes / (rope * 1e-3) / 1e9, 1)}
 
 
+def timed_steps(step, count):
+    """Runs `step` count times back to back with one event pair per step on the caller's
+    stream, bracketed by device synchronisations. Returns (per-step ms, mean ms over the
+    whole run: first start to last end / count)."""
+    import torch
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(count)]
+    torch.cuda.synchronize()
+    for s, e in evs:
+        s.record()
+        step()
+        e.record()
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in evs], evs[0][0].elapsed_time(evs[-1][1]) / count
+
+
 def visible_pairs(frames, spatial, radius):
     """Query-key pairs per head of the +-radius frame window."""
     total = 0
@@ -786,8 +805,8 @@ def main():
                    help="after the timed steps, negate one 1 GiB bf16 buffer into another (an "
                         "elementwise kernel of known traffic for scaling HBM byte counters)")
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=5)
-    p.add_argument("--warmup", type=int, default=2)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--frames", type=int, default=30)
     p.add_argument("--cpu-sample-frames", type=int, default=6)
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -798,6 +817,9 @@ def main():
     p.add_argument("--configs-only", action="store_true",
                    help="run only the stand-alone config measurements (C1, C2, C3, C4) and print "
                         "them as one JSON line (for profiling their kernels apart from the block)")
+    p.add_argument("--breakdown-steps", type=int, default=3,
+                   help="instrumented steps after the timed ones (an event pair around every "
+                        "launch) for the per-kernel breakdown, the roofline and idle_ms")
     p.add_argument("--isolated-steps", type=int, default=2,
                    help="untimed-for-value steps with the VDA branch after the window attention "
                         "on one stream, for the branch kernels' own launch times")
@@ -855,22 +877,32 @@ def main():
         step()
         torch.cuda.synchronize()
         log(f"warmup {i + 1}/{args.warmup} done")
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    names = set(_lib.SIGNATURES)
-    with _lib.LaunchTimer(names) as timer:
-        torch.cuda.synchronize()
-        start.record()
-        for i in range(args.steps):
-            step()
-        end.record()
-        torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
-    log(f"timed {args.steps} steps: {ms:.2f} ms per block")
+    # The headline: K steps back to back, one event pair per step on the caller's stream (the
+    # block joins its side stream back into it), no per-launch events; value = the median.
+    steps_ms, wall_ms = timed_steps(step, args.steps)
+    ms = statistics.median(steps_ms)
+    log(f"timed {args.steps} steps: median {ms:.2f} ms per block (mean {wall_ms:.2f}, "
+        f"min {min(steps_ms):.2f}, max {max(steps_ms):.2f})")
     if args.calibrate_copy:
         calibrate_copy()
 
+    # The per-kernel breakdown comes from separate instrumented steps (an event pair around
+    # every launch). idle_ms = a step's wall time minus the sum of its caller-stream launch
+    # times: what the caller's stream spends waiting (on the host, or on the side stream).
+    names = set(_lib.SIGNATURES)
+    b_steps = max(args.breakdown_steps, 1)
+    with _lib.LaunchTimer(names) as timer:
+        inst_ms, _ = timed_steps(step, b_steps)
     per = aggregate(timer, plans)
-    breakdown = breakdown_of(per, args.steps)
+    breakdown = breakdown_of(per, b_steps)
+    main_launch_ms = sum(per[nm][1] for nm in per if nm not in VDA_ENTRIES) / b_steps
+    idle = {"ms": round(ms - main_launch_ms, 3),
+            "instrumented_ms": round(statistics.median(inst_ms) - main_launch_ms, 3),
+            "caller_stream_launch_ms": round(main_launch_ms, 3),
+            "instrumented_step_ms": round(statistics.median(inst_ms), 3),
+            "steps": b_steps}
+    log(f"instrumented {b_steps} steps: caller-stream launches {main_launch_ms:.2f} ms, "
+        f"idle {idle['ms']:.3f} ms per block")
     g = [sum(per[nm][i] for nm in GEMMS if nm in per) for i in range(4)]
     gemm_tflops = g[2] / (g[1] * 1e-3) / 1e12
 
@@ -878,17 +910,18 @@ def main():
     # window attention in the timed steps above, so their launch times there are wall times
     # under contention. These steps give each branch kernel's own launch time.
     iso_steps = args.isolated_steps
+    serial_ms = None
     if iso_steps > 0:
         block.overlap_vda = False
+        serial_ms = statistics.median(timed_steps(step, iso_steps)[0])
         with _lib.LaunchTimer(set(VDA_ENTRIES) | set(ATTENTION)) as iso_timer:
-            for i in range(iso_steps):
-                step()
-            torch.cuda.synchronize()
+            timed_steps(step, iso_steps)
         block.overlap_vda = True
         iso = aggregate(iso_timer, plans)
-        log(f"isolated branch kernels timed over {iso_steps} steps")
+        log(f"isolated branch kernels timed over {iso_steps} steps; the block without the "
+            f"side stream: {serial_ms:.2f} ms")
     else:   # only the overlapped times exist
-        iso, iso_steps = per, args.steps
+        iso, iso_steps = per, b_steps
     vda_t = sum(iso[n][1] for n in VDA_ENTRIES if n in iso)
     vda_bytes = sum(iso[n][3] for n in VDA_ENTRIES if n in iso)
     vda_gbs = vda_bytes / (vda_t * 1e-3) / 1e9
@@ -911,6 +944,12 @@ def main():
     result = {
         "metric": METRIC, "value": round(ms, 3), "unit": "ms", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
+        "step_ms": {"median": round(ms, 3), "mean": round(wall_ms, 3),
+                    "min": round(min(steps_ms), 3), "max": round(max(steps_ms), 3),
+                    "all": [round(t, 3) for t in steps_ms]},
+        "idle_ms": idle,
+        "vda_side_stream": {"overlapped_ms": round(ms, 3),
+                            "serial_ms": None if serial_ms is None else round(serial_ms, 3)},
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "mxfp8-e4m3 GEMMs, bf16 attention/activations, fp32 VDA state",
         "data": "synthetic: random-init weights N(0,0.02), hidden/temb/context N(0,1)",

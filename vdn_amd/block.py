@@ -344,15 +344,17 @@ class HybridDiTBlock(nn.Module):
 
             # The VDA branch runs on a side stream while RoPE and the window attention run on
             # the caller's stream (the reference's paper_vda_overlap, tensor_parallel.py:
-            # 202-216): its latency-bound passes fill the attention's gaps.
+            # 202-216): its latency-bound passes fill the attention's gaps. The tensors it
+            # shares with the caller's stream (qkv, the gates, alpha, the [O | O_lin] operand)
+            # are all released after main.wait_stream(side), so a later allocation on the
+            # caller's stream is ordered after the branch without record_stream (which would
+            # keep ~5 GB per block out of the allocator's cache while the host runs ahead).
             main = torch.cuda.current_stream(dev)
             if self.overlap_vda:
                 side = self._side_stream(dev)
                 side.wait_stream(main)
                 with torch.cuda.stream(side):
                     linear_branch()
-                for t in (qkv, gate_down, beta, alpha, qb, sb):
-                    t.record_stream(side)
             q, kk = vw.paper_qk_rmsnorm_rope(raw_q, raw_k, k["norm_q"], k["norm_k"], cfg.eps,
                                              cos, sin, enabled=True)
             vw.paper_window_attention(q, kk, value, window_plan, d ** -0.5, enabled=True,

@@ -33,15 +33,17 @@ constexpr int kGRank = 128;      // output-gate down and alpha-down widths
 constexpr int kARing = 6;        // x1 stages in LDS (issued 5 stages ahead)
 constexpr int kWRing = 4;        // W stages in LDS (issued 3 stages ahead)
 
-// global -> LDS DMA of 16 bytes per lane (lane l's bytes land at LDS byte m0 + 16 l), as
+// global -> LDS DMA of 16 bytes per lane (lane l's bytes land at LDS byte M0 + 16 l), as
 // inline asm: the compiler does not see it as an LDS write, so it never makes a fragment read
 // wait for a DMA into another ring slot; the kernel orders the DMAs itself (vmcnt waits before
-// its barriers; no other vector memory access is in flight in the K loop). One wait state
-// separates the m0 write from its use.
+// its barriers; no other vector memory access is in flight in the K loop). With either LDS
+// DMA builtin (global or buffer form) the compiler puts a vmcnt(0) before every stage's
+// fragment reads, which serializes the rings. M0 is an input operand ("{m0}"): the compiler
+// writes it and knows it is live; the s_nop is the wait state between an M0 write and an
+// LDS DMA that reads it.
 __device__ __forceinline__ void g_load_lds16(const void* src, void* lds_wave_base) {
   const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)lds_wave_base));
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               ::"s"(lds), "v"(src) : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
 }
 
 // 16-byte chunk c (0..3) of a 64-byte tile row r is stored at c ^ ((r >> 2) & 3): the 16 lanes

@@ -442,7 +442,7 @@ mxfp8_gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ As,
 // and a tile's epilogue (straight from the accumulators: 8-byte bf16 or 4-byte MXFP8 stores)
 // runs while the next tile's first steps are in flight.
 // Tiles are fetched with buffer_load ... lds through buffer resources (rows past the padded
-// end read as zero) issued from inline asm (see buffer_to_lds16).
+// end read as zero; see buffer_to_lds16).
 constexpr int kPTile = 256;
 constexpr int kPScaleOff = 2 * kPTile * kBK;                 // A tile, then W tile
 constexpr int kPStep = kPScaleOff + 2 * kPTile * 4;          // + four 512-byte scale runs
@@ -455,26 +455,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
                                            0x00020000);
 }
 
-// LDS DMA through a buffer resource, written as inline asm: lane l's 16 (4) bytes at
-// voffset land at LDS byte lds_base + 16 l (4 l); M0 carries lds_base. The compiler does not
-// see these as LDS writes, so it does not make every later LDS read wait for them (it
-// cannot tell the two step buffers apart); the kernel orders them itself with explicit
-// vmcnt waits before its barriers. They are issued where the compiler has no vector memory
-// access of its own in flight, so its own vmcnt counts stay conservative.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)p));
-}
-
+// LDS DMA through a buffer resource: lane l's 16 (4) bytes at voffset land at LDS byte
+// lds_base + 16 l (4 l). The compiler sets M0 to the wave's LDS base itself (with the wait
+// state an M0 write needs before an LDS DMA) and counts these loads on vmcnt only: the
+// fragment reads of the other step buffer keep their exact lgkmcnt waits, and the kernel
+// orders the step buffers with its own vmcnt waits before its barriers.
 __device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, uint32_t voffset,
-                                                uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               ::"s"(lds_base), "v"(voffset), "s"(r) : "memory");
+                                                void* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds_base, 16, voffset, 0, 0, 0);
 }
 
 __device__ __forceinline__ void buffer_to_lds4(__amdgpu_buffer_rsrc_t r, uint32_t voffset,
-                                               uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
-               ::"s"(lds_base), "v"(voffset), "s"(r) : "memory");
+                                               void* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds_base, 4, voffset, 0, 0, 0);
 }
 
 // Virtual tile id b (b % 8 is the XCD that runs it) -> (tile row, tile column).
@@ -570,16 +563,16 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
     const bool is_a = wave < 2;
     const int64_t blk = (is_a ? d_m0 : d_n0) / 128 + (wave & 1);
     const uint32_t off = static_cast<uint32_t>((blk * col_tiles + d_ks) * 512) + lane * 4;
-    const uint32_t dst = lds_addr(buf + kPScaleOff + wave * 512);
+    uint8_t* dst = buf + kPScaleOff + wave * 512;
     buffer_to_lds4(is_a ? as_rsrc : ws_rsrc, off, dst);
     buffer_to_lds4(is_a ? as_rsrc : ws_rsrc, off + 256, dst + 256);
   };
   auto dma_segment = [&](uint8_t* buf, int seg) __attribute__((always_inline)) {
     const uint32_t off = dma_voff + static_cast<uint32_t>(d_ks) * kBK + (seg & 7) * 32 * kpu;
     if (seg < 8)
-      buffer_to_lds16(d_a, off, lds_addr(buf + ((seg & 7) * 4 + wave) * 1024));
+      buffer_to_lds16(d_a, off, buf + ((seg & 7) * 4 + wave) * 1024);
     else
-      buffer_to_lds16(d_w, off, lds_addr(buf + kPTile * kBK + ((seg & 7) * 4 + wave) * 1024));
+      buffer_to_lds16(d_w, off, buf + kPTile * kBK + ((seg & 7) * 4 + wave) * 1024);
   };
 
   // ---- consumer side ----

@@ -632,10 +632,16 @@ constexpr int kCvHalo = kCvTile + 4;
 constexpr int kCvPos = kCvHalo * kCvHalo;       // 144 staged positions
 constexpr int kCvBuf = kCvPos * kD * 2;         // 36864 bytes per frame
 
+// LDS DMA through a buffer resource as inline asm: lane l's 16 bytes at voffset land at LDS
+// byte lds_base + 16 l. The compiler does not see it as an LDS write, so the reads of the
+// current frame's buffer do not wait for the next frame's DMA into the other buffer (with the
+// builtin they would); the kernel waits on vmcnt itself before its barrier. M0 is an input
+// operand ("{m0}"): the compiler writes it and knows it is live; the s_nop is the wait state
+// between an M0 write and an LDS DMA that reads it.
 __device__ __forceinline__ void cv_buffer_to_lds16(__amdgpu_buffer_rsrc_t r, uint32_t voffset,
                                                    uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               ::"s"(lds_base), "v"(voffset), "s"(r) : "memory");
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               ::"v"(voffset), "s"(r), "{m0}"(lds_base) : "memory");
 }
 
 // Sum over the 64 lanes of a wave (every lane gets the same bits).
