@@ -252,13 +252,15 @@ int vdn_vda_epilogue(const void* readout, const void* weight, int weight_f32, fl
  * ------------------------------------------------------------------------------------- */
 
 /*
- * QK RMSNorm + rotate-half RoPE: n = bf16((x * rsqrt(mean(x^2) + eps)) * w); for channel
- * i < rot: out = bf16(bf16(n_i * c_i) + bf16(r_i * s_i)) with r_i = -n_{i+rot/2} (i < rot/2)
- * or n_{i-rot/2}; channels >= rot pass n. q, k: bf16 [tokens, heads, head_dim] with element
- * strides (token, head, channel); weights [head_dim] with stride (flags bit0 / bit1: fp32
- * q / k weight, else bf16); cos, sin (nullable together): [tokens, rot] with strides, fp32
- * when flags bit2 else bf16 (values rounded to bf16 before use). qo, ko: contiguous bf16.
- * flags bit3: q only (k, k's weight and ko may be null).
+ * QK RMSNorm + rotate-half RoPE, with act() the rounding to the activation dtype (flags bits
+ * 4-5: 0 bf16, 1 fp16, 2 fp32, which has no rounding): n = act((x * rsqrt(mean(x^2) + eps)) *
+ * w); for channel i < rot: out = act(act(n_i * c_i) + act(r_i * s_i)) with r_i = -n_{i+rot/2}
+ * (i < rot/2) or n_{i-rot/2}; channels >= rot pass n. q, k: [tokens, heads, head_dim] of the
+ * activation dtype with element strides (token, head, channel); weights [head_dim] with
+ * stride (flags bit0 / bit1: fp32 q / k weight, else the activation dtype); cos, sin
+ * (nullable together): [tokens, rot] with strides, fp32 when flags bit2 else the activation
+ * dtype (values rounded to the activation dtype before use). qo, ko: contiguous, activation
+ * dtype. flags bit3: q only (k, k's weight and ko may be null).
  * Replaces: paper_qk_rmsnorm_rope (src/models/softmax_attention/paper_qk_rope.py:145-211).
  */
 int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64_t q_sd, const void* k,
@@ -269,21 +271,22 @@ int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64_t q_sd,
                         void* stream);
 
 /*
- * Exact softmax attention of query blocks over key intervals (bf16, head_dim 64, 128 or 256):
- * blocks int32 [nblocks, 3] = (first query, end of its query range, group), <= 256 queries
- * each; grp_kv int32 [groups, 8, 2] key intervals [a, b); grp_n int32 [groups].
- * q, k, v addressed by (token, head) strides with unit channel stride. gate (nullable): bf16
- * per (token, head) scalar applied as out = bf16(bf16(o) * gate). out: bf16 (token, head)
- * strides; lse (nullable): fp32 natural-log sum-exp of the scaled scores.
+ * Exact softmax attention of query blocks over key intervals (dtype 0: bf16, 1: fp16; head_dim
+ * 64, 128 or 256): blocks int32 [nblocks, 3] = (first query, end of its query range, group),
+ * <= 256 queries each; grp_kv int32 [groups, 8, 2] key intervals [a, b); grp_n int32 [groups].
+ * q, k, v addressed by (token, head) strides with unit channel stride. gate (nullable): per
+ * (token, head) scalar of the activation dtype applied as out = act(act(o) * gate). out:
+ * activation dtype, (token, head) strides; lse (nullable): fp32 natural-log sum-exp of the
+ * scaled scores.
  * Replaces: paper_window_attention (src/models/softmax_attention/paper_window.py:182-243)
  * and apply_softmax_gate (src/models/softmax_attention/kernels.py:51-67).
  */
 int vdn_window_attention(const void* q, int64_t q_st, int64_t q_sh, const void* k, int64_t k_st,
                          int64_t k_sh, const void* v, int64_t v_st, int64_t v_sh,
                          const int* blocks, int nblocks, const int* grp_kv, const int* grp_n,
-                         int heads, int head_dim, float scale, const void* gate, int64_t g_st,
-                         int64_t g_sh, void* out, int64_t o_st, int64_t o_sh, float* lse,
-                         int64_t l_st, int64_t l_sh, void* stream);
+                         int heads, int head_dim, int dtype, float scale, const void* gate,
+                         int64_t g_st, int64_t g_sh, void* out, int64_t o_st, int64_t o_sh,
+                         float* lse, int64_t l_st, int64_t l_sh, void* stream);
 
 /* vdn_window_attention with the output quantized in the epilogue instead of stored as bf16:
  * query row q, head h -> MXFP8 codes[q, 128 (chunk0 + h) .. +128) of a [rows, kp] code

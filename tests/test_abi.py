@@ -34,7 +34,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     lib = _lib.load()
     for name in declared_functions():
         assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
-    assert lib.vdn_abi_version() == 5
+    assert lib.vdn_abi_version() == 6
     assert lib.vdn_last_error() is not None
 
 

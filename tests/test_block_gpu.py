@@ -10,8 +10,8 @@ from oracle import block as ob
 from oracle import mxfp8 as omx
 from oracle import window as ow
 from vdn_amd import window as vw
-from vdn_amd.block import (BlockConfig, BlockWeights, HybridDiTBlock, cross_attention_plan,
-                           make_inputs)
+from vdn_amd.block import (BlockConfig, BlockWeights, FinitePredicate, HybridDiTBlock,
+                           cross_attention_plan, make_inputs)
 
 pytestmark = pytest.mark.gpu
 
@@ -23,6 +23,9 @@ WIDE = BlockConfig()
 H3 = BlockConfig(hidden=5376, heads=56, head_dim=128, ffn=14336, ffn_act="swiglu")
 SMALL_H3 = BlockConfig(hidden=384, heads=2, head_dim=128, ffn=320, ffn_act="swiglu", context=16,
                        lora_rank=8, lora_scale=0.5)
+# an odd head count (the gate projection runs one zero-padded extra head)
+ODD_HEADS = BlockConfig(hidden=320, heads=5, head_dim=128, ffn=384, context=16, lora_rank=8,
+                        lora_scale=0.5)
 REL = 1e-2
 END_TO_END = 5e-2
 
@@ -107,6 +110,10 @@ def test_small_block_matches_oracle():
     check(run(SMALL, 4, 4, 8, seed=11))
 
 
+def test_odd_head_count_block_matches_oracle():
+    check(run(ODD_HEADS, 4, 4, 8, seed=13))
+
+
 def test_full_width_block_short_clip_matches_oracle():
     check(run(WIDE, 4, 4, 8, seed=12))
 
@@ -181,3 +188,44 @@ def test_cross_attention_query_norm_in_kernel_equals_norm_pass(w_dtype, rows):
     assert torch.equal(qa, qb) and torch.equal(sa, sb)
     with pytest.raises(ValueError, match="MXFP8-output form"):
         cross_attention(q, k, v, plan, d ** -0.5, q_norm=(w, 1e-6))
+
+
+def test_guard_receives_device_predicates():
+    """guard= hands the three prenorm producers' row flags and the projections' flag to
+    guard.predicate as device bool tensors (paper_block_forward, fused_block.py:144-155) and
+    leaves the output unchanged; a NaN in the hidden state and an inf in the context each
+    make the predicate false."""
+    cfg = SMALL
+    w = BlockWeights.random(cfg, 31, device="cuda")
+    block = HybridDiTBlock(cfg, w)
+    hidden, temb, ctx, layout, rope = make_inputs(cfg, 4, 4, 8, 32, device="cuda")
+    plan = vw.prepare_paper_window_plan(layout, vw.window_bounds(4, cfg.radius), device="cuda")
+    cplan = cross_attention_plan(hidden.shape[0], ctx.shape[0], "cuda")
+
+    class Recorder(FinitePredicate):
+        def __init__(self):
+            super().__init__("cuda")
+            self.seen = []
+
+        def predicate(self, parts):
+            self.seen.append((parts.device.type, parts.dtype))
+            super().predicate(parts)
+
+    guard = Recorder()
+    out = block(hidden, temb, ctx, layout, rope, plan, cplan, guard=guard)
+    ref = block(hidden, temb, ctx, layout, rope, plan, cplan)
+    assert torch.equal(out, ref)
+    assert guard.seen == [("cuda", torch.bool)] * 4
+    guard.check("block")
+    bad = hidden.clone()
+    bad[7, 3] = float("nan")
+    block(bad, temb, ctx, layout, rope, plan, cplan, guard=guard)
+    with pytest.raises(FloatingPointError):
+        guard.check("block")
+    bad_ctx = ctx.clone()
+    bad_ctx[2, 5] = float("inf")
+    block(hidden, temb, bad_ctx, layout, rope, plan, cplan, guard=guard)
+    with pytest.raises(FloatingPointError):
+        guard.check("block")
+    block(hidden, temb, ctx, layout, rope, plan, cplan, guard=guard)
+    guard.check("block")

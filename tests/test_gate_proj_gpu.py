@@ -15,6 +15,8 @@ from vdn_amd.block import BlockConfig, BlockWeights
 pytestmark = pytest.mark.gpu
 
 WIDE = BlockConfig(hidden=512, heads=40, head_dim=128, ffn=512, context=16, lora_rank=8)
+# an odd head count runs the kernel on one zero-padded extra head
+ODD = BlockConfig(hidden=320, heads=5, head_dim=128, ffn=384, context=16, lora_rank=8)
 
 
 def _bf16(x):
@@ -70,6 +72,11 @@ def wide():
     return BlockWeights.random(WIDE, seed=6)
 
 
+@pytest.fixture(scope="module")
+def odd():
+    return BlockWeights.random(ODD, seed=7)
+
+
 def test_adaln_closed_forms(small):
     check_adaln_closed_forms(lambda t, temb: kernel_tables(t, SMALL, temb), small, SMALL)
 
@@ -90,13 +97,15 @@ def _ulps(a, ref):
     return np.abs(a.numpy() - ref) / ulp
 
 
-@pytest.mark.parametrize("frames,spatial", [(3, 300), (2, 128), (1, 45)])
-def test_gate_projection_matches_oracle(wide, frames, spatial):
-    """40 heads, hidden 512: softmax gate, beta and the output-gate down projection within one
-    bf16 rounding of the float64 oracle (fp32 accumulation against float64), the output gate
-    through the same; FrameKDAAlpha from the kernel's per-frame sums against the oracle's
-    frame mean of the same x1. Frames of 300 rows end in a partial 128-row block."""
-    cfg, w = WIDE, wide
+@pytest.mark.parametrize("frames,spatial,width", [(3, 300, "wide"), (2, 128, "wide"),
+                                                 (1, 45, "wide"), (2, 200, "odd")])
+def test_gate_projection_matches_oracle(wide, odd, frames, spatial, width):
+    """40 heads, hidden 512 (and 5 heads, hidden 320: an odd head count): softmax gate, beta
+    and the output-gate down projection within one bf16 rounding of the float64 oracle (fp32
+    accumulation against float64), the output gate through the same; FrameKDAAlpha from the
+    kernel's per-frame sums against the oracle's frame mean of the same x1. Frames of 300 rows
+    end in a partial 128-row block."""
+    cfg, w = (WIDE, wide) if width == "wide" else (ODD, odd)
     g = torch.Generator().manual_seed(frames * 1000 + spatial)
     x1 = torch.randn(frames * spatial, cfg.hidden, generator=g).to(torch.bfloat16).double()
     soft, beta, lin, down, partial = kernel_gates(w.tensors, cfg, x1, frames)
@@ -121,11 +130,13 @@ def test_gate_projection_matches_oracle(wide, frames, spatial):
 
 
 @pytest.mark.parametrize("hidden,m,dtype", [(512, 1, torch.float32), (5120, 1, torch.float32),
-                                            (520, 3, torch.float32), (512, 2, torch.bfloat16)])
+                                            (520, 3, torch.float32), (512, 2, torch.bfloat16),
+                                            (512, 2, torch.float16)])
 def test_adaln_tables_match_oracle(hidden, m, dtype):
-    """Random temb (m rows, fp32 or bf16) and weights: every table entry within one bf16
+    """Random temb (m rows, fp32, bf16 or fp16) and weights: every table entry within one bf16
     rounding of the float64 oracle, nearly all equal; K = 520 covers a partial last
-    512-column piece."""
+    512-column piece. The oracle takes temb.float() (exact for fp16 and bf16), as the
+    reference's SiLU(temb.float()) does."""
     g = torch.Generator().manual_seed(hidden + m)
     cfg = BlockConfig(hidden=hidden, heads=4, head_dim=128, ffn=512, context=16, lora_rank=8)
     tensors = {"adaln_w": (torch.randn(6 * hidden, hidden, generator=g) * 0.02).to(torch.bfloat16),
@@ -165,7 +176,7 @@ def test_argument_errors(wide):
         vb.frame_alpha(partial, 2, 64, t["alpha_up_w"].float(), t["dt_bias"], t["a_log"],
                        WIDE.heads, 128)
     with pytest.raises(ValueError):
-        vb.adaln_tables(torch.zeros(1, WIDE.hidden, dtype=torch.float16, device="cuda"),
+        vb.adaln_tables(torch.zeros(1, WIDE.hidden, dtype=torch.int32, device="cuda"),
                         t["adaln_w"], t["adaln_b"], WIDE.hidden)
     with pytest.raises(ValueError):
         vb.adaln_tables(torch.zeros(1, WIDE.hidden, dtype=torch.bfloat16, device="cuda"),

@@ -148,3 +148,33 @@ def test_rope_tables_3d_match_oracle():
     torch.testing.assert_close(c1, c2, rtol=0, atol=1e-12)
     torch.testing.assert_close(s1, s2, rtol=0, atol=1e-12)
     assert c1.shape == (60, 128)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@torch.no_grad()
+def test_rope_disabled_eager_path_matches_oracle(dtype):
+    """paper_qk_rmsnorm_rope(enabled=False) is the reference's eager path on the tensors' own
+    device (paper_qk_rope.py:82-95, 168-176): bit-equal to the oracle on the rounding-trap
+    input (its mean square is exact) and within one rounding of the activation dtype on
+    random strided inputs, for each activation dtype; fp32 and activation-dtype weights."""
+    g = torch.Generator().manual_seed(715)
+    x = torch.ones(3, 7, 128, dtype=dtype)
+    w = (torch.rand(128, generator=g) * 1.7 + .1).to(dtype)
+    angles = torch.randn(3, 96, generator=g)
+    c, s = angles.cos(), angles.sin()
+    qo, ko = vw.paper_qk_rmsnorm_rope(x, x, w, w.float(), .25, c, s)
+    assert qo.dtype == dtype and torch.equal(qo, ow.qk_rope(x, w, .25, c, s))
+    assert torch.equal(ko, ow.qk_rope(x, w.float(), .25, c, s))
+    storage = torch.randn(13, 3 * 7 * 128, generator=g).to(dtype)
+    q, k = storage[:, :896].view(13, 7, 128), storage[:, 896:1792].view(13, 7, 128)
+    ang = torch.randn(13, 64, generator=g)
+    cos, sin = torch.cat((ang.cos(), ang.cos()), 1), torch.cat((ang.sin(), ang.sin()), 1)
+    qo, ko = vw.paper_qk_rmsnorm_rope(q, k, w, w, 1e-6, cos, sin)
+    for out, raw in ((qo, q), (ko, k)):
+        exp = ow.qk_rope(raw, w, 1e-6, cos, sin).float()
+        ulp = {torch.bfloat16: 2 ** -7, torch.float16: 2 ** -10, torch.float32: 2 ** -22}[dtype]
+        assert ((out.float() - exp).abs() <= 2 * ulp * exp.abs() + 1e-6).all()
+    n_only, _ = vw.paper_qk_rmsnorm_rope(q, k, w, w, 1e-6)
+    torch.testing.assert_close(n_only, ow.qk_rope(q, w, 1e-6), atol=0, rtol=2 ** -6)
+    with torch.enable_grad(), pytest.raises(RuntimeError, match="inference-only"):
+        vw.paper_qk_rmsnorm_rope(q, k, w, w, 1e-6, cos, sin)

@@ -363,3 +363,82 @@ def test_other_head_dims_reject_mxfp8_output(device):
     with pytest.raises(ValueError):
         bad = torch.randn(6, 2, 96, device=device, dtype=torch.bfloat16)
         vw.paper_window_attention(bad, bad, bad, plan, enabled=True)
+
+
+@pytest.mark.parametrize("before,after,frames,chunk,radius,anchor",
+                         [(3, 4, 7, 3, 1, "both"), (0, 0, 7, 0, 99, "none"),
+                          (0, 0, 3, 0, 1, "none")])
+@pytest.mark.parametrize("d", [64, 128, 256])
+@torch.no_grad()
+def test_fp16_dense_fp32_oracle(device, d, before, after, frames, chunk, radius, anchor):
+    """FP16 activations (paper_window.py:206 accepts BF16 and FP16): fp16 output against the
+    dense fp32 oracle of the fp16 inputs at the bf16 tests' tolerances (fp16 holds 3 more
+    mantissa bits, so the relative error bound is 4x tighter), LSE as for bf16; the fused
+    gate equals the separate fp16 product; padding rows zero."""
+    torch.manual_seed(900 + d + frames)
+    spatial = 300 if frames == 3 else 3
+    layout = vw.SequenceLayout(before + frames * spatial + after, before, frames, spatial)
+    bounds = vw.window_bounds(frames, radius, chunk)
+    backing = torch.randn(layout.seq_len + 5, 3, 5, d, device=device, dtype=torch.float16)
+    q, k, v = [backing[:, i, 1:4] for i in range(3)]
+    plan = vw.prepare_paper_window_plan(layout, bounds, anchor, device=device)
+    out, lse = vw.paper_window_attention(q, k, v, plan, enabled=True, return_lse=True)
+    assert out.dtype == torch.float16 and out.shape == q.shape
+    s = layout.seq_len
+    mask = ow.dense_mask(s, before, frames, spatial, bounds, anchor)
+    expected, el = ow.attention_dense(q[:s].cpu(), k[:s].cpu(), v[:s].cpu(), mask, d ** -.5)
+    got = out[:s].float().cpu()
+    torch.testing.assert_close(got, expected, atol=.003, rtol=.004)
+    assert ((got - expected).norm() / expected.norm()) < 1e-3
+    torch.testing.assert_close(lse[:s].cpu(), el, atol=3e-5, rtol=3e-6)
+    assert out[s:].count_nonzero() == 0
+    gate = torch.rand(q.shape[0], 3, device=device).to(torch.float16)
+    gated = vw.paper_window_attention(q, k, v, plan, enabled=True, gate=gate)
+    assert torch.equal(gated[:s], out[:s] * gate[:s, :, None])
+
+
+@torch.no_grad()
+def test_fp16_rejects_mxfp8_output(device):
+    from vdn_amd import mxfp8 as vm
+    layout = vw.SequenceLayout(6, 0, 2, 3)
+    plan = vw.prepare_paper_window_plan(layout, vw.window_bounds(2, 1), device=device)
+    q = torch.randn(6, 2, 128, device=device, dtype=torch.float16)
+    codes, scales = vm.empty_activation(6, 256, device)
+    with pytest.raises(ValueError, match="bf16"):
+        vw.paper_window_attention(q, q, q, plan, enabled=True, out_mxfp8=(codes, scales, 0))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("d,r,tables", [(128, 128, torch.float32), (128, 96, torch.bfloat16),
+                                        (64, 32, torch.float16), (256, 192, torch.float32),
+                                        (128, None, None)])
+@torch.no_grad()
+def test_rope_fp16_fp32_activations(device, dtype, d, r, tables):
+    """FP16 and FP32 activations (paper_qk_rope.py:168-186): the kernel against the oracle's
+    rounding points in the activation dtype (fp32: none), with weights of the activation
+    dtype (q) and fp32 (k), tables of any dtype cast to the activation dtype; and against the
+    eager disabled path on the same device."""
+    g = torch.Generator().manual_seed(d + (r or 0))
+    t, heads = 29, 5
+    storage = (torch.randn(t, 3 * heads * d, generator=g) * 2).to(dtype)
+    q = storage[:, :heads * d].view(t, heads, d)
+    k = storage[:, heads * d:2 * heads * d].view(t, heads, d)
+    qw = (torch.rand(d, generator=g) + 0.5).to(dtype)
+    kw = (torch.rand(d, generator=g) + 0.5).float()
+    c = s = None
+    if r is not None:
+        angles = torch.randn(t, r // 2, generator=g) * 3
+        c = torch.cat((angles.cos(), angles.cos()), 1).to(tables)
+        s = torch.cat((angles.sin(), angles.sin()), 1).to(tables)
+    dev = lambda x: None if x is None else x.to(device)
+    qo, ko = vw.paper_qk_rmsnorm_rope(dev(q), dev(k), dev(qw), dev(kw), 1e-6, dev(c), dev(s),
+                                      enabled=True)
+    eq, ek = vw.paper_qk_rmsnorm_rope(dev(q), dev(k), dev(qw), dev(kw), 1e-6, dev(c), dev(s),
+                                      enabled=False)
+    tol = dict(atol=4e-3, rtol=2e-3) if dtype == torch.float16 else dict(atol=2e-5, rtol=2e-5)
+    for out, eager, raw, w in ((qo, eq, q, qw), (ko, ek, k, kw)):
+        assert out.dtype == dtype and out.is_contiguous() and out.shape == (t, heads, d)
+        expected = ow.qk_rope(raw, w, 1e-6, None if c is None else c.float(),
+                              None if s is None else s.float())
+        torch.testing.assert_close(out.cpu(), expected, **tol)
+        torch.testing.assert_close(out, eager, **tol)

@@ -51,8 +51,8 @@ SIGNATURES = {
                             _i64, _f32, _ptr, _i64, _i64, _ptr, _i64, _i64, _i32, _i32, _i64,
                             _i32, _i32, _ptr, _ptr, _ptr],
     "vdn_window_attention": [_ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i32,
-                             _ptr, _ptr, _i32, _i32, _f32, _ptr, _i64, _i64, _ptr, _i64, _i64,
-                             _ptr, _i64, _i64, _ptr],
+                             _ptr, _ptr, _i32, _i32, _i32, _f32, _ptr, _i64, _i64, _ptr, _i64,
+                             _i64, _ptr, _i64, _i64, _ptr],
     "vdn_window_attention_mxfp8": [_ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr,
                                    _i32, _ptr, _ptr, _i32, _f32, _ptr, _i64, _i64, _ptr, _f32,
                                    _ptr, _ptr, _i64, _i32, _ptr],

@@ -43,9 +43,11 @@ GATE_ROWS = 128      # rows per gate-projection workgroup (per-frame partial sum
 
 def gate_weight(w: "BlockWeights", cfg: "BlockConfig") -> torch.Tensor:
     """[384, hidden] bf16 operand of vdn_gate_projection: softmax-gate rows, beta rows (each
-    group zero-padded to 64), output-gate down (128) and FrameKDAAlpha down (128)."""
-    if cfg.heads > GATE_GROUP or cfg.heads % 2 or cfg.head_dim != 128 or cfg.hidden % 32:
-        raise NotImplementedError("the gate projection needs an even head count <= 64, "
+    group zero-padded to 64), output-gate down (128) and FrameKDAAlpha down (128). An odd head
+    count runs as the next even one (the kernel stores head pairs): the extra gate and beta
+    rows are the zero padding, and gate_projection drops their columns."""
+    if cfg.heads + cfg.heads % 2 > GATE_GROUP or cfg.head_dim != 128 or cfg.hidden % 32:
+        raise NotImplementedError("the gate projection needs at most 64 heads (63 if odd), "
                                   "head_dim 128 and hidden % 32 == 0")
     out = torch.zeros(2 * GATE_GROUP + 256, cfg.hidden, dtype=torch.bfloat16,
                       device=w.soft_gate_w.device)
@@ -59,7 +61,10 @@ def gate_weight(w: "BlockWeights", cfg: "BlockConfig") -> torch.Tensor:
 def gate_projection(x1, weight, gate_bias, heads, frames, spatial):
     """soft_gate [T, heads], beta [T, heads], gate_down [T, 128] (bf16) and the per-frame
     column sums of x1 @ alpha_down^T [frames * ceil(spatial / 128), 128] (fp32) of x1
-    [frames * spatial, hidden] bf16 (attention_gates.py:52-55, tensor_parallel.py:194-198)."""
+    [frames * spatial, hidden] bf16 (attention_gates.py:52-55, tensor_parallel.py:194-198).
+    An odd head count runs the kernel on heads + 1 columns (weight rows `heads` of the gate
+    and beta groups are zero in gate_weight, the bias gets a zero) and returns the first
+    `heads` columns."""
     t, hd = x1.shape
     for name, ten in (("x1", x1), ("weight", weight), ("gate_bias", gate_bias)):
         _lib.require_gpu(ten, name)
@@ -72,14 +77,23 @@ def gate_projection(x1, weight, gate_bias, heads, frames, spatial):
     if gate_bias.numel() < heads or not gate_bias.is_contiguous():
         raise ValueError("gate_bias must be contiguous with heads entries")
     dev = x1.device
-    soft = torch.empty(t, heads, dtype=torch.bfloat16, device=dev)
-    beta = torch.empty(t, heads, dtype=torch.bfloat16, device=dev)
+    odd = heads % 2
+    if odd:
+        if heads + 1 > GATE_GROUP:
+            raise ValueError("an odd head count must be below 64")
+        gate_bias = torch.cat((gate_bias.reshape(-1)[:heads],
+                               torch.zeros(1, dtype=torch.bfloat16, device=dev)))
+    hk = heads + odd
+    soft = torch.empty(t, hk, dtype=torch.bfloat16, device=dev)
+    beta = torch.empty(t, hk, dtype=torch.bfloat16, device=dev)
     down = torch.empty(t, 128, dtype=torch.bfloat16, device=dev)
     bpf = -(-spatial // GATE_ROWS)
     partial = torch.empty(frames * bpf, 128, dtype=torch.float32, device=dev)
-    _lib.call("vdn_gate_projection", x1.data_ptr(), x1.stride(0), hd, weight.data_ptr(), heads,
+    _lib.call("vdn_gate_projection", x1.data_ptr(), x1.stride(0), hd, weight.data_ptr(), hk,
               frames, spatial, gate_bias.data_ptr(), soft.data_ptr(), beta.data_ptr(),
               down.data_ptr(), partial.data_ptr(), _lib.stream(dev))
+    if odd:
+        soft, beta = soft[:, :heads].contiguous(), beta[:, :heads].contiguous()
     return soft, beta, down, partial
 
 
@@ -106,10 +120,13 @@ def frame_alpha(partial, frames, spatial, up_w, dt_bias, a_log, heads, head_dim)
 
 def adaln_tables(temb, weight, bias, hidden):
     """Six [m, hidden] bf16 tables Linear(bf16(SiLU(temb in fp32)), weight, bias) in the order
-    shift, scale, gate (attention), shift, scale, gate (MLP) (paper_adaln.py:174-188); temb
-    bf16 or fp32."""
+    shift, scale, gate (attention), shift, scale, gate (MLP) (paper_adaln.py:174-188). The
+    kernel reads bf16 or fp32 temb and runs SiLU in fp32; any other floating dtype is taken
+    through temb.float() first, as the reference's SiLU(temb.float()) does (exact for fp16)."""
     if temb.dtype not in (torch.bfloat16, torch.float32):
-        raise ValueError("temb must be bf16 or fp32")
+        if not temb.dtype.is_floating_point:
+            raise ValueError("temb must be a floating-point tensor")
+        temb = temb.float()
     _lib.require_gpu(temb, "temb")
     for name, t in (("weight", weight),) + ((("bias", bias),) if bias is not None else ()):
         _lib.require_gpu(t, name)
@@ -267,8 +284,6 @@ class HybridDiTBlock(nn.Module):
     def adaln_tables(self, temb):
         """6 tables [1, H]: shift/scale/gate attention, then MLP (paper_adaln.py:174-188, 205-212)."""
         k = self.keep
-        if temb.dtype != torch.float32:
-            temb = temb.to(torch.bfloat16)   # SiLU runs in fp32 on either
         return adaln_tables(temb, k["adaln_w"], k["adaln_b"], self.cfg.hidden)
 
     def _side_stream(self, device):
@@ -292,11 +307,20 @@ class HybridDiTBlock(nn.Module):
     # --------------------------------------------------------------- forward ----
     @torch.no_grad()
     def forward(self, hidden, temb, context, layout: vw.SequenceLayout, rope, window_plan,
-                cross_plan, return_parts=False):
+                cross_plan, return_parts=False, guard=None):
         """hidden [T, H] bf16 (video rows), temb [1, H], context [L, H] bf16; rope = (cos, sin)
         [T, 128]; window_plan from prepare_paper_window_plan; cross_plan from cross_attention_plan.
         Returns the new hidden [T, H] (a fresh tensor); with return_parts also a dict of
-        intermediate copies (tables, x1, qkv, soft, far, h1, co, h2) for checking."""
+        intermediate copies (tables, x1, qkv, soft, far, h1, co, h2) for checking.
+
+        guard: an object with predicate(parts) (the reference's CoordinatedFiniteGuard,
+        paper_runtime.py:43-50, or FinitePredicate below). Each MXFP8 producer's finite
+        predicate is handed to it as a device bool tensor, as paper_block_forward does
+        (fused_block.py:144-155): the three prenorm producers' per-row flags and, last, one
+        flag for every projection output (q, k, v and the gated residuals in bf16, the FFN
+        activation before its quantization). The branch outputs are quantized in their kernels
+        and reach the [O | O_lin] projection, whose output carries any inf/NaN they hold.
+        Nothing is read on the host."""
         cfg, k = self.cfg, self.keep
         T, hd = hidden.shape
         heads, d = cfg.heads, cfg.head_dim
@@ -306,15 +330,21 @@ class HybridDiTBlock(nn.Module):
         shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = self.adaln_tables(temb)
         idx = self._table_index(T, dev)
         parts = {} if return_parts else None
+        nf = None if guard is None else torch.zeros(1, dtype=torch.int32, device=dev)
+
+        def producer(finite):
+            if guard is not None:
+                guard.predicate(finite)
 
         def snap(name, t):
             if parts is not None:
                 parts[name] = t.clone() if isinstance(t, torch.Tensor) else t
 
         # ---- hybrid self-attention ----
-        x1, q1, s1, _ = mx.launch_prenorm_quantize(hidden, k["norm1"], cfg.eps, scale_msa,
-                                                   shift_msa, idx, write_bf16=True)
-        qkv = self.qkv.forward_quantized(q1, s1, rows=T)
+        x1, q1, s1, fin = mx.launch_prenorm_quantize(hidden, k["norm1"], cfg.eps, scale_msa,
+                                                     shift_msa, idx, write_bf16=True)
+        producer(fin)
+        qkv = self.qkv.forward_quantized(q1, s1, rows=T, nonfinite=nf)
         snap("tables", (shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp))
         snap("x1", x1)
         snap("qkv", qkv)
@@ -381,19 +411,21 @@ class HybridDiTBlock(nn.Module):
         del qkv, raw_q, raw_k, value, lin_gate, gate_down
         # the first residual update writes a fresh tensor (no copy of the input)
         h = torch.empty_like(hidden)
-        self.o_cat.forward_quantized(qb, sb, rows=T, out=h, residual=hidden, gate=gate_msa)
+        self.o_cat.forward_quantized(qb, sb, rows=T, out=h, residual=hidden, gate=gate_msa,
+                                     nonfinite=nf)
         snap("h1", h)
         del qb, sb
 
         # ---- cross-attention to the context rows ----
         zeros = self._zeros(dev)
-        _, q3, s3, _ = mx.launch_prenorm_quantize(h, k["norm3"], cfg.eps, zeros, zeros, idx,
-                                                  write_bf16=False)
-        cq = self.cq.forward_quantized(q3, s3, rows=T).view(T, heads, d)
+        _, q3, s3, fin = mx.launch_prenorm_quantize(h, k["norm3"], cfg.eps, zeros, zeros, idx,
+                                                    write_bf16=False)
+        producer(fin)
+        cq = self.cq.forward_quantized(q3, s3, rows=T, nonfinite=nf).view(T, heads, d)
         cx, csx = mx.launch_quantize(context)
         L = context.shape[0]
-        ck = self.ck.forward_quantized(cx, csx, rows=L).view(L, heads, d)
-        cv = self.cv.forward_quantized(cx, csx, rows=L).view(L, heads, d)
+        ck = self.ck.forward_quantized(cx, csx, rows=L, nonfinite=nf).view(L, heads, d)
+        cv = self.cv.forward_quantized(cx, csx, rows=L, nonfinite=nf).view(L, heads, d)
         ck = vw.qk_rmsnorm(ck, k["norm_kc"], cfg.eps)
         if parts is None:
             # the queries' RMSNorm runs in the attention kernel as it loads them
@@ -407,19 +439,42 @@ class HybridDiTBlock(nn.Module):
             qo, so = mx.launch_quantize(co.view(T, inner))
             del co
         del cq, ck, cv
-        self.co.forward_quantized(qo, so, rows=T, out=h, residual=h)
+        self.co.forward_quantized(qo, so, rows=T, out=h, residual=h, nonfinite=nf)
         del qo, so
         snap("h2", h)
 
         # ---- FFN ----
-        _, q4, s4, _ = mx.launch_prenorm_quantize(h, k["norm2"], cfg.eps, scale_mlp, shift_mlp,
-                                                  idx, write_bf16=False)
+        _, q4, s4, fin = mx.launch_prenorm_quantize(h, k["norm2"], cfg.eps, scale_mlp,
+                                                    shift_mlp, idx, write_bf16=False)
+        producer(fin)
         # up + activation + MXFP8 in the GEMM's epilogue (for SwiGLU the [a | g] halves meet
         # in it: tp_ff_forward's project + launch_swiglu_quantize, tensor_parallel.py:147-161)
-        q5, s5 = self.up.forward_act_quantized(q4, s4, rows=T, act=cfg.ffn_act)
+        q5, s5 = self.up.forward_act_quantized(q4, s4, rows=T, act=cfg.ffn_act, nonfinite=nf)
         snap("ffn_codes", (q5, s5))
-        self.down.forward_quantized(q5, s5, rows=T, out=h, residual=h, gate=gate_mlp)
+        self.down.forward_quantized(q5, s5, rows=T, out=h, residual=h, gate=gate_mlp,
+                                    nonfinite=nf)
+        if guard is not None:
+            guard.predicate(nf == 0)
         return (h, parts) if return_parts else h
+
+
+class FinitePredicate:
+    """A single-GPU finite guard with the reference guard's predicate seam
+    (CoordinatedFiniteGuard.predicate / check, paper_runtime.py:43-50, 71-117, without the
+    multi-rank vote): predicate() folds a device bool tensor into one device flag with no
+    host sync; check() is the one explicit host read and raises FloatingPointError."""
+
+    def __init__(self, device):
+        self.pending = torch.ones((), dtype=torch.bool, device=device)
+
+    def predicate(self, parts: torch.Tensor) -> None:
+        self.pending.logical_and_(parts.all())
+
+    def check(self, label: str) -> None:
+        ok = bool(self.pending.item())
+        self.pending.fill_(True)
+        if not ok:
+            raise FloatingPointError(f"nonfinite value before {label}")
 
 
 def cross_attention_plan(num_queries: int, num_keys: int, device) -> vw.DevicePlan:
@@ -456,7 +511,7 @@ def cross_attention(q, k, v, plan: vw.DevicePlan, scale, out_mxfp8=None, q_norm=
     _lib.call("vdn_window_attention", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
               k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
               plan.blocks.data_ptr(), plan.nblocks, plan.intervals.data_ptr(),
-              plan.counts.data_ptr(), h, d, float(scale), None, 0, 0, out.data_ptr(),
+              plan.counts.data_ptr(), h, d, 0, float(scale), None, 0, 0, out.data_ptr(),
               out.stride(0), out.stride(1), None, 0, 0, _lib.stream(q.device))
     return out
 

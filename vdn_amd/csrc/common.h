@@ -29,6 +29,8 @@ typedef __bf16 bf16;
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -113,6 +115,20 @@ __device__ __forceinline__ void round_bf16_pair(float& a, float& b) {
   asm volatile("" : "+v"(p));
   a = __uint_as_float(p << 16);
   b = __uint_as_float(p & 0xffff0000u);
+}
+
+// fp16 storage: exact widening, round-to-nearest-even narrowing (v_cvt_f16_f32), as torch's
+// float <-> half conversions.
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+__device__ __forceinline__ float round_f16(float f) {
+  return static_cast<float>(static_cast<_Float16>(f));
 }
 
 // The four values of v rounded to bf16, two per conversion (as round_bf16_pair).

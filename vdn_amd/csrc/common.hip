@@ -28,4 +28,4 @@ int check_launch(const char* what) {
 
 VDN_API const char* vdn_last_error(void) { return vdn::g_last_error; }
 
-VDN_API int vdn_abi_version(void) { return 5; }
+VDN_API int vdn_abi_version(void) { return 6; }

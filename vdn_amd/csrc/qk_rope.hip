@@ -1,10 +1,13 @@
-// QK RMSNorm + rotate-half RoPE for gfx950 (bf16 activations).
+// QK RMSNorm + rotate-half RoPE for gfx950 (bf16 activations; fp16 and fp32 through the
+// general kernel).
 //
 // Per (token, head) row x of D channels (reference src/models/softmax_attention/
-// paper_qk_rope.py:105-140, eager semantics :82-95):
-//   n   = bf16((x * rsqrt(sum(x^2) / D + eps)) * w)            (fp32, one rounding)
-//   for channel i < R: out = bf16(bf16(n_i * c_i) + bf16(r_i * s_i)),
-//       r_i = -n_{i+R/2} (i < R/2), n_{i-R/2} (R/2 <= i < R); c, s = table values in bf16
+// paper_qk_rope.py:105-140, eager semantics :82-95), with act() the rounding to the
+// activation dtype (none for fp32):
+//   n   = act((x * rsqrt(sum(x^2) / D + eps)) * w)             (fp32, one rounding)
+//   for channel i < R: out = act(act(n_i * c_i) + act(r_i * s_i)),
+//       r_i = -n_{i+R/2} (i < R/2), n_{i-R/2} (R/2 <= i < R); c, s = table values in the
+//       activation dtype
 //   channels i >= R pass n through.
 // A row is held by D/8 lanes (8 channels each); the rotate partner is exchanged through a
 // per-row LDS line, which keeps arbitrary even R <= D exact (qk_rope_kernel), or, for the
@@ -17,13 +20,29 @@ namespace vdn {
 namespace {
 
 struct RopeArgs {
-  const uint16_t* x;
+  const uint16_t* x;   // activation storage (fp32 rows are read through this pointer's bytes)
   int64_t st, sh, sd;  // token, head, channel strides (elements)
   const void* w;
   int64_t ws;
   int w_f32;
-  uint16_t* out;  // contiguous [T, H, D]
+  uint16_t* out;  // contiguous [T, H, D] of the activation dtype
 };
+
+// Activation dtype of the general kernel: 0 bf16, 1 fp16, 2 fp32. Storage of a weight or a
+// table that is not fp32 is the activation dtype.
+template <int kT>
+__device__ __forceinline__ float act_load(const void* p, int64_t i) {
+  if constexpr (kT == 2) return static_cast<const float*>(p)[i];
+  else if constexpr (kT == 1) return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+  else return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+template <int kT>
+__device__ __forceinline__ float act_round(float f) {
+  if constexpr (kT == 2) return f;
+  else if constexpr (kT == 1) return round_f16(f);
+  else return round_bf16(f);
+}
 
 // Eight consecutive values (bf16 storage or fp32) starting at element `off`, as floats;
 // fp32 values are rounded to bf16 when `round` is set.
@@ -58,14 +77,16 @@ __device__ __forceinline__ void load8_row(const uint16_t* __restrict__ p, float*
   }
 }
 
-// kVec: unit channel strides, 16-byte aligned rows, weights and table rows, rot % 8 == 0;
-// every load is one (or two, fp32) 16-byte access per lane.
-template <int kD, bool kVec>
+// kVec (bf16 only): unit channel strides, 16-byte aligned rows, weights and table rows,
+// rot % 8 == 0; every load is one (or two, fp32) 16-byte access per lane. kT: activation
+// dtype (0 bf16, 1 fp16, 2 fp32).
+template <int kD, bool kVec, int kT = 0>
 __global__ void __launch_bounds__(256)
 qk_rope_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float eps,
                const void* __restrict__ cos_t, const void* __restrict__ sin_t, int64_t c_st,
                int64_t c_sd, int64_t s_st, int64_t s_sd, int table_f32, int rot) {
 #pragma clang fp contract(off)
+  static_assert(!kVec || kT == 0, "the vector form reads bf16 rows");
   constexpr int kLanes = kD / 8;
   constexpr int kRowsPerBlock = 256 / kLanes;
   __shared__ float line[kRowsPerBlock][kD + 1];
@@ -87,8 +108,9 @@ qk_rope_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float eps,
       for (int i = 0; i < 8; ++i) v[i] = 0.f;
     }
   } else {
+    const int64_t base = t * a.st + h * a.sh + static_cast<int64_t>(sub) * 8 * a.sd;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = live ? bf16_bits_to_f32(src[i * a.sd]) : 0.f;
+    for (int i = 0; i < 8; ++i) v[i] = live ? act_load<kT>(a.x, base + i * a.sd) : 0.f;
   }
   float ss = 0.f;
 #pragma unroll
@@ -104,14 +126,13 @@ qk_rope_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float eps,
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int c = sub * 8 + i;
-      wv[i] = a.w_f32 ? static_cast<const float*>(a.w)[c * a.ws]
-                      : bf16_bits_to_f32(static_cast<const uint16_t*>(a.w)[c * a.ws]);
+      wv[i] = a.w_f32 ? static_cast<const float*>(a.w)[c * a.ws] : act_load<kT>(a.w, c * a.ws);
     }
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int c = sub * 8 + i;
-    n[i] = round_bf16((v[i] * inv) * wv[i]);
+    n[i] = act_round<kT>((v[i] * inv) * wv[i]);
     line[slot][c] = n[i];
   }
   __syncthreads();
@@ -132,23 +153,34 @@ qk_rope_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float eps,
       const float other = c < half ? -line[slot][c + half] : line[slot][c - half];
       float cv, sv;
       if (table_f32) {
-        cv = round_bf16(static_cast<const float*>(cos_t)[t * c_st + c * c_sd]);
-        sv = round_bf16(static_cast<const float*>(sin_t)[t * s_st + c * s_sd]);
+        cv = act_round<kT>(static_cast<const float*>(cos_t)[t * c_st + c * c_sd]);
+        sv = act_round<kT>(static_cast<const float*>(sin_t)[t * s_st + c * s_sd]);
       } else {
-        cv = bf16_bits_to_f32(static_cast<const uint16_t*>(cos_t)[t * c_st + c * c_sd]);
-        sv = bf16_bits_to_f32(static_cast<const uint16_t*>(sin_t)[t * s_st + c * s_sd]);
+        cv = act_load<kT>(cos_t, t * c_st + c * c_sd);
+        sv = act_load<kT>(sin_t, t * s_st + c * s_sd);
       }
-      o[i] = round_bf16(round_bf16(n[i] * cv) + round_bf16(other * sv));
+      o[i] = act_round<kT>(act_round<kT>(n[i] * cv) + act_round<kT>(other * sv));
     } else {
       o[i] = n[i];
     }
   }
   if (live) {
-    uint16_t* dst = a.out + row * kD + sub * 8;
-    u32x4 packed;
+    if constexpr (kT == 2) {
+      float* dst = reinterpret_cast<float*>(a.out) + row * kD + sub * 8;
+      *reinterpret_cast<f32x4*>(dst) = f32x4{o[0], o[1], o[2], o[3]};
+      *reinterpret_cast<f32x4*>(dst + 4) = f32x4{o[4], o[5], o[6], o[7]};
+    } else {
+      uint16_t* dst = a.out + row * kD + sub * 8;
+      u32x4 packed;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) packed[i] = pack_bf16x2(o[2 * i], o[2 * i + 1]);
-    *reinterpret_cast<u32x4*>(dst) = packed;
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (kT == 1)
+          packed[i] = f32_to_f16_bits(o[2 * i]) | (static_cast<uint32_t>(f32_to_f16_bits(o[2 * i + 1])) << 16);
+        else
+          packed[i] = pack_bf16x2(o[2 * i], o[2 * i + 1]);
+      }
+      *reinterpret_cast<u32x4*>(dst) = packed;
+    }
   }
 }
 
@@ -282,11 +314,12 @@ qk_rope_token128_kernel(RopeArgs q, RopeArgs k, int64_t tokens, int heads, float
 using namespace vdn;
 
 // Reference: paper_qk_rmsnorm_rope (src/models/softmax_attention/paper_qk_rope.py:145-211).
-// q, k: bf16 [tokens, heads, D] with arbitrary element strides; weights [D] (stride w_s,
-// bf16 or fp32 per flags bit0 for q / bit1 for k); cos/sin (nullable: norm only): [tokens, R]
-// with strides, fp32 when flags bit2 else bf16; qo, ko: contiguous bf16 [tokens, heads, D].
-// flags bit3: q only (k, k_w and ko may be null), for a lone RMSNorm'd operand such as the
-// queries of a cross-attention whose keys have another row count.
+// q, k: [tokens, heads, D] of the activation dtype (flags bits 4-5: 0 bf16, 1 fp16, 2 fp32)
+// with arbitrary element strides; weights [D] (stride w_s, fp32 per flags bit0 for q / bit1
+// for k, else the activation dtype); cos/sin (nullable: norm only): [tokens, R] with strides,
+// fp32 when flags bit2 else the activation dtype; qo, ko: contiguous [tokens, heads, D] of the
+// activation dtype. flags bit3: q only (k, k_w and ko may be null), for a lone RMSNorm'd
+// operand such as the queries of a cross-attention whose keys have another row count.
 VDN_API int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64_t q_sd,
                                 const void* k, int64_t k_st, int64_t k_sh, int64_t k_sd,
                                 const void* q_w, int64_t q_ws, const void* k_w, int64_t k_ws,
@@ -304,6 +337,8 @@ VDN_API int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64
   if ((cos_t == nullptr) != (sin_t == nullptr) || rot < 0 || rot > head_dim || rot % 2 ||
       (cos_t != nullptr && rot == 0))
     return set_error(kInvalidArgument, "%s: invalid rotary width %d", name, rot);
+  const int act = (flags >> 4) & 3;
+  if (act > 2) return set_error(kInvalidArgument, "%s: activation dtype must be 0, 1 or 2", name);
   if (tokens == 0) return kOk;
   const RopeArgs qa{static_cast<const uint16_t*>(q), q_st, q_sh, q_sd, q_w, q_ws, flags & 1,
                     static_cast<uint16_t*>(qo)};
@@ -318,13 +353,16 @@ VDN_API int vdn_qk_rmsnorm_rope(const void* q, int64_t q_st, int64_t q_sh, int64
   auto operand_vec = [&](const RopeArgs& o) {
     return o.sd == 1 && o.st % 8 == 0 && o.sh % 8 == 0 && al16(o.x) && o.ws == 1 && al16(o.w);
   };
-  const bool vec = operand_vec(qa) && (q_only || operand_vec(ka)) && r % 8 == 0 &&
+  const bool vec = act == 0 && operand_vec(qa) && (q_only || operand_vec(ka)) && r % 8 == 0 &&
                    (r == 0 || (c_sd == 1 && s_sd == 1 && c_st % tab_align == 0 &&
                                s_st % tab_align == 0 && al16(cos_t) && al16(sin_t)));
 #define VDN_ROPE(D)                                                                             \
-  if (vec) VDN_ROPE_V(D, true) else VDN_ROPE_V(D, false)
-#define VDN_ROPE_V(D, V)                                                                        \
-  hipLaunchKernelGGL((qk_rope_kernel<D, V>), dim3(static_cast<unsigned>((rows + 256 / (D / 8) - 1) / \
+  if (vec) VDN_ROPE_V(D, true, 0)                                                               \
+  else if (act == 0) VDN_ROPE_V(D, false, 0)                                                    \
+  else if (act == 1) VDN_ROPE_V(D, false, 1)                                                    \
+  else VDN_ROPE_V(D, false, 2)
+#define VDN_ROPE_V(D, V, T)                                                                     \
+  hipLaunchKernelGGL((qk_rope_kernel<D, V, T>), dim3(static_cast<unsigned>((rows + 256 / (D / 8) - 1) / \
                                                                     (256 / (D / 8))),           \
                           q_only ? 1 : 2),                                                      \
                      dim3(256), 0, st, qa, ka, tokens, heads, eps, cos_t, sin_t, c_st, c_sd,    \

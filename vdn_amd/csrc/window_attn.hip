@@ -1,4 +1,4 @@
-// Frame-window softmax attention for gfx950 (bf16, head_dim 128), flash style.
+// Frame-window softmax attention for gfx950 (bf16 or fp16; head_dim 64, 128, 256), flash style.
 //
 // Replaces the packed varlen passes of paper_window_attention
 // (src/models/softmax_attention/paper_window.py:182-243) and the softmax gate
@@ -55,6 +55,47 @@ __device__ __forceinline__ bf16x4_t lds_read_tr(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
       (lds_bf16x4_t*)((__attribute__((address_space(3))) char*)(p)));
 }
+
+// the transpose read's own fp16 vector type (four __fp16), reinterpreted as f16x4
+typedef __fp16 fp16x4_raw __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) fp16x4_raw lds_f16x4_t;
+
+// The 16-bit element type of a kernel instance: bf16 (the block's) or fp16 (the reference's
+// other varlen dtype). Both share the storage layout, the LDS swizzles and the transpose
+// reads; they differ in the MFMA, the conversions of P and the output's rounding.
+template <bool kF16>
+struct Elem;
+
+template <>
+struct Elem<false> {
+  typedef __bf16 type;
+  typedef bf16x8 x8;
+  typedef bf16x4_t x4;
+  static __device__ __forceinline__ x4 read_tr(const uint16_t* p) { return lds_read_tr(p); }
+  static __device__ __forceinline__ f32x16 mfma(x8 a, x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float to_f32(uint16_t h) { return bf16_bits_to_f32(h); }
+  static __device__ __forceinline__ float round(float f) { return round_bf16(f); }
+  static __device__ __forceinline__ uint16_t bits(float f) { return f32_to_bf16_bits(f); }
+};
+
+template <>
+struct Elem<true> {
+  typedef _Float16 type;
+  typedef f16x8 x8;
+  typedef f16x4 x4;
+  static __device__ __forceinline__ x4 read_tr(const uint16_t* p) {
+    return __builtin_bit_cast(x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+        (lds_f16x4_t*)((__attribute__((address_space(3))) char*)(p))));
+  }
+  static __device__ __forceinline__ f32x16 mfma(x8 a, x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float to_f32(uint16_t h) { return f16_bits_to_f32(h); }
+  static __device__ __forceinline__ float round(float f) { return round_f16(f); }
+  static __device__ __forceinline__ uint16_t bits(float f) { return f32_to_f16_bits(f); }
+};
 
 // Key tile of each head_dim: 128 keys, 64 for D = 256 (whose Q and O fragments take 192
 // registers; the tile buffers then still hold the epilogue's 256 x 256 output block).
@@ -139,8 +180,9 @@ struct Layout {
 };
 
 // kWaves waves of 32 queries each: a workgroup owns kBM = 32 kWaves queries, and every K/V
-// tile it loads serves all of them. kD is the head dimension (64, 128 or 256).
-template <int kD, int kWaves, bool kMx>
+// tile it loads serves all of them. kD is the head dimension (64, 128 or 256); kF16 selects
+// fp16 activations (and gate, output) instead of bf16.
+template <int kD, int kWaves, bool kMx, bool kF16 = false>
 __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restrict__ grp_kv,
                    const int* __restrict__ grp_n, int nblocks, int heads, float scale_log2,
@@ -152,6 +194,9 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
   constexpr int kChunks = kD / 8;     // 16-byte chunks per tile row
   constexpr int kSegRows = 64 / kChunks;  // rows per 1 KB DMA segment (one wave instruction)
   static_assert(!kMx || kD == 128, "the MXFP8 destination holds one head per 128 columns");
+  static_assert(!kMx || !kF16, "the MXFP8 destination takes bf16 attention");
+  typedef Elem<kF16> E;
+  typedef typename E::x8 x8;
   // Separate arrays per buffer: with distinct LDS objects the compiler can tell a tile
   // prefetch into one buffer from reads of the other and does not wait on the prefetch.
   __shared__ __attribute__((aligned(1024))) uint16_t sK0[kBN * kD];
@@ -192,13 +237,13 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
   // waves without a live query still load their share of every tile and meet every barrier,
   // but skip the arithmetic, so the live waves of their SIMDs run at the full MFMA rate.
   const bool wave_live = q0 + wave * 32 < q1;
-  bf16x8 qf[kD / 16];
+  x8 qf[kD / 16];
   {
     const uint16_t* src = in.q + static_cast<int64_t>(q_live ? my_q : q0) * in.q_st + h * in.q_sh;
 #pragma unroll
     for (int ks = 0; ks < kD / 16; ++ks) {
       const u32x4 w = *reinterpret_cast<const u32x4*>(src + 16 * ks + 8 * g);
-      qf[ks] = __builtin_bit_cast(bf16x8, w);
+      qf[ks] = __builtin_bit_cast(x8, w);
     }
   }
 
@@ -284,8 +329,8 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
 #pragma unroll
       for (int ks = 0; ks < kD / 16; ++ks) {
         const int chunk = (2 * ks + g) ^ swz_k<kD>(row);
-        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(tk + row * kD + chunk * 8);
-        s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[ks], s[kt], 0, 0, 0);
+        const x8 ka = *reinterpret_cast<const x8*>(tk + row * kD + chunk * 8);
+        s[kt] = E::mfma(ka, qf[ks], s[kt]);
       }
     }
     // ---- online softmax (exp2 domain; scores scaled inside the exponent's fma) ----
@@ -330,26 +375,26 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     // ---- Oᵀ += Vᵀ Pᵀ, 16 keys per MFMA ----
 #pragma unroll
     for (int c = 0; c < kBN / 16; ++c) {
-      bf16x8 pb;
+      x8 pb;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pb[j] = static_cast<__bf16>(s[c >> 1][(c & 1) * 8 + j]);
+      for (int j = 0; j < 8; ++j) pb[j] = static_cast<typename E::type>(s[c >> 1][(c & 1) * 8 + j]);
 #pragma unroll
       for (int db = 0; db < kDB; ++db) {
-        bf16x4_t lo, hi;
+        typename E::x4 lo, hi;
         {
           const int row = 16 * c + tr_row;
           const int e = 32 * db + tr_col;
           const int chunk = (e >> 3) ^ swz_v<kD>(row);
-          lo = lds_read_tr(tv + row * kD + chunk * 8 + (e & 7));
+          lo = E::read_tr(tv + row * kD + chunk * 8 + (e & 7));
         }
         {
           const int row = 16 * c + 8 + tr_row;
           const int e = 32 * db + tr_col;
           const int chunk = (e >> 3) ^ swz_v<kD>(row);
-          hi = lds_read_tr(tv + row * kD + chunk * 8 + (e & 7));
+          hi = E::read_tr(tv + row * kD + chunk * 8 + (e & 7));
         }
-        const bf16x8 va{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, o[db], 0, 0, 0);
+        const x8 va{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[db] = E::mfma(va, pb, o[db]);
       }
     }
   };
@@ -436,7 +481,8 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
   __syncthreads();  // the epilogue reuses the K buffers
 
   // ---- epilogue: O / l, optional gate, through LDS to coalesced rows ----
-  // [kBM queries][kD channels] bf16 staged across the tile buffers, kBN queries per buffer
+  // [kBM queries][kD channels] 16-bit values staged across the tile buffers, kBN queries per
+  // buffer
   auto stage_rows = [&](int r) -> uint16_t* {
     const int which = r / kBN;  // uniform per wave for both uses below
     return which == 0 ? sK0 : which == 1 ? sK1 : which == 2 ? sV0 : sV1;
@@ -444,15 +490,15 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
   const int qr = wave * 32 + col;
   uint16_t* sO = stage_rows(qr);
   float gv = 1.f;
-  if (gate != nullptr && q_live) gv = bf16_bits_to_f32(gate[static_cast<int64_t>(my_q) * g_st + h * g_sh]);
+  if (gate != nullptr && q_live) gv = E::to_f32(gate[static_cast<int64_t>(my_q) * g_st + h * g_sh]);
 #pragma unroll
   for (int db = 0; db < kDB; ++db)
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int d = 32 * db + (v >> 2) * 8 + g * 4 + (v & 3);
-      float y = round_bf16(o[db][v] * inv_l);
+      float y = E::round(o[db][v] * inv_l);
       if (gate != nullptr) y = y * gv;
-      sO[(qr % kBN) * kD + d] = f32_to_bf16_bits(y);
+      sO[(qr % kBN) * kD + d] = E::bits(y);
     }
   if (lse != nullptr && q_live && g == 0)
     lse[static_cast<int64_t>(my_q) * l_st + h * l_sh] = (m + log2f(l)) * kLn2;
@@ -483,9 +529,9 @@ namespace {
 int launch_window(const char* name, const void* q, int64_t q_st, int64_t q_sh, const void* k,
                   int64_t k_st, int64_t k_sh, const void* v, int64_t v_st, int64_t v_sh,
                   const int* blocks, int nblocks, const int* grp_kv, const int* grp_n, int heads,
-                  int head_dim, float scale, const void* gate, int64_t g_st, int64_t g_sh,
-                  void* out, int64_t o_st, int64_t o_sh, float* lse, int64_t l_st, int64_t l_sh,
-                  const MxDst* mx, QNorm qn, void* stream) {
+                  int head_dim, int dtype, float scale, const void* gate, int64_t g_st,
+                  int64_t g_sh, void* out, int64_t o_st, int64_t o_sh, float* lse, int64_t l_st,
+                  int64_t l_sh, const MxDst* mx, QNorm qn, void* stream) {
   if (q == nullptr || k == nullptr || v == nullptr || blocks == nullptr || grp_kv == nullptr ||
       grp_n == nullptr || (mx == nullptr && out == nullptr))
     return set_error(kInvalidArgument, "%s: null pointer", name);
@@ -494,6 +540,10 @@ int launch_window(const char* name, const void* q, int64_t q_st, int64_t q_sh, c
     return set_error(kInvalidArgument, "%s: head_dim must be 64, 128 or 256", name);
   if (mx != nullptr && head_dim != 128)
     return set_error(kUnsupported, "%s: the MXFP8 output takes head_dim 128", name);
+  if (dtype != 0 && dtype != 1)
+    return set_error(kInvalidArgument, "%s: dtype must be 0 (bf16) or 1 (fp16)", name);
+  if (mx != nullptr && dtype != 0)
+    return set_error(kUnsupported, "%s: the MXFP8 output takes bf16 attention", name);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || q_st % 8 || q_sh % 8 || k_st % 8 ||
       k_sh % 8 || v_st % 8 || v_sh % 8 ||
       (mx == nullptr && (!aligned16(out) || o_st % 8 || o_sh % 8)))
@@ -531,18 +581,23 @@ int launch_window(const char* name, const void* q, int64_t q_st, int64_t q_sh, c
     hipLaunchKernelGGL((window_attn_kernel<128, kBlockWaves, true>), grid, block, 0, st, in,
                        blocks, grp_kv, grp_n, nblocks, heads, scale * kLog2e, g16, g_st, g_sh,
                        nullptr, 0, 0, nullptr, 0, 0, *mx, qn);
+#define VDN_WINDOW(D, F16)                                                                      \
+  hipLaunchKernelGGL((window_attn_kernel<D, kBlockWaves, false, F16>), grid, block, 0, st, in,  \
+                     blocks, grp_kv, grp_n, nblocks, heads, scale * kLog2e, g16, g_st, g_sh,    \
+                     o16, o_st, o_sh, lse, l_st, l_sh, none, QNorm{nullptr, 0.f})
+  else if (head_dim == 128 && dtype == 0)
+    VDN_WINDOW(128, false);
+  else if (head_dim == 64 && dtype == 0)
+    VDN_WINDOW(64, false);
+  else if (dtype == 0)
+    VDN_WINDOW(256, false);
   else if (head_dim == 128)
-    hipLaunchKernelGGL((window_attn_kernel<128, kBlockWaves, false>), grid, block, 0, st, in,
-                       blocks, grp_kv, grp_n, nblocks, heads, scale * kLog2e, g16, g_st, g_sh,
-                       o16, o_st, o_sh, lse, l_st, l_sh, none, QNorm{nullptr, 0.f});
+    VDN_WINDOW(128, true);
   else if (head_dim == 64)
-    hipLaunchKernelGGL((window_attn_kernel<64, kBlockWaves, false>), grid, block, 0, st, in,
-                       blocks, grp_kv, grp_n, nblocks, heads, scale * kLog2e, g16, g_st, g_sh,
-                       o16, o_st, o_sh, lse, l_st, l_sh, none, QNorm{nullptr, 0.f});
+    VDN_WINDOW(64, true);
   else
-    hipLaunchKernelGGL((window_attn_kernel<256, kBlockWaves, false>), grid, block, 0, st, in,
-                       blocks, grp_kv, grp_n, nblocks, heads, scale * kLog2e, g16, g_st, g_sh,
-                       o16, o_st, o_sh, lse, l_st, l_sh, none, QNorm{nullptr, 0.f});
+    VDN_WINDOW(256, true);
+#undef VDN_WINDOW
   return check_launch(name);
 }
 
@@ -551,22 +606,24 @@ int launch_window(const char* name, const void* q, int64_t q_st, int64_t q_sh, c
 
 // Reference: paper_window_attention (src/models/softmax_attention/paper_window.py:182-243),
 // window_softmax_reference (window.py:56-111), apply_softmax_gate (kernels.py:51-67).
-// q, k, v: bf16 [rows, heads, head_dim] (head_dim 64, 128 or 256; token / head strides,
-// unit channel stride);
+// q, k, v: bf16 (dtype 0) or fp16 (dtype 1) [rows, heads, head_dim] (head_dim 64, 128 or
+// 256; token / head strides, unit channel stride);
 // blocks: int32 [nblocks, 3] = (first query, end of its query group, group index), each
 // block at most 256 queries; grp_kv: int32 [groups, 8, 2] key intervals [a, b); grp_n:
-// int32 [groups] interval counts. gate (nullable): bf16 per (token, head) scalar multiplied
-// into the bf16 output. out: bf16 rows of head_dim channels; lse (nullable): fp32
-// natural-log sum of exp of the scaled scores.
+// int32 [groups] interval counts. gate (nullable): per (token, head) scalar of the
+// activation dtype, multiplied into the output after its rounding. out: rows of head_dim
+// channels of the activation dtype; lse (nullable): fp32 natural-log sum of exp of the scaled
+// scores.
 VDN_API int vdn_window_attention(const void* q, int64_t q_st, int64_t q_sh, const void* k,
                                  int64_t k_st, int64_t k_sh, const void* v, int64_t v_st,
                                  int64_t v_sh, const int* blocks, int nblocks, const int* grp_kv,
-                                 const int* grp_n, int heads, int head_dim, float scale,
-                                 const void* gate, int64_t g_st, int64_t g_sh, void* out,
-                                 int64_t o_st, int64_t o_sh, float* lse, int64_t l_st,
+                                 const int* grp_n, int heads, int head_dim, int dtype,
+                                 float scale, const void* gate, int64_t g_st, int64_t g_sh,
+                                 void* out, int64_t o_st, int64_t o_sh, float* lse, int64_t l_st,
                                  int64_t l_sh, void* stream) {
   return launch_window("vdn_window_attention", q, q_st, q_sh, k, k_st, k_sh, v, v_st, v_sh,
-                       blocks, nblocks, grp_kv, grp_n, heads, head_dim, scale, gate, g_st, g_sh,
+                       blocks, nblocks, grp_kv, grp_n, heads, head_dim, dtype, scale, gate,
+                       g_st, g_sh,
                        out, o_st, o_sh, lse, l_st, l_sh, nullptr, QNorm{nullptr, 0.f},
                        stream);
 }
@@ -586,7 +643,8 @@ VDN_API int vdn_window_attention_mxfp8(const void* q, int64_t q_st, int64_t q_sh
                                        void* stream) {
   const MxDst mx{static_cast<uint8_t*>(codes), static_cast<uint8_t*>(scales), kp, chunk0};
   return launch_window("vdn_window_attention_mxfp8", q, q_st, q_sh, k, k_st, k_sh, v, v_st,
-                       v_sh, blocks, nblocks, grp_kv, grp_n, heads, 128, scale, gate, g_st, g_sh,
+                       v_sh, blocks, nblocks, grp_kv, grp_n, heads, 128, 0, scale, gate, g_st,
+                       g_sh,
                        nullptr, 0, 0, nullptr, 0, 0, &mx,
                        QNorm{static_cast<const uint16_t*>(q_norm_w), q_norm_eps}, stream);
 }

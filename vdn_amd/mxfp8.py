@@ -327,13 +327,26 @@ def _check_scales(s, rows, kp, device, what):
         raise ValueError(f"{what} scales must hold RP * KP / 32 bytes")
 
 
+def _nonfinite_flag(nonfinite, check_finite, device):
+    """The device word a launch ORs 1 into on a nonfinite value: the caller's `nonfinite`
+    (int32 [1], never read here, so no host sync), else a fresh zero when check_finite."""
+    if nonfinite is not None:
+        if (nonfinite.dtype != torch.int32 or nonfinite.numel() != 1 or
+                nonfinite.device != device or not nonfinite.is_contiguous()):
+            raise ValueError("nonfinite must be a contiguous int32 [1] tensor on the operands' device")
+        return nonfinite
+    return torch.zeros(1, dtype=torch.int32, device=device) if check_finite else None
+
+
 def mxfp8_gemm(data, scales, weight_data, weight_scale, n, *, rows=None, bias=None, out=None,
-               accumulate=False, addend=None, residual=None, gate=None, check_finite=False):
+               accumulate=False, addend=None, residual=None, gate=None, check_finite=False,
+               nonfinite=None):
     """y[rows, n] = dequant(data) @ dequant(weight_data).T in bf16, then (each step rounded
     to bf16) + bias, addend + y, residual + gate * y.
 
     accumulate=True adds into `out` (addend = out), as `out += linear(x)`; `residual` /
-    `gate` ([n]) fuse the block's gated residual `hidden + gate * branch`.
+    `gate` ([n]) fuse the block's gated residual `hidden + gate * branch`. `nonfinite`
+    (int32 [1] on the device) becomes nonzero when an output is inf/NaN, with no host sync.
     """
     if data.device.type != "cuda":
         raise RuntimeError("native MXFP8 requires a HIP device; no fallback")
@@ -380,7 +393,7 @@ def mxfp8_gemm(data, scales, weight_data, weight_scale, n, *, rows=None, bias=No
     res_ptr, ld_res = _matrix_arg(residual, rows, n, "residual", dev)
     _check_alias(out, addend, rows, n, "addend")
     _check_alias(out, residual, rows, n, "residual")
-    flag = torch.zeros(1, dtype=torch.int32, device=data.device) if check_finite else None
+    flag = _nonfinite_flag(nonfinite, check_finite, dev)
     if rows:
         _lib.call("vdn_mxfp8_gemm", data.data_ptr(), scales.data_ptr(), mp,
                   weight_data.data_ptr(), weight_scale.data_ptr(), np_, kp, _lib.ptr(bias),
@@ -410,7 +423,8 @@ def interleave_swiglu(weight: torch.Tensor, bias: torch.Tensor | None = None):
     return arrange(weight), None if bias is None else arrange(bias)
 
 
-def _gemm_swiglu_quantize(data, scales, weight_data, weight_scale, n, rows, bias, check_finite):
+def _gemm_swiglu_quantize(data, scales, weight_data, weight_scale, n, rows, bias, check_finite,
+                          nonfinite):
     mp, kp = data.shape
     np_ = weight_data.shape[0]
     kp_out = -(-n // 128) * 128
@@ -421,9 +435,11 @@ def _gemm_swiglu_quantize(data, scales, weight_data, weight_scale, n, rows, bias
         # small problems: the GEMM's bf16 [a0 g0 a1 g1 ...] output, regrouped as [a | g], then
         # the stand-alone SwiGLU producer (the fused hand-over is in the persistent kernel)
         y = mxfp8_gemm(data, scales, weight_data, weight_scale, np_, rows=rows, bias=bias,
-                       check_finite=check_finite)
+                       check_finite=check_finite, nonfinite=nonfinite)
         y = y.view(rows, kp_out // 128, 2, 128).transpose(1, 2).reshape(rows, 2, kp_out)
-        q, s, _ = launch_swiglu_quantize(y[:, :, :n].reshape(rows, 2 * n))
+        q, s, fin = launch_swiglu_quantize(y[:, :, :n].reshape(rows, 2 * n))
+        if nonfinite is not None:
+            nonfinite.bitwise_or_((~fin.all()).to(torch.int32))
         if q.shape[0] != mp:
             q2 = torch.zeros((mp, kp_out), dtype=torch.uint8, device=data.device)
             s2 = torch.zeros(mp * kp_out // 32, dtype=torch.uint8, device=data.device)
@@ -433,7 +449,7 @@ def _gemm_swiglu_quantize(data, scales, weight_data, weight_scale, n, rows, bias
         return q, s
     q = torch.empty((mp, kp_out), dtype=torch.uint8, device=data.device)
     s = torch.empty(mp * kp_out // 32, dtype=torch.uint8, device=data.device)
-    flag = torch.zeros(1, dtype=torch.int32, device=data.device) if check_finite else None
+    flag = _nonfinite_flag(nonfinite, check_finite, data.device)
     if rows:
         _lib.call("vdn_mxfp8_gemm_act_quantize", data.data_ptr(), scales.data_ptr(), mp,
                   weight_data.data_ptr(), weight_scale.data_ptr(), np_, kp, _lib.ptr(bias), 2,
@@ -447,12 +463,13 @@ def _gemm_swiglu_quantize(data, scales, weight_data, weight_scale, n, rows, bias
 
 
 def mxfp8_gemm_act_quantize(data, scales, weight_data, weight_scale, n, *, rows=None, bias=None,
-                            act="gelu_tanh", check_finite=False):
+                            act="gelu_tanh", check_finite=False, nonfinite=None):
     """MXFP8 codes/scales of act(bf16(dequant(data) @ dequant(weight)ᵀ + bias)) for the next
     projection, produced in the GEMM epilogue. Bit-identical to mxfp8_gemm followed by
     launch_gelu_quantize (act "gelu_tanh"), launch_quantize (act None) or, for act "swiglu"
     over a weight from interleave_swiglu (n = the SwiGLU width), launch_swiglu_quantize of
-    the [a | g] output.
+    the [a | g] output. `nonfinite` (int32 [1] on the device) becomes nonzero on an inf/NaN
+    activation, with no host sync.
     Returns (codes u8 [RP, pad128(n)], flat swizzled scales u8)."""
     mp, kp = data.shape
     np_, kpw = weight_data.shape
@@ -462,12 +479,12 @@ def mxfp8_gemm_act_quantize(data, scales, weight_data, weight_scale, n, *, rows=
         raise ValueError("act must be 'gelu_tanh', 'swiglu' or None")
     if act == "swiglu":
         return _gemm_swiglu_quantize(data, scales, weight_data, weight_scale, n, rows, bias,
-                                     check_finite)
+                                     check_finite, nonfinite)
     rows = mp if rows is None else rows
     kp_out = -(-n // 128) * 128
     q = torch.empty((mp, kp_out), dtype=torch.uint8, device=data.device)
     s = torch.empty(mp * kp_out // 32, dtype=torch.uint8, device=data.device)
-    flag = torch.zeros(1, dtype=torch.int32, device=data.device) if check_finite else None
+    flag = _nonfinite_flag(nonfinite, check_finite, data.device)
     if rows:
         _lib.call("vdn_mxfp8_gemm_act_quantize", data.data_ptr(), scales.data_ptr(), mp,
                   weight_data.data_ptr(), weight_scale.data_ptr(), np_, kp, _lib.ptr(bias),
@@ -512,8 +529,10 @@ class MXFP8Linear(nn.Module):
 
     @torch.no_grad()
     def forward_quantized(self, data, scales, *, rows=None, out_dtype=torch.bfloat16, out=None,
-                          accumulate=False, addend=None, residual=None, gate=None):
-        """Consume padded uint8 codes and swizzled scales, return cropped bf16 [rows, N]."""
+                          accumulate=False, addend=None, residual=None, gate=None,
+                          nonfinite=None):
+        """Consume padded uint8 codes and swizzled scales, return cropped bf16 [rows, N].
+        `nonfinite` (int32 [1] on the device): set nonzero on an inf/NaN output, no host sync."""
         if self.training or out_dtype != torch.bfloat16:
             raise ValueError("MXFP8 supports eval BF16 output only")
         if data.device.type != "cuda":
@@ -541,7 +560,8 @@ class MXFP8Linear(nn.Module):
             bias = self.bias.to(device=data.device, dtype=torch.bfloat16).contiguous()
         return mxfp8_gemm(data, scales, self.weight_data, self.weight_scale, self.out_features,
                           rows=rows, bias=bias, out=out, accumulate=accumulate, addend=addend,
-                          residual=residual, gate=gate, check_finite=self.check_finite)
+                          residual=residual, gate=gate, check_finite=self.check_finite,
+                          nonfinite=nonfinite)
 
     @classmethod
     def swiglu_up(cls, linear: nn.Linear, *, chunk_rows=128, check_finite=True):
@@ -564,7 +584,7 @@ class MXFP8Linear(nn.Module):
         return module
 
     @torch.no_grad()
-    def forward_act_quantized(self, data, scales, *, rows=None, act="gelu_tanh"):
+    def forward_act_quantized(self, data, scales, *, rows=None, act="gelu_tanh", nonfinite=None):
         """Consume MXFP8 input and return the MXFP8 codes/scales of act(bf16 output): the
         producer of the next projection fused into this GEMM's epilogue. act "swiglu" needs a
         module built by swiglu_up."""
@@ -585,7 +605,7 @@ class MXFP8Linear(nn.Module):
                 raise ValueError("act 'swiglu' needs the interleaved weight of swiglu_up")
         return mxfp8_gemm_act_quantize(data, scales, self.weight_data, self.weight_scale,
                                        n, rows=rows, bias=bias, act=act,
-                                       check_finite=self.check_finite)
+                                       check_finite=self.check_finite, nonfinite=nonfinite)
 
     @torch.no_grad()
     def forward(self, x):

@@ -308,9 +308,11 @@ def paper_window_attention(query, key, value, plan: PaperWindowPlan, scale=None,
                            out_mxfp8=None):
     """[used+padding, H, D] -> fresh output of the same shape; padding rows are zero
     (paper_window.py:182-243). LSE (fp32 [rows, H], natural log) is -inf on padding.
-    `gate` ([rows, H] or [rows, H, 1]) fuses apply_softmax_gate: out = bf16(bf16(o) * gate).
-    `out` (optional bf16 [rows, H, D] view with unit channel stride) receives the result
-    instead of a fresh tensor, e.g. a column slice of a wider buffer.
+    BF16 and FP16 activations (the output takes the activation dtype). `gate` ([rows, H] or
+    [rows, H, 1]) fuses apply_softmax_gate: out = act(act(o) * gate), with the gate cast to
+    the activation dtype as apply_softmax_gate does. `out` (optional [rows, H, D] view of the
+    activation dtype with unit channel stride) receives the result instead of a fresh tensor,
+    e.g. a column slice of a wider buffer.
     `out_mxfp8` = (codes, scales, chunk0) instead quantizes the output in the kernel: head h of
     used row r becomes chunk chunk0 + h of row r of an MXFP8 activation (empty_activation),
     byte-identical to quantize_activation of the bf16 output; returns None then."""
@@ -330,8 +332,6 @@ def paper_window_attention(query, key, value, plan: PaperWindowPlan, scale=None,
         raise ValueError("native varlen requires BF16/FP16 and unit innermost stride")
     if not query.is_cuda or query.device != plan.device:
         raise ValueError("Q/K/V and prepared plan must be on the same CUDA device")
-    if query.dtype != torch.bfloat16:
-        raise NotImplementedError("the gfx950 window kernel takes bf16 activations")
     scale = query.shape[-1] ** -0.5 if scale is None else float(scale)
     if not math.isfinite(scale):
         raise ValueError("scale must be finite")
@@ -341,10 +341,12 @@ def paper_window_attention(query, key, value, plan: PaperWindowPlan, scale=None,
             raise ValueError("out_mxfp8 excludes out and return_lse")
         if d != 128:
             raise ValueError("out_mxfp8 holds one head per 128-column chunk: head_dim 128")
+        if query.dtype != torch.bfloat16:
+            raise ValueError("out_mxfp8 quantizes bf16 attention (the block's activations)")
         codes, scales, chunk0 = mxfp8_destination(out_mxfp8, plan.layout.seq_len, h,
                                                   query.device)
         if gate is not None:
-            gate = _gate_rows(gate, plan.layout.seq_len, h)
+            gate = _gate_rows(gate, plan.layout.seq_len, h, query.dtype)
         dp = plan.device_plan
         _lib.call("vdn_window_attention_mxfp8", query.data_ptr(), query.stride(0),
                   query.stride(1), key.data_ptr(), key.stride(0), key.stride(1),
@@ -366,12 +368,13 @@ def paper_window_attention(query, key, value, plan: PaperWindowPlan, scale=None,
         if lse is not None:
             lse[used:].fill_(-float("inf"))
     if gate is not None:
-        gate = _gate_rows(gate, used, h)
+        gate = _gate_rows(gate, used, h, query.dtype)
     dp = plan.device_plan
     _lib.call("vdn_window_attention", query.data_ptr(), query.stride(0), query.stride(1),
               key.data_ptr(), key.stride(0), key.stride(1), value.data_ptr(), value.stride(0),
               value.stride(1), dp.blocks.data_ptr(), dp.nblocks, dp.intervals.data_ptr(),
-              dp.counts.data_ptr(), h, d, scale, _lib.ptr(gate),
+              dp.counts.data_ptr(), h, d, int(query.dtype == torch.float16), scale,
+              _lib.ptr(gate),
               0 if gate is None else gate.stride(0), 0 if gate is None else gate.stride(1),
               out.data_ptr(), out.stride(0), out.stride(1), _lib.ptr(lse),
               0 if lse is None else lse.stride(0), 0 if lse is None else lse.stride(1),
@@ -379,11 +382,13 @@ def paper_window_attention(query, key, value, plan: PaperWindowPlan, scale=None,
     return (out, lse) if return_lse else out
 
 
-def _gate_rows(gate, used, h):
+def _gate_rows(gate, used, h, dtype):
     if gate.shape[0] < used or gate.numel() != gate.shape[0] * h:
         raise ValueError("gate must be [rows, H] or [rows, H, 1] covering the used rows")
+    if gate.device.type != "cuda":
+        raise ValueError("gate must be on the activations' device")
     gate = gate.reshape(gate.shape[0], h)
-    return gate if gate.dtype == torch.bfloat16 else gate.to(torch.bfloat16)
+    return gate if gate.dtype == dtype else gate.to(dtype)
 
 
 def apply_softmax_gate(softmax_out, gate, inference=False):
@@ -448,31 +453,37 @@ def _validate_rope(q, k, q_weight, k_weight, eps, cos, sin, enabled, nvtx):
 
 def paper_qk_rmsnorm_rope(q, k, q_weight, k_weight, eps=1e-6, cos=None, sin=None, *,
                           enabled=False, nvtx=True):
-    """New contiguous normalized/rotated Q and K (paper_qk_rope.py:145-211).
+    """New contiguous normalized/rotated Q and K (paper_qk_rope.py:145-211) for BF16, FP16 and
+    FP32 activations.
 
-    enabled=False is refused here: the disabled path of the reference is its eager CPU/CUDA
-    implementation, which this build does not ship (the oracle holds it). enabled=True runs
-    the gfx950 kernel for bf16 activations.
+    enabled=True runs the gfx950 kernel (a HIP device is required; there is no fallback).
+    enabled=False is the reference's disabled path: its eager torch ops on the tensors'
+    own device (CPU or GPU), with the same rounding points (_eager_norm / _eager_rope,
+    paper_qk_rope.py:82-95). Callers select it explicitly; the device path never takes it.
     """
     _validate_rope(q, k, q_weight, k_weight, eps, cos, sin, enabled, nvtx)
     if not enabled:
-        raise RuntimeError("paper_qk_rmsnorm_rope: only the enabled (device) path is built")
+        qo, ko = _eager_rms(q, q_weight, eps), _eager_rms(k, k_weight, eps)
+        if cos is not None:
+            qo, ko = _eager_rotate(qo, cos, sin), _eager_rotate(ko, cos, sin)
+        return qo, ko
     if not q.is_cuda:
         raise ValueError("enabled=True requires a HIP device")
-    if q.dtype != torch.bfloat16:
-        raise NotImplementedError("the gfx950 QK norm/RoPE kernel takes bf16 activations")
     qo = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     ko = torch.empty(k.shape, dtype=k.dtype, device=k.device)
     if q.shape[0] == 0:
         return qo, ko
     tables = cos is not None
     if tables:
-        if cos.dtype == torch.float16:
-            cos, sin = cos.float(), sin.float()
+        # the kernel reads tables of the activation dtype or fp32 (any other dtype is widened
+        # to fp32 exactly; the kernel then rounds to the activation dtype, as cos.to(dtype))
+        if cos.dtype not in (q.dtype, torch.float32):
+            cos = cos.float()
         if sin.dtype != cos.dtype:
             sin = sin.to(cos.dtype)
+    act = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}[q.dtype]
     flags = (int(q_weight.dtype == torch.float32) | (int(k_weight.dtype == torch.float32) << 1)
-             | (int(tables and cos.dtype == torch.float32) << 2))
+             | (int(tables and cos.dtype == torch.float32) << 2) | (act << 4))
     t, h, d = q.shape
     _lib.call("vdn_qk_rmsnorm_rope", q.data_ptr(), *q.stride(), k.data_ptr(), *k.stride(),
               q_weight.data_ptr(), q_weight.stride(0), k_weight.data_ptr(), k_weight.stride(0),
@@ -482,6 +493,25 @@ def paper_qk_rmsnorm_rope(q, k, q_weight, k_weight, eps=1e-6, cos=None, sin=None
               cos.shape[1] if tables else 0, flags, t, h, d, qo.data_ptr(), ko.data_ptr(),
               _lib.stream(q.device))
     return qo, ko
+
+
+def _eager_rms(x, weight, eps):
+    """RMSNorm over the last dim in fp32, the weight multiplied in fp32, one rounding to x's
+    dtype (nn.RMSNorm's order, paper_qk_rope.py:82-87)."""
+    xf = x.float()
+    inv = torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps)
+    return ((xf * inv) * weight.float()).to(x.dtype).contiguous()
+
+
+def _eager_rotate(x, cos, sin):
+    """Rotate-half RoPE of the first R channels in x's dtype: each product and the sum round
+    to that dtype (torch's elementwise ops on x's dtype, paper_qk_rope.py:90-95)."""
+    r = cos.shape[-1]
+    lo, hi = x[..., :r // 2], x[..., r // 2:r]
+    c = cos.to(x.dtype)[:, None, :]
+    s = sin.to(x.dtype)[:, None, :]
+    turned = torch.cat((-hi, lo), dim=-1)
+    return torch.cat((x[..., :r] * c + turned * s, x[..., r:]), dim=-1).contiguous()
 
 
 def qk_rmsnorm(x, weight, eps=1e-6):
