@@ -341,6 +341,14 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
 // double-buffered LDS line so each step needs a single barrier (a thread writes the line
 // of step k + 1 only after the barrier of step k, by which time every thread has read the
 // line of step k - 1 that it overwrites).
+// J = B M^-1 then runs on v_mfma_f32_16x16x4_f32 (lane l: A = B[i = l % 16][k slot l / 16],
+// B = M^-1[k slot l / 16][j = l % 16], accumulator rows 4 (l / 16) + v, column l % 16), M^-1
+// staged in LDS. Wave w computes J rows [32 w, 32 w + 32) as two 16-row tiles mt by eight
+// 16-column tiles nt, where MFMA column c of tile nt is J column 8 c + nt: a lane's eight
+// B operands of one k are the 8 consecutive floats M^-1[k][8 c .. 8 c + 8) (two 16-byte LDS
+// reads) and its results for one row are 8 consecutive J columns (two 16-byte stores). K runs
+// in the order k = 16 q + 4 g + s (chunk q < 8, lane group g, element s < 4), so lane (i, g)
+// takes its A operands of chunk q from one 16-byte load B[i][16 q + 4 g .. + 4).
 __global__ void __launch_bounds__(256, 2)
 vda_factors_kernel(const float* __restrict__ A, const float* __restrict__ B,
                    const float* __restrict__ alpha, float* __restrict__ T,
@@ -351,6 +359,16 @@ vda_factors_kernel(const float* __restrict__ A, const float* __restrict__ B,
   const int64_t mat = static_cast<int64_t>(blockIdx.x) * kD * kD;
   const int tid = threadIdx.x, ti = tid >> 4, tj = tid & 15;
   const int i0 = ti * 8, j0 = tj * 8;
+  // the lane's A operands of J = B M^-1 (rows 32 w + 16 mt + li, chunks q), loaded now so
+  // that their latency passes under the elimination
+  const int wave = tid >> 6, li = tid & 15, lg = (tid >> 4) & 3;
+  f32x4 bq[2][8];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      bq[mt][q] = *reinterpret_cast<const f32x4*>(B + mat + (32 * wave + 16 * mt + li) * kD +
+                                                  16 * q + 4 * lg);
   float m[8][8];
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
@@ -430,43 +448,34 @@ vda_factors_kernel(const float* __restrict__ A, const float* __restrict__ B,
     *reinterpret_cast<f32x4*>(&minv[(i0 + r) * kLd + j0 + 4]) = hi;
   }
   __syncthreads();
-  float acc[8][8];
+  f32x4 acc[2][8];
 #pragma unroll
-  for (int r = 0; r < 8; ++r)
+  for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-    for (int c = 0; c < 8; ++c) acc[r][c] = 0.f;
-  const float* Bn = B + mat + i0 * kD;
-#pragma unroll 1
-  for (int k = 0; k < kD; k += 4) {
-    f32x4 brow[8];
+    for (int nt = 0; nt < 8; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 8; ++r) brow[r] = *reinterpret_cast<const f32x4*>(Bn + r * kD + k);
+  for (int q = 0; q < 8; ++q) {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const f32x4 x0 = *reinterpret_cast<const f32x4*>(&minv[(k + kk) * kLd + j0]);
-      const f32x4 x1 = *reinterpret_cast<const f32x4*>(&minv[(k + kk) * kLd + j0 + 4]);
+    for (int s = 0; s < 4; ++s) {
+      const float* xr = &minv[(16 * q + 4 * lg + s) * kLd + 8 * li];
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(xr);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(xr + 4);
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const float bv = brow[r][kk];
+      for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          acc[r][c] = fmaf(bv, x0[c], acc[r][c]);
-          acc[r][c + 4] = fmaf(bv, x1[c], acc[r][c + 4]);
-        }
-      }
+        for (int mt = 0; mt < 2; ++mt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(bq[mt][q][s], nt < 4 ? x0[nt] : x1[nt - 4],
+                                                             acc[mt][nt], 0, 0, 0);
     }
   }
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    f32x4 lo, hi;
+  for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      lo[c] = acc[r][c];
-      hi[c] = acc[r][c + 4];
+    for (int v = 0; v < 4; ++v) {
+      float* dst = J + mat + (32 * wave + 16 * mt + 4 * lg + v) * kD + 8 * li;
+      *reinterpret_cast<f32x4*>(dst) = f32x4{acc[mt][0][v], acc[mt][1][v], acc[mt][2][v], acc[mt][3][v]};
+      *reinterpret_cast<f32x4*>(dst + 4) = f32x4{acc[mt][4][v], acc[mt][5][v], acc[mt][6][v], acc[mt][7][v]};
     }
-    *reinterpret_cast<f32x4*>(J + mat + (i0 + r) * kD + j0) = lo;
-    *reinterpret_cast<f32x4*>(J + mat + (i0 + r) * kD + j0 + 4) = hi;
-  }
 }
 
 // --------------------------------------------------------- affine recurrence ----
