@@ -692,19 +692,43 @@ vda_conv_prepare_kernel(const uint16_t* __restrict__ tokens, int64_t row_stride,
     for (int j = 0; j < 9; ++j) cv_buffer_to_lds16(r, voff[j], base + (wave * 9 + j) * 1024);
   };
 
-  // ---- bf16 weights of channels c0 = 128 h + 2 lane, c0 + 1, as channel pairs per tap ----
+  // ---- bf16 weights of channels c0 = 128 h + 2 lane (ch 0) and c0 + 1 (ch 1). Taps go in
+  // pairs through v_dot2c_f32_bf16 (two bf16 products added to an fp32 sum): per channel and
+  // tap row i, the words (w[i][0], w[i][1]) and (w[i][2], w[i][3]) and tap 4 as a float; the
+  // temporal taps as (w[0], w[1]), (w[2], w[3]) and w[4]. ----
   const int c0 = h * kD + 2 * lane;
   const uint16_t* wsp16 = static_cast<const uint16_t*>(w_sp);
   const uint16_t* wtm16 = static_cast<const uint16_t*>(w_tm);
-  uint32_t wsp[25], wtm[5];
+  auto word = [](const uint16_t* p) {
+    return static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 16);
+  };
+  uint32_t wsp2[2][5][2], wtm2[2][2];
+  float wsp4[2][5], wtm4[2];
 #pragma unroll
-  for (int i = 0; i < 25; ++i)
-    wsp[i] = static_cast<uint32_t>(wsp16[c0 * 25 + i]) | (static_cast<uint32_t>(wsp16[(c0 + 1) * 25 + i]) << 16);
+  for (int c = 0; c < 2; ++c) {
+    const uint16_t* ws = wsp16 + (c0 + c) * 25;
 #pragma unroll
-  for (int i = 0; i < 5; ++i)
-    wtm[i] = static_cast<uint32_t>(wtm16[c0 * 5 + i]) | (static_cast<uint32_t>(wtm16[(c0 + 1) * 5 + i]) << 16);
-  auto lo = [](uint32_t w) { return __uint_as_float(w << 16); };
-  auto hi = [](uint32_t w) { return __uint_as_float(w & 0xffff0000u); };
+    for (int i = 0; i < 5; ++i) {
+      wsp2[c][i][0] = word(ws + 5 * i);
+      wsp2[c][i][1] = word(ws + 5 * i + 2);
+      wsp4[c][i] = bf16_bits_to_f32(ws[5 * i + 4]);
+    }
+    const uint16_t* wt = wtm16 + (c0 + c) * 5;
+    wtm2[c][0] = word(wt);
+    wtm2[c][1] = word(wt + 2);
+    wtm4[c] = bf16_bits_to_f32(wt[4]);
+  }
+  // (x.ch c of word a, x.ch c of word b) as one bf16 pair: v_perm_b32 byte selects
+  auto pair = [](uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_perm(b, a, c ? 0x07060302u : 0x05040100u);
+  };
+  auto dot2 = [](uint32_t x, uint32_t w, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x),
+                                           __builtin_bit_cast(bf16x2, w), acc, false);
+  };
+  auto chan = [](uint32_t w, int c) {
+    return __uint_as_float(c ? w & 0xffff0000u : w << 16);
+  };
 
   const int by = wave >> 1, bx = wave & 1;
   // spatial outputs (bf16 channel pairs) of frames t - 4 .. t, oldest first
@@ -734,28 +758,35 @@ vda_conv_prepare_kernel(const uint16_t* __restrict__ tokens, int64_t row_stride,
 #pragma unroll
       for (int ir = 0; ir < 8; ++ir) {
         // one input row in flight at a time: the scheduler would otherwise hoist all 64 LDS
-        // reads (and their 128 unpacked values) ahead of the arithmetic
+        // reads (and their pairs) ahead of the arithmetic
         __builtin_amdgcn_sched_barrier(0);
-        float xr[8][2];
+        uint32_t xw[8];
 #pragma unroll
-        for (int ic = 0; ic < 8; ++ic) {
-          const uint32_t w2 = *reinterpret_cast<const uint32_t*>(src + (ir * kCvHalo + ic) * 256);
-          xr[ic][0] = __uint_as_float(w2 << 16);
-          xr[ic][1] = __uint_as_float(w2 & 0xffff0000u);
+        for (int ic = 0; ic < 8; ++ic)
+          xw[ic] = *reinterpret_cast<const uint32_t*>(src + (ir * kCvHalo + ic) * 256);
+        // per channel: horizontally adjacent positions (ic, ic + 1) as one bf16 pair, and
+        // positions 4..7 (tap 4 of the four outputs) as floats
+        uint32_t xp[2][7];
+        float x4[2][4];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+#pragma unroll
+          for (int ic = 0; ic < 7; ++ic) xp[c][ic] = pair(xw[ic], xw[ic + 1], c);
+#pragma unroll
+          for (int ox = 0; ox < 4; ++ox) x4[c][ox] = chan(xw[ox + 4], c);
         }
 #pragma unroll
         for (int oy = 0; oy < 4; ++oy) {
           const int i = ir - oy;
           if (i < 0 || i > 4) continue;
 #pragma unroll
-          for (int j = 0; j < 5; ++j) {
-            const float w0 = lo(wsp[i * 5 + j]), w1 = hi(wsp[i * 5 + j]);
+          for (int c = 0; c < 2; ++c)
 #pragma unroll
             for (int ox = 0; ox < 4; ++ox) {
-              acc[oy][ox][0] = __builtin_fmaf(xr[ox + j][0], w0, acc[oy][ox][0]);
-              acc[oy][ox][1] = __builtin_fmaf(xr[ox + j][1], w1, acc[oy][ox][1]);
+              float a = dot2(xp[c][ox], wsp2[c][i][0], acc[oy][ox][c]);
+              a = dot2(xp[c][ox + 2], wsp2[c][i][1], a);
+              acc[oy][ox][c] = __builtin_fmaf(x4[c][ox], wsp4[c][i], a);
             }
-          }
         }
       }
 #pragma unroll
@@ -770,31 +801,41 @@ vda_conv_prepare_kernel(const uint16_t* __restrict__ tokens, int64_t row_stride,
     // ---- frame o = t - 2: temporal taps, SiLU, L2, store ----
     const int o = t - 2;
     uint16_t* out_f = out + (static_cast<int64_t>(o) * heads + h) * spatial * kD;
+    float y[16][2];
 #pragma unroll
-    for (int p = 0; p < 16; ++p) {
-      float y[2];
+    for (int p = 0; p < 16; ++p)
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        float a = 0.f;
+        // frames o .. o + 4 in pairs (o, o + 1), (o + 2, o + 3), then o + 4
+        float a = dot2(pair(win[0][p], win[1][p], c), wtm2[c][0], 0.f);
+        a = dot2(pair(win[2][p], win[3][p], c), wtm2[c][1], a);
+        a = __builtin_fmaf(chan(win[4][p], c), wtm4[c], a);
+        y[p][c] = silu(a);
+      }
+    if (l2norm) {
+      // the 16 positions' sums over the head's 128 channels, reduced side by side so that
+      // their cross-lane steps fill each other's wait states
+      float ss[16];
 #pragma unroll
-        for (int k = 0; k < 5; ++k) {
-          const float xv = __uint_as_float(c ? win[k][p] & 0xffff0000u : win[k][p] << 16);
-          a = __builtin_fmaf(xv, c ? hi(wtm[k]) : lo(wtm[k]), a);
-        }
-        y[c] = silu(a);
+      for (int p = 0; p < 16; ++p) ss[p] = y[p][0] * y[p][0] + y[p][1] * y[p][1];
+#pragma unroll
+      for (int p = 0; p < 16; ++p) ss[p] = wave_sum(ss[p]);
+#pragma unroll
+      for (int p = 0; p < 16; ++p) {
+        const float inv = __builtin_amdgcn_rsqf(fmaxf(ss[p], 1e-12f));
+        y[p][0] *= inv;
+        y[p][1] *= inv;
       }
-      if (l2norm) {
-        const float inv = __builtin_amdgcn_rsqf(fmaxf(wave_sum(y[0] * y[0] + y[1] * y[1]), 1e-12f));
-        y[0] *= inv;
-        y[1] *= inv;
-      }
+    }
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
       const int yy = ty * kCvTile + by * 4 + (p >> 2), xx = tx * kCvTile + bx * 4 + (p & 3);
       if (yy < fh && xx < fw) {
         // a 32-bit offset from the frame's base (a frame spans < 2 GiB), made opaque so the
         // 16 offsets are not kept as 64-bit values across the frame loop
         uint32_t off = static_cast<uint32_t>((yy * fw + xx) * kD + 2 * lane);
         asm volatile("" : "+v"(off));
-        *reinterpret_cast<uint32_t*>(out_f + off) = pack_bf16x2(y[0], y[1]);
+        *reinterpret_cast<uint32_t*>(out_f + off) = pack_bf16x2(y[p][0], y[p][1]);
       }
     }
   }
