@@ -142,7 +142,7 @@ def breakdown_of(per, steps):
     return out
 
 
-def short_conv_prepare(cfg, hidden, frames, steps):
+def short_conv_prepare(cfg, device, frames, steps):
     """The linear branch's short-conv feature prep (vdn_vda_conv_prepare) on K and V of the
     clip shape, outside the block (the block's configuration has no short conv): random
     N(0,1) K/V columns of a fused [T, 3H] projection, a random-init LinearAttentionSepConv.
@@ -155,10 +155,10 @@ def short_conv_prepare(cfg, hidden, frames, steps):
     from vdn_amd import vda as vv
     tokens = frames * HEIGHT * WIDTH
     hd, heads = cfg.hidden, cfg.heads
-    g = torch.Generator(device=hidden.device).manual_seed(7)
-    qkv = torch.randn(tokens, 3 * hd, generator=g, device=hidden.device).to(torch.bfloat16)
+    g = torch.Generator(device=device).manual_seed(7)
+    qkv = torch.randn(tokens, 3 * hd, generator=g, device=device).to(torch.bfloat16)
     torch.manual_seed(7)
-    conv = vv.LinearAttentionSepConv(hd, ("k", "v")).to(torch.bfloat16).to(hidden.device)
+    conv = vv.LinearAttentionSepConv(hd, ("k", "v")).to(torch.bfloat16).to(device)
 
     def run():
         for i, proj in ((1, "k"), (2, "v")):
@@ -815,8 +815,9 @@ def main():
                         "at head_dim 64, C2 quantize + GEMMs, C3 VDA branch, C4 RoPE + window "
                         "attention); 0 skips them")
     p.add_argument("--configs-only", action="store_true",
-                   help="run only the stand-alone config measurements (C1, C2, C3, C4) and print "
-                        "them as one JSON line (for profiling their kernels apart from the block)")
+                   help="run only the stand-alone config measurements (C1, C2, C3, C4 and the "
+                        "short-conv prepare) and print them as one JSON line (for profiling their "
+                        "kernels apart from the block)")
     p.add_argument("--breakdown-steps", type=int, default=3,
                    help="instrumented steps after the timed ones (an event pair around every "
                         "launch) for the per-kernel breakdown, the roofline and idle_ms")
@@ -852,7 +853,9 @@ def main():
         steps = max(args.config_steps, 1)
         print(json.dumps({"configs": {"C1": c1_vda(steps), "C2": c2_quantize_gemm(steps),
                                       "C3": c3_vda(steps, frames),
-                                      "C4": c4_window(steps, frames)}}), flush=True)
+                                      "C4": c4_window(steps, frames)},
+                          "short_conv_prepare": short_conv_prepare(cfg, torch.device("cuda"),
+                                                                   frames, steps)}), flush=True)
         if args.calibrate_copy:
             calibrate_copy()
         return
@@ -929,7 +932,7 @@ def main():
     hb_bytes = sum(iso[n][3] for n in VDA_HBM_BOUND if n in iso)
     hb_gbs = hb_bytes / (hb_t * 1e-3) / 1e9
     w = [sum(iso[nm][i] for nm in ATTENTION if nm in iso) for i in range(4)]
-    conv = short_conv_prepare(cfg, hidden, frames, args.isolated_steps)
+    conv = short_conv_prepare(cfg, hidden.device, frames, args.isolated_steps)
     production = production_geometry(args.isolated_steps)
     h3 = h3_block(args.isolated_steps,
                   lambda p, c, f, s, t, l: {p.device_plan.intervals.data_ptr():
