@@ -444,6 +444,7 @@ def c1_vda(steps):
     import torch
     import torch.nn.functional as F
     from oracle import vda as ov
+    from vdn_amd import _lib
     from vdn_amd import vda as vv
     frames, spatial, heads, d = 4, 256, 8, 64
     g = torch.Generator().manual_seed(0)
@@ -473,6 +474,14 @@ def c1_vda(steps):
             run()
         end.record()
         torch.cuda.synchronize()
+        # the layer's own kernels, apart from the zero-padding of its d = 64 operands to the
+        # 128-wide kernels (torch copies) and the launch gaps
+        with _lib.LaunchTimer(set(VDA_ENTRIES) | {"vdn_vda_prepare"}) as timer:
+            for _ in range(reps):
+                run()
+            torch.cuda.synchronize()
+        kernel_ms = sum(t for _, _, t in timer.durations()) / reps
+        launches = len(timer.durations()) // reps
     gpu_ms = start.elapsed_time(end) / reps
     threads = host_threads()
     torch.set_num_threads(threads)
@@ -480,10 +489,11 @@ def c1_vda(steps):
     ref = ov.eager_branch_fp32(q, k, v, beta, gate, alpha, bounds, frames, spatial, w)
     cpu_ms = (time.perf_counter() - t0) * 1e3
     rel = float((out.float().cpu() - ref).norm() / ref.norm())
-    log(f"C1: VDA layer {gpu_ms:.3f} ms on the GPU, {cpu_ms:.1f} ms eager fp32 on {threads} "
-        f"host threads, rel-L2 {rel:.1e}")
+    log(f"C1: VDA layer {gpu_ms:.3f} ms on the GPU ({kernel_ms:.3f} ms in {launches} kernels), "
+        f"{cpu_ms:.1f} ms eager fp32 on {threads} host threads, rel-L2 {rel:.1e}")
     return {"workload": f"VDA layer, {frames} frames x {spatial} tokens, {heads}x{d} heads",
             "ms": round(gpu_ms, 4), "tokens_per_s": round(frames * spatial / gpu_ms * 1e3),
+            "kernel_ms": round(kernel_ms, 4), "kernel_launches": launches,
             "rel_l2_vs_cpu_eager_fp32": float(f"{rel:.3g}"),
             "cpu_baseline": {"ms": round(cpu_ms, 2), "cores": threads, "kind": "port",
                              "sample": "the whole layer, eager fp32 body on the host"}}
