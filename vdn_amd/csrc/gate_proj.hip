@@ -79,30 +79,50 @@ gate_projection_kernel(const uint16_t* __restrict__ x, int64_t x_st, int k,
   const int wm = wave & 1, wn = wave >> 1;
   const int g = lane >> 5, col = lane & 31;
 
-  // ---- DMA: the x1 tile is 512 16-byte chunks (1 per lane), the W tile 1536 (3 per lane);
-  // chunk q of a tile is LDS chunk q, i.e. row q / 4, stored chunk q % 4. Rows past the
-  // block's last row repeat it (their results are dropped). ----
-  const char* a_src;
-  const char* w_src[3];
-  {
-    const int q = 64 * wave + lane, r = q >> 2, c = q & 3;
-    a_src = reinterpret_cast<const char*>(x + (grow0 + min(r, nrows - 1)) * x_st) +
-            16 * (c ^ gswz(r));
-  }
+  // ---- DMA: the x1 tile is 512 16-byte chunks, the W tile 1536; chunk q of a tile is LDS
+  // chunk q, i.e. row q / 4, stored chunk q % 4. Waves 0-3 load x1 (2 chunks per lane), waves
+  // 4-7 load W (6 per lane): vmcnt retires in order, so with each stream in waves of its own a
+  // wait for W from L2 never waits for x1 loads from HBM issued after it (and x1 keeps its
+  // full prefetch distance). Rows past the block's last row repeat it (their results are
+  // dropped). ----
+  const bool a_loader = wave < 4;   // wave-uniform
+  const int lw = a_loader ? wave : wave - 4;
+  const char* src[6];
+  if (a_loader) {
 #pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    const int q = 64 * (3 * wave + i) + lane, r = q >> 2, c = q & 3;
-    w_src[i] = reinterpret_cast<const char*>(w + static_cast<int64_t>(r) * k) + 16 * (c ^ gswz(r));
+    for (int i = 0; i < 2; ++i) {
+      const int q = 64 * (2 * lw + i) + lane, r = q >> 2, c = q & 3;
+      src[i] = reinterpret_cast<const char*>(x + (grow0 + min(r, nrows - 1)) * x_st) +
+               16 * (c ^ gswz(r));
+    }
+#pragma unroll
+    for (int i = 2; i < 6; ++i) src[i] = src[1];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      const int q = 64 * (6 * lw + i) + lane, r = q >> 2, c = q & 3;
+      src[i] = reinterpret_cast<const char*>(w + static_cast<int64_t>(r) * k) + 16 * (c ^ gswz(r));
+    }
   }
+  // DMA i (0-1 for x1 waves, 0-5 for W waves) of stage s into ring slot `slot`
+  auto issue_one = [&](int i, int s, int slot) __attribute__((always_inline)) {
+    const int64_t off = static_cast<int64_t>(s) * kGK * 2;
+    if (a_loader)
+      g_load_lds16(src[i] + off, sA + slot * (kGRows * kGK) + 64 * (2 * lw + i) * 8);
+    else
+      g_load_lds16(src[i] + off, sW + slot * (kGCols * kGK) + 64 * (6 * lw + i) * 8);
+  };
   auto issue_a = [&](int s, int slot) __attribute__((always_inline)) {
-    g_load_lds16(a_src + static_cast<int64_t>(s) * kGK * 2,
-                 sA + slot * (kGRows * kGK) + 64 * wave * 8);
+    if (a_loader) {
+      issue_one(0, s, slot);
+      issue_one(1, s, slot);
+    }
   };
   auto issue_w = [&](int s, int slot) __attribute__((always_inline)) {
-    const int64_t off = static_cast<int64_t>(s) * kGK * 2;
-    uint16_t* d = sW + slot * (kGCols * kGK);
+    if (!a_loader) {
 #pragma unroll
-    for (int i = 0; i < 3; ++i) g_load_lds16(w_src[i] + off, d + 64 * (3 * wave + i) * 8);
+      for (int i = 0; i < 6; ++i) issue_one(i, s, slot);
+    }
   };
 
   f32x16 acc[2][3];
@@ -140,12 +160,11 @@ gate_projection_kernel(const uint16_t* __restrict__ x, int64_t x_st, int k,
       for (int nb = 0; nb < 3; ++nb) fr.w[j][nb] = *reinterpret_cast<const bf16x8*>(tW + w_off[nb][j]);
     }
   };
-  // The 12 MFMAs of one stage, with the stage's 4 DMAs (x1 stage sa into slot sla, W stage sw
-  // into slot slw) issued after MFMAs 0, 3, 6 and 9: a DMA issue can stall while the CU's
-  // address unit is busy, and in the shadow of queued MFMAs the stall costs less than a burst.
+  // The 12 MFMAs of one stage, with the wave's DMAs of one batch (x1 stage sa into slot sla
+  // after MFMAs 0 and 6, or W stage sw into slot slw after MFMAs 0, 2, .., 10): a DMA issue
+  // can stall while the CU's address unit is busy, and in the shadow of queued MFMAs the
+  // stall costs less than a burst.
   auto mfmas = [&](const Frags& fr, int sa, int sla, int sw, int slw) __attribute__((always_inline)) {
-    const int64_t woff = static_cast<int64_t>(sw) * kGK * 2;
-    uint16_t* dw = sW + slw * (kGCols * kGK);
     int n = 0;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -154,13 +173,14 @@ gate_projection_kernel(const uint16_t* __restrict__ x, int64_t x_st, int k,
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
           acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr.a[j][mb], fr.w[j][nb], acc[mb][nb], 0, 0, 0);
-          if (n % 3 == 0) {
+          if (n % 2 == 0) {
             asm volatile("" ::"v"(acc[mb][nb]) : "memory");
             __builtin_amdgcn_sched_barrier(0);
-            if (n == 0)
-              issue_a(sa, sla);
-            else
-              g_load_lds16(w_src[n / 3 - 1] + woff, dw + 64 * (3 * wave + n / 3 - 1) * 8);
+            if (a_loader) {
+              if (n % 6 == 0) issue_one(n / 6, sa, sla);
+            } else {
+              issue_one(n / 2, sw, slw);
+            }
             __builtin_amdgcn_sched_barrier(0);
           }
           ++n;
@@ -168,24 +188,27 @@ gate_projection_kernel(const uint16_t* __restrict__ x, int64_t x_st, int k,
   };
 
   // ---- K loop. Stage s lives in x1 slot s % 6 and W slot s % 4. The prologue issues x1
-  // stages 0-4, then W stages 0-2; iteration s (after its barrier) reads the fragments of
-  // stage s + 1 into registers, then runs the MFMAs of stage s from the registers read one
-  // iteration earlier and, among them, issues one batch, x1 stage s + 5 and W stage s + 3,
-  // into the slots of stage s - 1 (whose fragments every wave read in iteration s - 2 and
-  // consumed in iteration s - 1), so the LDS reads of one stage overlap the MFMAs of the
-  // previous. Past the last
-  // stage a batch loads the last stage again (into those free slots), so every batch is 4
-  // DMAs per wave and the waits are exact: stage s + 1 must have landed before the barrier
-  // of iteration s; its W came with batch s - 2 (the prologue for s < 2), its x1 earlier, so
-  // only the batch of iteration s - 1 may still be in flight (4 DMAs); at s = 0 W stage 2
-  // (3 DMAs); before the prologue's barrier stage 0 is needed (W stages 1-2 in flight). ----
+  // stages 0-4 (x1 waves) and W stages 0-2 (W waves); iteration s (after its barrier) reads
+  // the fragments of stage s + 1 into registers, then runs the MFMAs of stage s from the
+  // registers read one iteration earlier and, among them, issues x1 stage s + 5 (x1 waves) or
+  // W stage s + 3 (W waves) into the slots of stage s - 1 (whose fragments every wave read
+  // in iteration s - 2 and consumed in iteration s - 1), so the LDS reads of one stage
+  // overlap the MFMAs of the previous. Past the last stage a batch loads the last stage again
+  // (into those free slots), so every batch is 2 (x1) or 6 (W) DMAs per wave and the waits
+  // are exact: stage s + 1 must have landed before the barrier of iteration s, which leaves
+  // x1 stages s + 2 .. s + 4 (6 DMAs) or W stage s + 2 (6 DMAs) in flight. ----
   static_assert(kARing >= kWRing, "x1 runs at least as far ahead as W");
   const int stages = k / kGK;
 #pragma unroll
   for (int a = 0; a < kARing - 1; ++a) issue_a(min(a, stages - 1), a);
 #pragma unroll
   for (int b = 0; b < kWRing - 1; ++b) issue_w(min(b, stages - 1), b);
-  asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
+  // stage 0 must have landed: x1 stages 1-4 (8 DMAs) or W stages 1-2 (12) may be in flight
+  if (a_loader)
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+  __syncthreads();
   Frags fr[2];
   read_frags(fr[0], sA, sW);
   int aslot = 0, wslot = 0;  // slots of stage s
@@ -195,13 +218,15 @@ gate_projection_kernel(const uint16_t* __restrict__ x, int64_t x_st, int k,
     for (int h = 0; h < 2; ++h) {
       const int si = s + h;
       if (si >= stages) break;
-      if (si == 0)
-        asm volatile("s_waitcnt vmcnt(3)\n\ts_barrier" ::: "memory");
-      else
-        asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+      // stage si + 1 must have landed: x1 waves may have stages si + 2 .. si + 4 in flight (3
+      // batches of 2), W waves stage si + 2 (one batch of 6)
+      asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
       const int an = aslot == kARing - 1 ? 0 : aslot + 1;
       const int wn2 = wslot == kWRing - 1 ? 0 : wslot + 1;
-      if (si + 1 < stages) read_frags(fr[1 - h], sA + an * (kGRows * kGK), sW + wn2 * (kGCols * kGK));
+      // unconditional (past the last stage the values are unused): with a path that skipped
+      // the reads, the merged LDS wait before the first MFMA would be lgkmcnt(0), i.e. for the
+      // reads just issued, instead of only those of the fragments the MFMAs use
+      read_frags(fr[1 - h], sA + an * (kGRows * kGK), sW + wn2 * (kGCols * kGK));
       mfmas(fr[h], min(si + kARing - 1, stages - 1), aslot == 0 ? kARing - 1 : aslot - 1,
             min(si + kWRing - 1, stages - 1), wslot == 0 ? kWRing - 1 : wslot - 1);
       aslot = an;
