@@ -320,18 +320,30 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     if (!wave_live) return;
 
     // ---- Sᵀ = K Qᵀ for the tile's kBN keys (kKT 32-key accumulators) ----
+    // channel step major: the kKT K fragments of step ks + 1 are read while the kKT MFMAs of
+    // step ks run (each accumulator's chain is in the same order as key block major)
     f32x16 s[kKT];
 #pragma unroll
-    for (int kt = 0; kt < kKT; ++kt) {
+    for (int kt = 0; kt < kKT; ++kt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) s[kt][v] = 0.f;
-      const int row = kt * 32 + col;
+    x8 kf[2][kKT];
+    auto kload = [&](int ks, x8 (&dst)[kKT]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int ks = 0; ks < kD / 16; ++ks) {
+      for (int kt = 0; kt < kKT; ++kt) {
+        const int row = kt * 32 + col;
         const int chunk = (2 * ks + g) ^ swz_k<kD>(row);
-        const x8 ka = *reinterpret_cast<const x8*>(tk + row * kD + chunk * 8);
-        s[kt] = E::mfma(ka, qf[ks], s[kt]);
+        dst[kt] = *reinterpret_cast<const x8*>(tk + row * kD + chunk * 8);
       }
+    };
+    kload(0, kf[0]);
+#pragma unroll
+    for (int ks = 0; ks < kD / 16; ++ks) {
+      if (ks + 1 < kD / 16) kload(ks + 1, kf[(ks + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of this step's MFMAs
+#pragma unroll
+      for (int kt = 0; kt < kKT; ++kt) s[kt] = E::mfma(kf[ks & 1][kt], qf[ks], s[kt]);
+      __builtin_amdgcn_sched_barrier(0);
     }
     // ---- online softmax (exp2 domain; scores scaled inside the exponent's fma) ----
     if (b - a < kBN) {  // tail tile: keys past the interval end do not exist
@@ -372,30 +384,43 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     rs += __shfl_xor(rs, 32);
     l += rs;
 
-    // ---- Oᵀ += Vᵀ Pᵀ, 16 keys per MFMA ----
-#pragma unroll
-    for (int c = 0; c < kBN / 16; ++c) {
-      x8 pb;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) pb[j] = static_cast<typename E::type>(s[c >> 1][(c & 1) * 8 + j]);
-#pragma unroll
-      for (int db = 0; db < kDB; ++db) {
-        typename E::x4 lo, hi;
-        {
-          const int row = 16 * c + tr_row;
-          const int e = 32 * db + tr_col;
-          const int chunk = (e >> 3) ^ swz_v<kD>(row);
-          lo = E::read_tr(tv + row * kD + chunk * 8 + (e & 7));
-        }
-        {
-          const int row = 16 * c + 8 + tr_row;
-          const int e = 32 * db + tr_col;
-          const int chunk = (e >> 3) ^ swz_v<kD>(row);
-          hi = E::read_tr(tv + row * kD + chunk * 8 + (e & 7));
-        }
-        const x8 va{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        o[db] = E::mfma(va, pb, o[db]);
+    // ---- Oᵀ += Vᵀ Pᵀ, 16 keys per MFMA; the V fragments of MFMA i + kVA are read before
+    // MFMA i (the barriers order only the LDS reads and MFMAs; VALU and transcendental
+    // instructions may cross them) ----
+    constexpr int kItems = (kBN / 16) * kDB;
+    constexpr int kVA = 2;
+    x8 vf[kVA + 1];
+    auto vload = [&](int i, x8& dst) __attribute__((always_inline)) {
+      const int c = i / kDB, db = i % kDB;
+      typename E::x4 lo, hi;
+      {
+        const int row = 16 * c + tr_row;
+        const int e = 32 * db + tr_col;
+        const int chunk = (e >> 3) ^ swz_v<kD>(row);
+        lo = E::read_tr(tv + row * kD + chunk * 8 + (e & 7));
       }
+      {
+        const int row = 16 * c + 8 + tr_row;
+        const int e = 32 * db + tr_col;
+        const int chunk = (e >> 3) ^ swz_v<kD>(row);
+        hi = E::read_tr(tv + row * kD + chunk * 8 + (e & 7));
+      }
+      dst = x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+#pragma unroll
+    for (int i = 0; i < kVA; ++i) vload(i, vf[i]);
+    x8 pb;
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+      if (i + kVA < kItems) vload(i + kVA, vf[(i + kVA) % (kVA + 1)]);
+      __builtin_amdgcn_sched_barrier(0x406);
+      const int c = i / kDB, db = i % kDB;
+      if (db == 0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pb[j] = static_cast<typename E::type>(s[c >> 1][(c & 1) * 8 + j]);
+      }
+      o[db] = E::mfma(vf[i % (kVA + 1)], pb, o[db]);
+      __builtin_amdgcn_sched_barrier(0x406);
     }
   };
   // ---- key intervals of the group, one after another ----
