@@ -461,11 +461,14 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     // ---- MXFP8 epilogue straight from the accumulators ----
     // Lane (col, g) holds channels 32 db + 8 j + 4 g + i (v = 4 j + i) of query my_q: 16 of
     // the 32 channels of MXFP8 block db; lane ^ 32 holds the other 16. y = bf16(bf16(o / l)
-    // * gate) as in the bf16 form; the block's amax takes one exchange, and each group of 4
-    // channels leaves as one 4-byte store of codes.
+    // * gate) as in the bf16 form; the block's amax takes one exchange, and the codes leave
+    // as one 16-byte store per lane and block (below).
     float gv = 1.f;
     if (gate != nullptr && q_live) gv = bf16_bits_to_f32(gate[static_cast<int64_t>(my_q) * g_st + h * g_sh]);
-    uint8_t* crow = mx.codes + static_cast<int64_t>(my_q) * mx.kp + (mx.chunk0 + h) * 128 + 4 * g;
+    // Lanes l and l + 32 hold the same query row. After two swaps per block each holds 16
+    // contiguous code bytes of it (bytes 16 g .. + 16 of the block): one 16-byte store instead
+    // of four 4-byte ones scattered over 32 rows.
+    uint8_t* crow = mx.codes + static_cast<int64_t>(my_q) * mx.kp + (mx.chunk0 + h) * 128 + 16 * g;
     uint32_t word = 0;
 #pragma unroll
     for (int db = 0; db < kDB; ++db) {
@@ -485,16 +488,32 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
       float amax = 0.f;
 #pragma unroll
       for (int v = 0; v < 16; ++v) amax = fmaxf(amax, fabsf(y[v]));
-      amax = fmaxf(amax, __shfl_xor(amax, 32));
+      {
+        // v_permlane32_swap (vdst, vsrc): lane l < 32 receives lane l + 32's vdst in vsrc and
+        // lane l + 32 receives lane l's vsrc in vdst; with one value in both operands the
+        // pair holds the lane's own value and its partner's
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(amax),
+                                                         __float_as_uint(amax), false, false);
+        amax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      }
       float sinv;
       word |= e8m0_from_amax(amax, &sinv) << (8 * db);
+      // word j of the lane: code bytes 8 j + 4 g .. + 4 of the block
+      uint32_t wv[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         int c = 0;
         c = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * j] * sinv, y[4 * j + 1] * sinv, c, false);
         c = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * j + 2] * sinv, y[4 * j + 3] * sinv, c, true);
-        if (q_live) *reinterpret_cast<uint32_t*>(crow + 32 * db + 8 * j) = static_cast<uint32_t>(c);
+        wv[j] = static_cast<uint32_t>(c);
       }
+      // lane g = 0 takes words 0 and 1 of lane g = 1 (bytes 4-7, 12-15), lane g = 1 takes
+      // words 2 and 3 of lane g = 0 (bytes 16-19, 24-27)
+      const auto s02 = __builtin_amdgcn_permlane32_swap(wv[0], wv[2], false, false);
+      const auto s13 = __builtin_amdgcn_permlane32_swap(wv[1], wv[3], false, false);
+      const u32x4 out16 = g == 0 ? u32x4{wv[0], s02[1], wv[1], s13[1]}
+                                 : u32x4{s02[0], wv[2], s13[0], wv[3]};
+      if (q_live) *reinterpret_cast<u32x4*>(crow + 32 * db) = out16;
     }
     if (q_live && g == 0)
       *reinterpret_cast<uint32_t*>(
