@@ -614,8 +614,9 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
 
   // ---- producer epilogue of one tile (kMode 2), straight from the accumulators ----
   // acc[mt][nt][v] is C[m0 + 128 wm + 16 mt + r][n0 + 128 wn + 16 nt + 4 g + v] with r = lane % 16
-  // and g = lane / 16: each lane holds 4 consecutive columns of one row, so their 4 codes
-  // leave as one 4-byte store, with no LDS staging. A 32-column block is nt = 2b, 2b + 1 of
+  // and g = lane / 16: each lane holds 4 consecutive columns of one row, and a 4 x 4 lane
+  // transpose of the code words gives each of the row's 4 lanes 16 contiguous code bytes (two
+  // 16-byte stores per row group), with no LDS staging. A 32-column block is nt = 2b, 2b + 1 of
   // the four lanes g of a row (two permlane swaps give its amax), and the wave's 128 columns
   // are one MXFP8 chunk, whose 4 scale bytes are one dword of the swizzled layout.
   // SwiGLU (ep.act 2) reads W with its a and g halves interleaved in 128-row blocks: block j
@@ -757,10 +758,11 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
             }
         }
       }
-      // every lane takes part in the block maxima; only the stores are predicated
+      // every lane takes part in the block maxima and the code transposes; only the stores
+      // are predicated (uniform over the 4 lanes of a row)
       const bool store = chunk_in && row < mp;
-      uint8_t* qrow = ep.q_out + row * ep.kp_out + chunk128 * 128 + c_lo * 4;
       uint32_t word = 0;
+      uint32_t cw[TN];   // codes of columns 16 nt + 4 c_lo .. + 4
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         float amax = 0.f;
@@ -776,8 +778,26 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
           int c = 0;
           c = __builtin_amdgcn_cvt_pk_fp8_f32(y[nt][0] * sinv, y[nt][1] * sinv, c, false);
           c = __builtin_amdgcn_cvt_pk_fp8_f32(y[nt][2] * sinv, y[nt][3] * sinv, c, true);
-          if (store) *reinterpret_cast<uint32_t*>(qrow + nt * 16) = static_cast<uint32_t>(c);
+          cw[nt] = static_cast<uint32_t>(c);
         }
+      }
+      // 4 x 4 transpose of code words over the row's 4 lanes (c_lo = lane / 16): afterwards
+      // lane c_lo holds word c' of column group 4 q + c_lo from lane c', i.e. the 16
+      // contiguous code bytes of columns 16 (4 q + c_lo) ..; c_lo bit 1 first (lanes 32
+      // apart, v_permlane32_swap), then bit 0 (16 apart, v_permlane16_swap). Each swap
+      // gives lane l < 32 (row 2 j) lane l + 32's (row 2 j + 1's) vdst in vsrc and that lane
+      // l's vsrc in vdst, so the returned pair is the new words k, k + 2 (k, k + 1).
+#pragma unroll
+      for (int qg = 0; qg < 2; ++qg) {
+        uint32_t* w4 = cw + 4 * qg;
+        const auto a02 = __builtin_amdgcn_permlane32_swap(w4[0], w4[2], false, false);
+        const auto a13 = __builtin_amdgcn_permlane32_swap(w4[1], w4[3], false, false);
+        const auto b01 = __builtin_amdgcn_permlane16_swap(a02[0], a13[0], false, false);
+        const auto b23 = __builtin_amdgcn_permlane16_swap(a02[1], a13[1], false, false);
+        const u32x4 out16 = {b01[0], b01[1], b23[0], b23[1]};
+        if (store)
+          *reinterpret_cast<u32x4*>(ep.q_out + row * ep.kp_out + chunk128 * 128 +
+                                    16 * (4 * qg + c_lo)) = out16;
       }
       if (store && c_lo == 0)
         *reinterpret_cast<uint32_t*>(
