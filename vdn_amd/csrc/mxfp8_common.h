@@ -30,17 +30,54 @@ __device__ __forceinline__ int64_t swizzled_scale_offset(int64_t r, int64_t c, i
   return tile * 512 + (r & 31) * 16 + ((r & 127) >> 5) * 4 + (c & 3);
 }
 
-// Eight fp32 values (already multiplied by 2^-e) -> eight E4M3FN codes, RNE.
-__device__ __forceinline__ u32x2 e4m3x8(const float* v) {
-  int lo = 0, hi = 0;
-  lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], lo, false);
-  lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], lo, true);
-  hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4], v[5], hi, false);
-  hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6], v[7], hi, true);
+typedef short s16x2_t __attribute__((ext_vector_type(2)));
+
+// 2^e as fp32 from an E8M0 byte (byte = e + 127). Byte 0 gives exponent field 0, which the
+// scaled conversion below reads as 2^-127.
+__device__ __forceinline__ float e8m0_scale(uint32_t byte) { return __uint_as_float(byte << 23); }
+
+// E4M3FN codes of value / 2^e (s = e8m0_scale(byte)), four fp32 values to one word, low
+// value in the low byte. On gfx950 v_cvt_scalef32_pk_fp8_f32 gives, for every bf16-valued
+// input and every exponent, nonfinite inputs included, the code v_cvt_pk_fp8_f32 gives for
+// value * 2^-e (RNE; measured over all 2^16 patterns, both halves of the word), without the
+// multiplies.
+__device__ __forceinline__ uint32_t e4m3x4_scaled(float a, float b, float c, float d, float s) {
+  s16x2_t r = {0, 0};
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, a, b, s, false);
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, c, d, s, true);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// Eight packed bf16 values (the low half of a word first) -> their eight codes of
+// value / 2^e. (The packed-bf16 form of the instruction, v_cvt_scalef32_pk_fp8_bf16, gives
+// the same codes, but this compiler fed it the same source pair for every word of a u32x4;
+// the values go through the fp32 form instead.)
+__device__ __forceinline__ u32x2 e4m3x8_bf16(const u32x4& w, float s) {
   u32x2 out;
-  out[0] = static_cast<uint32_t>(lo);
-  out[1] = static_cast<uint32_t>(hi);
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    out[h] = e4m3x4_scaled(__uint_as_float(w[2 * h] << 16), __uint_as_float(w[2 * h] & 0xffff0000u),
+                           __uint_as_float(w[2 * h + 1] << 16),
+                           __uint_as_float(w[2 * h + 1] & 0xffff0000u), s);
   return out;
+}
+
+// max |x| over eight packed bf16 values as fp32, with NaN ignored as a running fmaxf from 0
+// ignores it. Non-negative values order as their magnitude bits, so the maximum is an integer
+// one on the packed halves; a NaN (magnitude above 0x7f80) sends the lane to the fmaxf form.
+__device__ __forceinline__ float amax8_bf16(const u32x4& w) {
+  u16x2 m = {0, 0};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[i] & 0x7fff7fffu));
+  const uint32_t mb = m[0] > m[1] ? m[0] : m[1];
+  if (mb <= 0x7f80u) return __uint_as_float(mb << 16);
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    amax = fmaxf(amax, fabsf(__uint_as_float(w[i] << 16)));
+    amax = fmaxf(amax, fabsf(__uint_as_float(w[i] & 0xffff0000u)));
+  }
+  return amax;
 }
 
 
@@ -108,11 +145,25 @@ __device__ __forceinline__ void quantize_store8_at(const float* v, uint8_t* __re
   amax = block_amax4(amax);
   float inv;
   const uint32_t scale = e8m0_from_amax(amax, &inv);
-  float scaled[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) scaled[i] = v[i] * inv;
-  const u32x2 codes = e4m3x8(scaled);
+  const float sf = e8m0_scale(scale);
+  u32x2 codes;
+  codes[0] = e4m3x4_scaled(v[0], v[1], v[2], v[3], sf);
+  codes[1] = e4m3x4_scaled(v[4], v[5], v[6], v[7], sf);
   // 16 lanes write the chunk's 128 contiguous bytes: a streaming store of whole lines
+  __builtin_nontemporal_store(codes, reinterpret_cast<u32x2*>(qdst));
+  const uint32_t word = scale_word16(scale);
+  if (scale_lane) *reinterpret_cast<uint32_t*>(sdst) = word;
+}
+
+// quantize_store8_at for 8 values held as packed bf16 (the low half of each word first): the
+// amax and the codes come from the packed words directly.
+__device__ __forceinline__ void quantize_store8_bf16_at(const u32x4& w, uint8_t* __restrict__ qdst,
+                                                        uint8_t* __restrict__ sdst,
+                                                        bool scale_lane) {
+  const float amax = block_amax4(amax8_bf16(w));
+  float inv;
+  const uint32_t scale = e8m0_from_amax(amax, &inv);
+  const u32x2 codes = e4m3x8_bf16(w, e8m0_scale(scale));
   __builtin_nontemporal_store(codes, reinterpret_cast<u32x2*>(qdst));
   const uint32_t word = scale_word16(scale);
   if (scale_lane) *reinterpret_cast<uint32_t*>(sdst) = word;

@@ -772,14 +772,12 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
           for (int v = 0; v < 4; ++v) amax = fmaxf(amax, fabsf(y[nt][v]));
         amax = max_quad_rows(amax);
         float sinv;
-        word |= e8m0_from_amax(amax, &sinv) << (8 * b);
+        const uint32_t byte = e8m0_from_amax(amax, &sinv);
+        word |= byte << (8 * b);
+        const float sf = e8m0_scale(byte);
 #pragma unroll
-        for (int nt = 2 * b; nt < 2 * b + 2; ++nt) {
-          int c = 0;
-          c = __builtin_amdgcn_cvt_pk_fp8_f32(y[nt][0] * sinv, y[nt][1] * sinv, c, false);
-          c = __builtin_amdgcn_cvt_pk_fp8_f32(y[nt][2] * sinv, y[nt][3] * sinv, c, true);
-          cw[nt] = static_cast<uint32_t>(c);
-        }
+        for (int nt = 2 * b; nt < 2 * b + 2; ++nt)
+          cw[nt] = e4m3x4_scaled(y[nt][0], y[nt][1], y[nt][2], y[nt][3], sf);
       }
       // 4 x 4 transpose of code words over the row's 4 lanes (c_lo = lane / 16): afterwards
       // lane c_lo holds word c' of column group 4 q + c_lo from lane c', i.e. the 16

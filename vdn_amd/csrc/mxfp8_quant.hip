@@ -173,24 +173,15 @@ mxfp8_quantize32_kernel(const uint16_t* __restrict__ x, int rows, int k, int str
     if (item >= items) break;  // uniform across the 16-lane group
     const uint32_t r = row_of[j], chunk = chunk_of[j];
     u16x2 mag = {0, 0};
-    float v[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 4; ++i)
       mag = __builtin_elementwise_max(mag, __builtin_bit_cast(u16x2, w[j][i] & 0x7f807f80u));
-      v[2 * i] = __uint_as_float(w[j][i] << 16);
-      v[2 * i + 1] = __uint_as_float(w[j][i] & 0xffff0000u);
-    }
     any_bad |= mag[0] == 0x7f80 || mag[1] == 0x7f80;
-    float amax = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    amax = block_amax4(amax);
+    // amax and codes straight from the packed bf16 words
+    const float amax = block_amax4(amax8_bf16(w[j]));
     float inv;
     const uint32_t scale = e8m0_from_amax(amax, &inv);
-    float scaled[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) scaled[i] = v[i] * inv;
-    const u32x2 codes = e4m3x8(scaled);
+    const u32x2 codes = e4m3x8_bf16(w[j], e8m0_scale(scale));
     __builtin_nontemporal_store(
         codes, reinterpret_cast<u32x2*>(q + (r * static_cast<uint32_t>(kp) + chunk * 128 + lane16 * 8)));
     const uint32_t word = scale_word16(scale);
@@ -373,9 +364,7 @@ prenorm_quantize_full_rows_kernel(const uint16_t* __restrict__ x, int64_t rows, 
       mag = __builtin_elementwise_max(mag, __builtin_bit_cast(u16x2, packed[i] & 0x7fff7fffu));
     }
     if (y != nullptr) __builtin_nontemporal_store(packed, reinterpret_cast<u32x4*>(ylane + 512 * j));
-    float v[8];
-    unpack_bf16x8(packed, v);
-    quantize_store8_at(v, qlane + 512 * j, slane + 2048 * j, scale_lane);
+    quantize_store8_bf16_at(packed, qlane + 512 * j, slane + 2048 * j, scale_lane);
   }
   const bool any_bad = __ballot(mag[0] >= 0x7f80 || mag[1] >= 0x7f80) != 0;
   if (lane == 0) finite[r] = any_bad ? 0 : 1;

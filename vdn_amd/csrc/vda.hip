@@ -1150,15 +1150,14 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
           for (int v = 0; v < 4; ++v) amax = fmaxf(amax, fabsf(ay[m][v]));
         amax = max_quad_rows(amax);
         float sinv;
-        word |= e8m0_from_amax(amax, &sinv) << (8 * b);
+        const uint32_t byte = e8m0_from_amax(amax, &sinv);
+        word |= byte << (8 * b);
+        const float sf = e8m0_scale(byte);
         u32x2 c2;
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
-          int c = 0;
           const f32x4& y4 = ay[2 * b + m];
-          c = __builtin_amdgcn_cvt_pk_fp8_f32(y4[0] * sinv, y4[1] * sinv, c, false);
-          c = __builtin_amdgcn_cvt_pk_fp8_f32(y4[2] * sinv, y4[3] * sinv, c, true);
-          c2[m] = static_cast<uint32_t>(c);
+          c2[m] = e4m3x4_scaled(y4[0], y4[1], y4[2], y4[3], sf);
         }
         if (valid) *reinterpret_cast<u32x2*>(crow + b * 32) = c2;
       }

@@ -497,16 +497,14 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
         amax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
       }
       float sinv;
-      word |= e8m0_from_amax(amax, &sinv) << (8 * db);
+      const uint32_t byte = e8m0_from_amax(amax, &sinv);
+      word |= byte << (8 * db);
+      const float sf = e8m0_scale(byte);
       // word j of the lane: code bytes 8 j + 4 g .. + 4 of the block
       uint32_t wv[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        int c = 0;
-        c = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * j] * sinv, y[4 * j + 1] * sinv, c, false);
-        c = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * j + 2] * sinv, y[4 * j + 3] * sinv, c, true);
-        wv[j] = static_cast<uint32_t>(c);
-      }
+      for (int j = 0; j < 4; ++j)
+        wv[j] = e4m3x4_scaled(y[4 * j], y[4 * j + 1], y[4 * j + 2], y[4 * j + 3], sf);
       // lane g = 0 takes words 0 and 1 of lane g = 1 (bytes 4-7, 12-15), lane g = 1 takes
       // words 2 and 3 of lane g = 0 (bytes 16-19, 24-27)
       const auto s02 = __builtin_amdgcn_permlane32_swap(wv[0], wv[2], false, false);
