@@ -351,14 +351,38 @@ class HybridDiTBlock(nn.Module):
         raw_q = qkv[:, :inner].view(T, heads, d)
         raw_k = qkv[:, inner:2 * inner].view(T, heads, d)
         value = qkv[:, 2 * inner:].view(T, heads, d)
-        soft_gate, beta, gate_down, partial = gate_projection(
-            x1, self.gate_w, k["soft_gate_b"], heads, frames, spatial)
-        # the low-rank gate sigmoid(up(down(x1))) is formed inside the VDA readout
-        lin_gate = vv.OutputGateProjection(gate_down, k["lgate_up_w"], k["lgate_up_b"])
-        alpha = frame_alpha(partial, frames, spatial, k["alpha_up_w"], k["dt_bias"], k["a_log"],
-                            heads, d)
-        del partial
         cos, sin = rope
+        main = torch.cuda.current_stream(dev)
+        side = self._side_stream(dev) if (self.overlap_vda and parts is None) else None
+
+        def gates():
+            soft_gate, beta, gate_down, partial = gate_projection(
+                x1, self.gate_w, k["soft_gate_b"], heads, frames, spatial)
+            # the low-rank gate sigmoid(up(down(x1))) is formed inside the VDA readout
+            lin_gate = vv.OutputGateProjection(gate_down, k["lgate_up_w"], k["lgate_up_b"])
+            alpha = frame_alpha(partial, frames, spatial, k["alpha_up_w"], k["dt_bias"],
+                                k["a_log"], heads, d)
+            return soft_gate, beta, lin_gate, alpha
+
+        def context_kv():
+            """Context K (RMSNorm'd) and V of the cross-attention: they depend on the context
+            rows only, so the overlapped schedule computes them on the side stream."""
+            cx, csx = mx.launch_quantize(context)
+            L = context.shape[0]
+            ck = self.ck.forward_quantized(cx, csx, rows=L, nonfinite=nf).view(L, heads, d)
+            cv = self.cv.forward_quantized(cx, csx, rows=L, nonfinite=nf).view(L, heads, d)
+            return vw.qk_rmsnorm(ck, k["norm_kc"], cfg.eps), cv
+
+        if side is not None:
+            # The gate projection (x1 only) runs on the side stream beside the QK norm + RoPE
+            # pass; the window attention waits for its softmax gate through an event.
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                soft_gate, beta, lin_gate, alpha = gates()
+                gate_ready = torch.cuda.Event()
+                gate_ready.record(side)
+        else:
+            soft_gate, beta, lin_gate, alpha = gates()
         # The two branch outputs are the two halves of the [O | O_lin] operand. The kernels
         # quantize them in their epilogues straight into the MXFP8 operand (chunks 0..H-1 for
         # the softmax branch, H.. for VDA); with return_parts they are kept in bf16 for the
@@ -374,23 +398,26 @@ class HybridDiTBlock(nn.Module):
 
             # The VDA branch runs on a side stream while RoPE and the window attention run on
             # the caller's stream (the reference's paper_vda_overlap, tensor_parallel.py:
-            # 202-216): its latency-bound passes fill the attention's gaps. The tensors it
-            # shares with the caller's stream (qkv, the gates, alpha, the [O | O_lin] operand)
-            # are all released after main.wait_stream(side), so a later allocation on the
-            # caller's stream is ordered after the branch without record_stream (which would
-            # keep ~5 GB per block out of the allocator's cache while the host runs ahead).
-            main = torch.cuda.current_stream(dev)
-            if self.overlap_vda:
-                side = self._side_stream(dev)
-                side.wait_stream(main)
+            # 202-216): its latency-bound passes fill the attention's gaps. The context K and V
+            # of the cross-attention follow it there. The tensors the side stream shares with
+            # the caller's stream (x1, qkv, the gates, alpha, the [O | O_lin] operand, the
+            # context K and V) are all released after main.wait_stream(side), so a later
+            # allocation on the caller's stream is ordered after the branch without
+            # record_stream (which would keep ~5 GB per block out of the allocator's cache
+            # while the host runs ahead); a side-stream allocation is ordered after them by
+            # the next side.wait_stream(main).
+            if side is not None:
                 with torch.cuda.stream(side):
                     linear_branch()
+                    ck, cv = context_kv()
             q, kk = vw.paper_qk_rmsnorm_rope(raw_q, raw_k, k["norm_q"], k["norm_k"], cfg.eps,
                                              cos, sin, enabled=True)
+            if side is not None:
+                main.wait_event(gate_ready)
             vw.paper_window_attention(q, kk, value, window_plan, d ** -0.5, enabled=True,
                                       gate=soft_gate, out_mxfp8=(qb, sb, 0))
             del q, kk
-            if self.overlap_vda:
+            if side is not None:
                 main.wait_stream(side)
             else:
                 linear_branch()
@@ -408,7 +435,7 @@ class HybridDiTBlock(nn.Module):
             snap("far", both[:, inner:])
             qb, sb = mx.launch_quantize(both)
             del both
-        del qkv, raw_q, raw_k, value, lin_gate, gate_down
+        del qkv, raw_q, raw_k, value, lin_gate, soft_gate, beta, alpha
         # the first residual update writes a fresh tensor (no copy of the input)
         h = torch.empty_like(hidden)
         self.o_cat.forward_quantized(qb, sb, rows=T, out=h, residual=hidden, gate=gate_msa,
@@ -422,11 +449,8 @@ class HybridDiTBlock(nn.Module):
                                                     write_bf16=False)
         producer(fin)
         cq = self.cq.forward_quantized(q3, s3, rows=T, nonfinite=nf).view(T, heads, d)
-        cx, csx = mx.launch_quantize(context)
-        L = context.shape[0]
-        ck = self.ck.forward_quantized(cx, csx, rows=L, nonfinite=nf).view(L, heads, d)
-        cv = self.cv.forward_quantized(cx, csx, rows=L, nonfinite=nf).view(L, heads, d)
-        ck = vw.qk_rmsnorm(ck, k["norm_kc"], cfg.eps)
+        if side is None:
+            ck, cv = context_kv()
         if parts is None:
             # the queries' RMSNorm runs in the attention kernel as it loads them
             qo, so = mx.empty_activation(T, inner, dev)
