@@ -48,27 +48,38 @@ __device__ __forceinline__ uint32_t e4m3x4_scaled(float a, float b, float c, flo
   return __builtin_bit_cast(uint32_t, r);
 }
 
-// Eight packed bf16 values (the low half of a word first) -> their eight codes of
-// value / 2^e. (The packed-bf16 form of the instruction, v_cvt_scalef32_pk_fp8_bf16, gives
-// the same codes, but this compiler fed it the same source pair for every word of a u32x4;
-// the values go through the fp32 form instead.)
+// The two codes of value / 2^e (s = e8m0_scale(byte)) of the packed bf16 pair w (low half
+// first) into byte pair kHi of `old` (the other pair kept): v_cvt_scalef32_pk_fp8_bf16, which
+// gives the codes of v_cvt_scalef32_pk_fp8_f32 on the same values (measured over all 2^16
+// patterns at every exponent, both byte pairs). w arrives by value: __builtin_bit_cast of a
+// vector element lvalue (w4[i] of a u32x4) reads element 0 whatever i is, with this compiler.
+template <bool kHi>
+__device__ __forceinline__ uint32_t e4m3x2_bf16(uint32_t old, uint32_t w, float s) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(
+      __builtin_bit_cast(s16x2_t, old), __builtin_bit_cast(bf16x2, w), s, kHi));
+}
+
+// Eight packed bf16 values (the low half of a word first) -> their eight codes of value / 2^e.
 __device__ __forceinline__ u32x2 e4m3x8_bf16(const u32x4& w, float s) {
   u32x2 out;
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-    out[h] = e4m3x4_scaled(__uint_as_float(w[2 * h] << 16), __uint_as_float(w[2 * h] & 0xffff0000u),
-                           __uint_as_float(w[2 * h + 1] << 16),
-                           __uint_as_float(w[2 * h + 1] & 0xffff0000u), s);
+  out[0] = e4m3x2_bf16<true>(e4m3x2_bf16<false>(0u, w[0], s), w[1], s);
+  out[1] = e4m3x2_bf16<true>(e4m3x2_bf16<false>(0u, w[2], s), w[3], s);
   return out;
 }
 
-// max |x| over eight packed bf16 values as fp32, with NaN ignored as a running fmaxf from 0
-// ignores it. Non-negative values order as their magnitude bits, so the maximum is an integer
-// one on the packed halves; a NaN (magnitude above 0x7f80) sends the lane to the fmaxf form.
-__device__ __forceinline__ float amax8_bf16(const u32x4& w) {
+// Per-half maxima of the magnitude bits of eight packed bf16 values. Non-negative values
+// order as their magnitude bits; a bf16 is nonfinite iff its magnitude bits reach 0x7f80.
+__device__ __forceinline__ u16x2 mag8_bf16(const u32x4& w) {
   u16x2 m = {0, 0};
 #pragma unroll
   for (int i = 0; i < 4; ++i) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[i] & 0x7fff7fffu));
+  return m;
+}
+
+// max |x| over eight packed bf16 values as fp32 (m = mag8_bf16(w)), with NaN ignored as a
+// running fmaxf from 0 ignores it: the maximum is an integer one on the magnitude bits, and
+// a NaN (magnitude above 0x7f80) sends the lane to the fmaxf form.
+__device__ __forceinline__ float amax8_bf16(const u32x4& w, u16x2 m) {
   const uint32_t mb = m[0] > m[1] ? m[0] : m[1];
   if (mb <= 0x7f80u) return __uint_as_float(mb << 16);
   float amax = 0.f;
@@ -80,6 +91,19 @@ __device__ __forceinline__ float amax8_bf16(const u32x4& w) {
   return amax;
 }
 
+__device__ __forceinline__ float amax8_bf16(const u32x4& w) { return amax8_bf16(w, mag8_bf16(w)); }
+
+// Sum of squares of eight packed bf16 values added to acc, two per v_dot2_f32_bf16 (a bf16
+// square is exact in fp32).
+__device__ __forceinline__ float sumsq8_bf16(const u32x4& w, float acc) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t word = w[i];  // by value (see e4m3x2_bf16)
+    const bf16x2 p = __builtin_bit_cast(bf16x2, word);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(p, p, acc, false);
+  }
+  return acc;
+}
 
 // torch's GELU(approximate='tanh') in fp32, rounded to bf16 by the caller:
 //   0.5 x (1 + tanh(u)) = x / (1 + exp(-2u)),  u = sqrt(2/pi) (x + 0.044715 x^3).
@@ -155,12 +179,13 @@ __device__ __forceinline__ void quantize_store8_at(const float* v, uint8_t* __re
   if (scale_lane) *reinterpret_cast<uint32_t*>(sdst) = word;
 }
 
-// quantize_store8_at for 8 values held as packed bf16 (the low half of each word first): the
-// amax and the codes come from the packed words directly.
-__device__ __forceinline__ void quantize_store8_bf16_at(const u32x4& w, uint8_t* __restrict__ qdst,
+// quantize_store8_at for 8 values held as packed bf16 (the low half of each word first), mag =
+// mag8_bf16(w): the amax and the codes come from the packed words directly.
+__device__ __forceinline__ void quantize_store8_bf16_at(const u32x4& w, u16x2 mag,
+                                                        uint8_t* __restrict__ qdst,
                                                         uint8_t* __restrict__ sdst,
                                                         bool scale_lane) {
-  const float amax = block_amax4(amax8_bf16(w));
+  const float amax = block_amax4(amax8_bf16(w, mag));
   float inv;
   const uint32_t scale = e8m0_from_amax(amax, &inv);
   const u32x2 codes = e4m3x8_bf16(w, e8m0_scale(scale));

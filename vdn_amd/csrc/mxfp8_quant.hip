@@ -172,13 +172,10 @@ mxfp8_quantize32_kernel(const uint16_t* __restrict__ x, int rows, int k, int str
     const uint32_t item = group + j * ngroups;
     if (item >= items) break;  // uniform across the 16-lane group
     const uint32_t r = row_of[j], chunk = chunk_of[j];
-    u16x2 mag = {0, 0};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      mag = __builtin_elementwise_max(mag, __builtin_bit_cast(u16x2, w[j][i] & 0x7f807f80u));
-    any_bad |= mag[0] == 0x7f80 || mag[1] == 0x7f80;
-    // amax and codes straight from the packed bf16 words
-    const float amax = block_amax4(amax8_bf16(w[j]));
+    // the nonfinite test, the amax and the codes straight from the packed bf16 words
+    const u16x2 m8 = mag8_bf16(w[j]);
+    any_bad |= m8[0] >= 0x7f80 || m8[1] >= 0x7f80;
+    const float amax = block_amax4(amax8_bf16(w[j], m8));
     float inv;
     const uint32_t scale = e8m0_from_amax(amax, &inv);
     const u32x2 codes = e4m3x8_bf16(w[j], e8m0_scale(scale));
@@ -316,14 +313,14 @@ prenorm_quantize_full_rows_kernel(const uint16_t* __restrict__ x, int64_t rows, 
     return;
   }
   const int64_t table_row = shared_row ? idx0 : indices[r];
-  float ss = 0.f;
+  // sum of squares, two products per v_dot2 on the packed words, in two chains
+  float ss0 = 0.f, ss1 = 0.f;
 #pragma unroll
   for (int j = 0; j < kS; ++j) {
-    float f[8];
-    unpack_bf16x8(raw[j], f);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ss += f[i] * f[i];
+    if (j & 1) ss1 = sumsq8_bf16(raw[j], ss1);
+    else ss0 = sumsq8_bf16(raw[j], ss0);
   }
+  float ss = ss0 + ss1;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
   const float ms = ss / static_cast<float>(kCols) + eps;
@@ -361,10 +358,11 @@ prenorm_quantize_full_rows_kernel(const uint16_t* __restrict__ x, int64_t rows, 
       const float t0 = (xv[2 * i] * inv_rms) * w[2 * i];
       const float t1 = (xv[2 * i + 1] * inv_rms) * w[2 * i + 1];
       packed[i] = pack_bf16x2(t0 * u[2 * i] + sh[2 * i], t1 * u[2 * i + 1] + sh[2 * i + 1]);
-      mag = __builtin_elementwise_max(mag, __builtin_bit_cast(u16x2, packed[i] & 0x7fff7fffu));
     }
+    const u16x2 m8 = mag8_bf16(packed);
+    mag = __builtin_elementwise_max(mag, m8);
     if (y != nullptr) __builtin_nontemporal_store(packed, reinterpret_cast<u32x4*>(ylane + 512 * j));
-    quantize_store8_bf16_at(packed, qlane + 512 * j, slane + 2048 * j, scale_lane);
+    quantize_store8_bf16_at(packed, m8, qlane + 512 * j, slane + 2048 * j, scale_lane);
   }
   const bool any_bad = __ballot(mag[0] >= 0x7f80 || mag[1] >= 0x7f80) != 0;
   if (lane == 0) finite[r] = any_bad ? 0 : 1;
