@@ -204,16 +204,33 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
       activate8_f32(kf, true);
       activate8_f32(vf, false);
     }
+    // bf16 x bf16 products are exact in fp32: with bf16 beta, v_dot2_f32_bf16 of a packed
+    // pair against (beta, 0) or (0, beta) gives each product straight from the packed words.
+    // (The builtin becomes v_dot2c_f32_bf16, whose accumulator needs a zeroing move per
+    // product; the three-operand form takes the zero as a constant.)
+    auto times = [](uint32_t pair, uint32_t b_pair) {
+      float r;
+      asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(pair), "v"(b_pair));
+      return r;
+    };
     // The packed words are made opaque so that the values are taken back out of them (one
     // shift or mask each) rather than rounded again one by one.
     u32x4 kw = pack8(kf);  // k' (bf16)
-    asm volatile("" : "+v"(kw));
-    unpack8(kw, kf);
     const float b = __uint_as_float(kSplit == 3 ? braw : braw << 16);
-    const float b16 = round_bf16(b);
+    const uint32_t b16 = kSplit == 3 ? f32_to_bf16_bits(b) : (braw & 0xffffu);  // bf16(beta)
     float prod[8];
+    if constexpr (kSplit == 2) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) prod[i] = b * kf[i];  // exact for bf16 beta
+      for (int i = 0; i < 4; ++i) {
+        prod[2 * i] = times(kw[i], b16);              // exact
+        prod[2 * i + 1] = times(kw[i], b16 << 16);
+      }
+    } else {
+      asm volatile("" : "+v"(kw));
+      unpack8(kw, kf);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) prod[i] = b * kf[i];
+    }
     u32x4 hw = pack8(prod);                             // hi = bf16(prod)
     asm volatile("" : "+v"(hw));
     float hi[8];
@@ -234,11 +251,12 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
       *reinterpret_cast<u32x4*>(row + 2 * kTile) = mw;
       *reinterpret_cast<u32x4*>(row + 3 * kTile) = pack8(prod);
     }
-    u32x4 vw = pack8(vf);  // v' (bf16)
-    asm volatile("" : "+v"(vw));
-    unpack8(vw, vf);
+    const u32x4 vw = pack8(vf);  // v' (bf16)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) vf[i] *= b16;
+    for (int i = 0; i < 4; ++i) {
+      vf[2 * i] = times(vw[i], b16);                    // exact
+      vf[2 * i + 1] = times(vw[i], b16 << 16);
+    }
     *reinterpret_cast<u32x4*>(row + (1 + kSplit) * kTile) = pack8(vf);  // bf16(v'·bf16(beta))
   };
 
@@ -982,23 +1000,29 @@ __device__ __forceinline__ void rows_times_tokens(const uint16_t* m, const bf16x
 
 // The global operands of one 16-token group in this lane: q channels 32 ks + 8 g .. +8 and,
 // for a read gate, gate channels 32 j + 8 g .. +8, or, for a formed gate, the same channels
-// of the token's down-projection row (its B operands). Zero for tokens past the frame.
+// of the token's down-projection row (its B operands). A token past the frame reads the
+// frame's last token instead: every value of a token stays in its own lanes (the B column of
+// its MFMAs and the four lanes of its sums and maxima), and nothing of it is stored.
 struct RoLoads {
   u32x4 q[4];
   u32x4 gt[4];
 };
 
-template <bool kProj>
-__device__ __forceinline__ void ro_load(const View& qv, const View& gv, const GateProj& gp,
-                                        int f, int h, int s, bool valid, int64_t row0, int g,
-                                        RoLoads& L) {
-  const uint16_t* qrow = qv.at(f, h, s) + g * 8;
-  const uint16_t* grow =
-      kProj ? gp.down + (row0 + s) * gp.d_st + g * 8 : gv.at(f, h, s) + g * 8;
+// Per-lane row bases of one (frame, head): q and gate rows of token s are at q0 + s * qs and
+// g0 + s * gs (elements).
+struct RoRows {
+  const uint16_t* q0;
+  const uint16_t* g0;
+  int64_t qs, gs;
+};
+
+__device__ __forceinline__ void ro_load(const RoRows& rows, int s, RoLoads& L) {
+  const uint16_t* qrow = rows.q0 + s * rows.qs;
+  const uint16_t* grow = rows.g0 + s * rows.gs;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    L.q[j] = valid ? *reinterpret_cast<const u32x4*>(qrow + j * 32) : u32x4{0u, 0u, 0u, 0u};
-    L.gt[j] = valid ? *reinterpret_cast<const u32x4*>(grow + j * 32) : u32x4{0u, 0u, 0u, 0u};
+    L.q[j] = *reinterpret_cast<const u32x4*>(qrow + j * 32);
+    L.gt[j] = *reinterpret_cast<const u32x4*>(grow + j * 32);
   }
 }
 
@@ -1045,9 +1069,11 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
   const int g_end = min(groups, (part + 1) * per);
   const int64_t row0 = static_cast<int64_t>(f) * spatial;
   int grp = part * per + wave;
+  const RoRows rows{qv.at(f, h, 0) + g * 8,
+                    kProj ? gp.down + row0 * gp.d_st + g * 8 : gv.at(f, h, 0) + g * 8, qv.ss,
+                    kProj ? gp.d_st : gv.ss};
   RoLoads cur;
-  if (grp < g_end)
-    ro_load<kProj>(qv, gv, gp, f, h, grp * 16 + t16, grp * 16 + t16 < spatial, row0, g, cur);
+  if (grp < g_end) ro_load(rows, min(grp * 16 + t16, spatial - 1), cur);
   for (; grp < g_end; grp += kRoWaves) {
     const int s = grp * 16 + t16;
     const bool valid = s < spatial;
@@ -1178,9 +1204,7 @@ vda_readout_kernel(View qv, int activate_q, const uint16_t* __restrict__ state,
     }
     // the next group's loads (a copy into a second register set held across the MFMAs
     // would not fit the 128-VGPR budget)
-    if (grp + kRoWaves < g_end)
-      ro_load<kProj>(qv, gv, gp, f, h, s + 16 * kRoWaves, s + 16 * kRoWaves < spatial, row0, g,
-                     cur);
+    if (grp + kRoWaves < g_end) ro_load(rows, min(s + 16 * kRoWaves, spatial - 1), cur);
   }
 }
 
