@@ -116,10 +116,13 @@ def work(name, a, plans):
     return 0.0, 0.0
 
 
-def aggregate(timer, plans):
-    """name -> [launches, ms, flop, bytes] over the timer's records."""
+def aggregate(timer, plans, stream=None):
+    """name -> [launches, ms, flop, bytes] over the timer's records (those on `stream`, a
+    stream handle, if given)."""
     per = {}
-    for name, a, t in timer.durations():
+    for name, a, t, handle in timer.durations():
+        if stream is not None and handle != stream:
+            continue
         flop, nbytes = work(name, a, plans)
         e = per.setdefault(name, [0, 0.0, 0.0, 0.0])
         e[0] += 1
@@ -172,7 +175,7 @@ def short_conv_prepare(cfg, device, frames, steps):
         for _ in range(steps):
             run()
         torch.cuda.synchronize()
-    times = [t for _, _, t in timer.durations()]
+    times = [t for _, _, t, _ in timer.durations()]
     ms = sum(times) / len(times)
     nbytes = 2 * tokens * hd * 2
     log(f"short-conv prepare: {ms:.3f} ms per projection")
@@ -252,7 +255,7 @@ def production_geometry(steps):
                 run()
             torch.cuda.synchronize()
     per = {}
-    for name, _, t in timer.durations():
+    for name, _, t, _ in timer.durations():
         per[name] = per.get(name, 0.0) + t / steps
     attn = sum(per.get(n, 0.0) for n in ATTENTION)
     vda = sum(t for n, t in per.items() if n not in ATTENTION)
@@ -300,7 +303,9 @@ def h3_block(steps, plans_of):
             end.record()
             torch.cuda.synchronize()
     ms = start.elapsed_time(end) / steps
-    per = aggregate(timer, plans)
+    # the projections on the caller's stream (the two context projections run on the side
+    # stream, where an event pair also spans their wait for the attention's CUs)
+    per = aggregate(timer, plans, torch.cuda.current_stream().cuda_stream)
     g = [sum(per[nm][i] for nm in GEMMS if nm in per) for i in range(4)]
     log(f"H3 widths: {ms:.2f} ms per block")
     return {"workload": f"block at hidden {cfg.hidden}, {cfg.heads}x{cfg.head_dim} heads, SwiGLU FFN "
@@ -314,7 +319,7 @@ def h3_block(steps, plans_of):
 
 
 def _launch_ms(timer, name):
-    times = [t for n, _, t in timer.durations() if n == name]
+    times = [t for n, _, t, _ in timer.durations() if n == name]
     return sum(times) / len(times) if times else float("nan")
 
 
@@ -480,7 +485,7 @@ def c1_vda(steps):
             for _ in range(reps):
                 run()
             torch.cuda.synchronize()
-        kernel_ms = sum(t for _, _, t in timer.durations()) / reps
+        kernel_ms = sum(t for _, _, t, _ in timer.durations()) / reps
         launches = len(timer.durations()) // reps
     gpu_ms = start.elapsed_time(end) / reps
     threads = host_threads()
@@ -902,13 +907,16 @@ def main():
     # The per-kernel breakdown comes from separate instrumented steps (an event pair around
     # every launch). idle_ms = a step's wall time minus the sum of its caller-stream launch
     # times: what the caller's stream spends waiting (on the host, or on the side stream).
+    # A side-stream entry's time in the breakdown is a wall time: its event pair also spans
+    # the time the launch waits for the CUs the caller's stream holds.
     names = set(_lib.SIGNATURES)
     b_steps = max(args.breakdown_steps, 1)
+    caller = torch.cuda.current_stream().cuda_stream
     with _lib.LaunchTimer(names) as timer:
         inst_ms, _ = timed_steps(step, b_steps)
     per = aggregate(timer, plans)
     breakdown = breakdown_of(per, b_steps)
-    main_launch_ms = sum(per[nm][1] for nm in per if nm not in VDA_ENTRIES) / b_steps
+    main_launch_ms = sum(v[1] for v in aggregate(timer, plans, caller).values()) / b_steps
     idle = {"ms": round(ms - main_launch_ms, 3),
             "instrumented_ms": round(statistics.median(inst_ms) - main_launch_ms, 3),
             "caller_stream_launch_ms": round(main_launch_ms, 3),
@@ -916,9 +924,6 @@ def main():
             "steps": b_steps}
     log(f"instrumented {b_steps} steps: caller-stream launches {main_launch_ms:.2f} ms, "
         f"idle {idle['ms']:.3f} ms per block")
-    g = [sum(per[nm][i] for nm in GEMMS if nm in per) for i in range(4)]
-    gemm_tflops = g[2] / (g[1] * 1e-3) / 1e12
-
     # The branch kernels again, one stream, no overlap: the VDA passes share the GPU with the
     # window attention in the timed steps above, so their launch times there are wall times
     # under contention. These steps give each branch kernel's own launch time.
@@ -927,7 +932,7 @@ def main():
     if iso_steps > 0:
         block.overlap_vda = False
         serial_ms = statistics.median(timed_steps(step, iso_steps)[0])
-        with _lib.LaunchTimer(set(VDA_ENTRIES) | set(ATTENTION)) as iso_timer:
+        with _lib.LaunchTimer(set(VDA_ENTRIES) | set(ATTENTION) | set(GEMMS)) as iso_timer:
             timed_steps(step, iso_steps)
         block.overlap_vda = True
         iso = aggregate(iso_timer, plans)
@@ -935,6 +940,11 @@ def main():
             f"side stream: {serial_ms:.2f} ms")
     else:   # only the overlapped times exist
         iso, iso_steps = per, b_steps
+    # The GEMM family from the steps without the side stream: there every projection launches
+    # on the caller's stream and runs alone (in the overlapped block the two context
+    # projections queue on the side stream behind the attention's workgroups).
+    g = [sum(iso[nm][i] for nm in GEMMS if nm in iso) for i in range(4)]
+    gemm_tflops = g[2] / (g[1] * 1e-3) / 1e12
     vda_t = sum(iso[n][1] for n in VDA_ENTRIES if n in iso)
     vda_bytes = sum(iso[n][3] for n in VDA_ENTRIES if n in iso)
     vda_gbs = vda_bytes / (vda_t * 1e-3) / 1e9
@@ -974,6 +984,11 @@ def main():
                    "head_dim": cfg.head_dim, "ffn": cfg.ffn, "context": ctx.shape[0],
                    "parallelism": "single GPU"},
         "roofline": {"kernel": "mxfp8_gemm_persistent_kernel / mxfp8_gemm_kernel (all block "
+                               "projections: vdn_mxfp8_gemm and the FFN-up "
+                               "vdn_mxfp8_gemm_act_quantize; launch times from the block "
+                               "steps without the side stream)" if iso_steps and
+                               args.isolated_steps > 0 else
+                               "mxfp8_gemm_persistent_kernel / mxfp8_gemm_kernel (all block "
                                "projections: vdn_mxfp8_gemm and the FFN-up "
                                "vdn_mxfp8_gemm_act_quantize)", "bound": "mfma",
                      "achieved": round(gemm_tflops, 1), "peak": PEAK_MXFP8_TFLOPS,

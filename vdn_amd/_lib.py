@@ -101,7 +101,8 @@ def exported_symbols() -> list[str]:
 class LaunchTimer:
     """Records a pair of timing events around every call of the named entry points while
     active (`with LaunchTimer({...}) as t:`). The events go on the caller's current stream,
-    the stream every entry point launches on, so each pair brackets that launch."""
+    the stream every entry point launches on, so each pair brackets that launch; the stream's
+    handle is kept with them."""
 
     def __init__(self, names):
         self.names = set(names)
@@ -115,9 +116,9 @@ class LaunchTimer:
         _TIMERS.remove(self)
 
     def durations(self):
-        """[(name, args, milliseconds)] after synchronising the device."""
+        """[(name, args, milliseconds, stream handle)] after synchronising the device."""
         torch.cuda.synchronize()
-        return [(n, a, s.elapsed_time(e)) for n, a, s, e in self.records]
+        return [(n, a, s.elapsed_time(e), h) for n, a, s, e, h in self.records]
 
 
 _TIMERS: list[LaunchTimer] = []
@@ -135,8 +136,9 @@ def call(name: str, *args) -> None:
     if timers:
         end = torch.cuda.Event(enable_timing=True)
         end.record()
+        handle = torch.cuda.current_stream().cuda_stream
         for t in timers:
-            t.records.append((name, args, start, end))
+            t.records.append((name, args, start, end, handle))
 
 
 def ptr(t: torch.Tensor | None) -> int | None:
