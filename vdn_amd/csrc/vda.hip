@@ -27,6 +27,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 namespace vdn {
 namespace {
@@ -204,33 +205,16 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
       activate8_f32(kf, true);
       activate8_f32(vf, false);
     }
-    // bf16 x bf16 products are exact in fp32: with bf16 beta, v_dot2_f32_bf16 of a packed
-    // pair against (beta, 0) or (0, beta) gives each product straight from the packed words.
-    // (The builtin becomes v_dot2c_f32_bf16, whose accumulator needs a zeroing move per
-    // product; the three-operand form takes the zero as a constant.)
-    auto times = [](uint32_t pair, uint32_t b_pair) {
-      float r;
-      asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(pair), "v"(b_pair));
-      return r;
-    };
     // The packed words are made opaque so that the values are taken back out of them (one
     // shift or mask each) rather than rounded again one by one.
     u32x4 kw = pack8(kf);  // k' (bf16)
+    asm volatile("" : "+v"(kw));
+    unpack8(kw, kf);
     const float b = __uint_as_float(kSplit == 3 ? braw : braw << 16);
-    const uint32_t b16 = kSplit == 3 ? f32_to_bf16_bits(b) : (braw & 0xffffu);  // bf16(beta)
+    const float b16 = round_bf16(b);
     float prod[8];
-    if constexpr (kSplit == 2) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        prod[2 * i] = times(kw[i], b16);              // exact
-        prod[2 * i + 1] = times(kw[i], b16 << 16);
-      }
-    } else {
-      asm volatile("" : "+v"(kw));
-      unpack8(kw, kf);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) prod[i] = b * kf[i];
-    }
+    for (int i = 0; i < 8; ++i) prod[i] = b * kf[i];  // exact for bf16 beta
     u32x4 hw = pack8(prod);                             // hi = bf16(prod)
     asm volatile("" : "+v"(hw));
     float hi[8];
@@ -251,12 +235,11 @@ vda_statistics_kernel(View kv, View vv, const void* __restrict__ beta, int64_t b
       *reinterpret_cast<u32x4*>(row + 2 * kTile) = mw;
       *reinterpret_cast<u32x4*>(row + 3 * kTile) = pack8(prod);
     }
-    const u32x4 vw = pack8(vf);  // v' (bf16)
+    u32x4 vw = pack8(vf);  // v' (bf16)
+    asm volatile("" : "+v"(vw));
+    unpack8(vw, vf);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      vf[2 * i] = times(vw[i], b16);                    // exact
-      vf[2 * i + 1] = times(vw[i], b16 << 16);
-    }
+    for (int i = 0; i < 8; ++i) vf[i] *= b16;
     *reinterpret_cast<u32x4*>(row + (1 + kSplit) * kTile) = pack8(vf);  // bf16(v'·bf16(beta))
   };
 
@@ -628,7 +611,7 @@ vda_recur_kernel(const float* __restrict__ Tm, const float* __restrict__ Jm, int
 #pragma unroll
     for (int v = 0; v < 4; ++v) jcur[v] = jnext[v];
   }
-  if (kMode == kCompose) {
+  if constexpr (kMode == kCompose) {
     __syncthreads();
     const int64_t o = ((static_cast<int64_t>(dir) * chunks + c) * heads + h) * mat;
     for (int idx = tid; idx < 16 * kD; idx += kRecThreads) {
@@ -749,23 +732,32 @@ vda_conv_prepare_kernel(const uint16_t* __restrict__ tokens, int64_t row_stride,
   };
 
   const int by = wave >> 1, bx = wave & 1;
-  // spatial outputs (bf16 channel pairs) of frames t - 4 .. t, oldest first
+  // Byte offsets of the lane's 16 output words in a (frame, head) slice of `out` (32-bit: a
+  // slice spans spatial * 256 bytes); a position outside the frame gets an offset past the
+  // slice, where the buffer store is dropped.
+  uint32_t out_off[16];
+#pragma unroll
+  for (int p = 0; p < 16; ++p) {
+    const int yy = ty * kCvTile + by * 4 + (p >> 2), xx = tx * kCvTile + bx * 4 + (p & 3);
+    out_off[p] = yy < fh && xx < fw
+                     ? static_cast<uint32_t>(((yy * fw + xx) * kD + 2 * lane) * 2)
+                     : 0x80000000u;
+  }
+  // spatial outputs (bf16 channel pairs) of the last five frames, frame t in slot t % 5
   uint32_t win[5][16];
 #pragma unroll
   for (int k = 0; k < 5; ++k)
 #pragma unroll
     for (int p = 0; p < 16; ++p) win[k][p] = 0u;
 
-  if (frames > 0) dma_frame(0, 0);
-  for (int t = 0; t < frames + 2; ++t) {
+  // Frame t's spatial output goes to slot t % 5 of win; the frame loop is unrolled five
+  // times so that every slot index is a constant (no register rotation per frame).
+  auto step = [&](int t, auto phase_tag) __attribute__((always_inline)) {
+    constexpr int P = decltype(phase_tag)::value;   // t % 5
     const int buf = t & 1;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();   // frame t is in LDS; every wave is done with frame t - 1's buffer
     if (t + 1 < frames) dma_frame(t + 1, buf ^ 1);
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-#pragma unroll
-      for (int p = 0; p < 16; ++p) win[k][p] = win[k + 1][p];
     if (t < frames) {
       float acc[4][4][2];
 #pragma unroll
@@ -810,12 +802,12 @@ vda_conv_prepare_kernel(const uint16_t* __restrict__ tokens, int64_t row_stride,
 #pragma unroll
       for (int oy = 0; oy < 4; ++oy)
 #pragma unroll
-        for (int ox = 0; ox < 4; ++ox) win[4][oy * 4 + ox] = pack_bf16x2(acc[oy][ox][0], acc[oy][ox][1]);
+        for (int ox = 0; ox < 4; ++ox) win[P][oy * 4 + ox] = pack_bf16x2(acc[oy][ox][0], acc[oy][ox][1]);
     } else {
 #pragma unroll
-      for (int p = 0; p < 16; ++p) win[4][p] = 0u;
+      for (int p = 0; p < 16; ++p) win[P][p] = 0u;
     }
-    if (t < 2) continue;
+    if (t < 2) return;
     // ---- frame o = t - 2: temporal taps, SiLU, L2, store ----
     const int o = t - 2;
     uint16_t* out_f = out + (static_cast<int64_t>(o) * heads + h) * spatial * kD;
@@ -825,9 +817,9 @@ vda_conv_prepare_kernel(const uint16_t* __restrict__ tokens, int64_t row_stride,
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         // frames o .. o + 4 in pairs (o, o + 1), (o + 2, o + 3), then o + 4
-        float a = dot2(pair(win[0][p], win[1][p], c), wtm2[c][0], 0.f);
-        a = dot2(pair(win[2][p], win[3][p], c), wtm2[c][1], a);
-        a = __builtin_fmaf(chan(win[4][p], c), wtm4[c], a);
+        float a = dot2(pair(win[(P + 1) % 5][p], win[(P + 2) % 5][p], c), wtm2[c][0], 0.f);
+        a = dot2(pair(win[(P + 3) % 5][p], win[(P + 4) % 5][p], c), wtm2[c][1], a);
+        a = __builtin_fmaf(chan(win[P][p], c), wtm4[c], a);
         y[p][c] = silu(a);
       }
     if (l2norm) {
@@ -845,17 +837,23 @@ vda_conv_prepare_kernel(const uint16_t* __restrict__ tokens, int64_t row_stride,
         y[p][1] *= inv;
       }
     }
+    const __amdgpu_buffer_rsrc_t orsrc =
+        __builtin_amdgcn_make_buffer_rsrc(out_f, 0, spatial * kD * 2, 0x00020000);
 #pragma unroll
-    for (int p = 0; p < 16; ++p) {
-      const int yy = ty * kCvTile + by * 4 + (p >> 2), xx = tx * kCvTile + bx * 4 + (p & 3);
-      if (yy < fh && xx < fw) {
-        // a 32-bit offset from the frame's base (a frame spans < 2 GiB), made opaque so the
-        // 16 offsets are not kept as 64-bit values across the frame loop
-        uint32_t off = static_cast<uint32_t>((yy * fw + xx) * kD + 2 * lane);
-        asm volatile("" : "+v"(off));
-        *reinterpret_cast<uint32_t*>(out_f + off) = pack_bf16x2(y[p][0], y[p][1]);
-      }
-    }
+    for (int p = 0; p < 16; ++p)
+      __builtin_amdgcn_raw_buffer_store_b32(pack_bf16x2(y[p][0], y[p][1]), orsrc, out_off[p], 0, 0);
+  };
+  if (frames > 0) dma_frame(0, 0);
+  for (int t0 = 0; t0 < frames + 2; t0 += 5) {
+    step(t0, std::integral_constant<int, 0>{});
+    if (t0 + 1 >= frames + 2) break;
+    step(t0 + 1, std::integral_constant<int, 1>{});
+    if (t0 + 2 >= frames + 2) break;
+    step(t0 + 2, std::integral_constant<int, 2>{});
+    if (t0 + 3 >= frames + 2) break;
+    step(t0 + 3, std::integral_constant<int, 3>{});
+    if (t0 + 4 >= frames + 2) break;
+    step(t0 + 4, std::integral_constant<int, 4>{});
   }
 }
 
