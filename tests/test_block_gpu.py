@@ -142,6 +142,36 @@ def test_block_is_deterministic_and_leaves_its_input_alone():
     assert torch.isfinite(a.float()).all()
 
 
+def test_side_stream_schedule_matches_serial_over_chained_blocks():
+    """The overlapped schedule (gate projection, VDA branch and context projections on a side
+    stream) and the serial one give the same bytes over four chained blocks launched back to
+    back with no host sync between them, so the caching allocator hands memory freed on one
+    stream to the other while earlier blocks are still running."""
+    cfg = WIDE
+    w = BlockWeights.random(cfg, 7, device="cuda")
+    block = HybridDiTBlock(cfg, w)
+    hidden, temb, ctx, layout, rope = make_inputs(cfg, 3, 4, 8, 6, device="cuda")
+    plan = vw.prepare_paper_window_plan(layout, vw.window_bounds(3, 1), device="cuda")
+    cplan = cross_attention_plan(hidden.shape[0], ctx.shape[0], "cuda")
+
+    def chain(overlap):
+        block.overlap_vda = overlap
+        h = hidden
+        for _ in range(4):
+            h = block(h, temb, ctx, layout, rope, plan, cplan)
+        torch.cuda.synchronize()
+        return h
+
+    try:
+        with torch.no_grad():
+            first, serial, again = chain(True), chain(False), chain(True)
+    finally:
+        block.overlap_vda = True
+    assert torch.equal(first, serial)
+    assert torch.equal(first, again)
+    assert torch.isfinite(first.float()).all()
+
+
 def test_fused_mxfp8_epilogues_give_the_unfused_block():
     """The block's default path quantizes the attention, VDA and cross-attention outputs in
     their kernels; return_parts keeps them in bf16 and quantizes them separately. Both feed
