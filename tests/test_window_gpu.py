@@ -40,6 +40,38 @@ def test_dense_fp32_oracle(device, before, after, frames, chunk, radius, anchor)
     assert out.is_contiguous() and out.data_ptr() != backing.data_ptr()
 
 
+@pytest.mark.parametrize("growth", [1.0, -1.0])
+@torch.no_grad()
+def test_large_scores_lazy_rescale(device, growth):
+    """Scores of up to several hundred (log2 units) whose per-tile maximum grows (or shrinks)
+    from one key tile to the next: the running maximum is raised many times past the lazy
+    threshold (8) and every raise rescales the accumulators. Dense fp32 oracle at the
+    reference test's tolerances; the log-sum-exp at a tolerance relative to its size."""
+    torch.manual_seed(77)
+    frames, spatial = 3, 300
+    layout = vw.SequenceLayout(frames * spatial, 0, frames, spatial)
+    bounds = vw.window_bounds(frames, 1)
+    n = layout.seq_len
+    q = torch.randn(n, 2, 128) * 8
+    # key magnitude ramps over the sequence, so each 128-key tile's maximum differs from the
+    # previous one by far more than the threshold
+    ramp = torch.linspace(1.0, 6.0, n)
+    if growth < 0:
+        ramp = ramp.flip(0)
+    k = torch.randn(n, 2, 128) * ramp[:, None, None]
+    v = torch.randn(n, 2, 128)
+    q, k, v = (t.to(device=device, dtype=torch.bfloat16) for t in (q, k, v))
+    plan = vw.prepare_paper_window_plan(layout, bounds, device=device)
+    out, lse = vw.paper_window_attention(q, k, v, plan, enabled=True, return_lse=True)
+    mask = ow.dense_mask(n, 0, frames, spatial, bounds, "none")
+    expected, el = ow.attention_dense(q.cpu(), k.cpu(), v.cpu(), mask, 128 ** -.5)
+    assert el.abs().max() > 100, "the scores must span far more than the lazy threshold"
+    got = out.float().cpu()
+    assert torch.isfinite(got).all() and torch.isfinite(lse).all()
+    torch.testing.assert_close(got, expected, atol=.009, rtol=.015)
+    torch.testing.assert_close(lse.cpu(), el, atol=3e-5, rtol=3e-6)
+
+
 @pytest.mark.parametrize("spatial", [300, 470])
 @torch.no_grad()
 def test_partial_last_query_block(device, spatial):
