@@ -355,9 +355,11 @@ class HybridDiTBlock(nn.Module):
         main = torch.cuda.current_stream(dev)
         side = self._side_stream(dev) if (self.overlap_vda and parts is None) else None
 
-        def gates():
+        def gates(ready=None):
             soft_gate, beta, gate_down, partial = gate_projection(
                 x1, self.gate_w, k["soft_gate_b"], heads, frames, spatial)
+            if ready is not None:   # the softmax gate exists: the attention may start
+                ready.record()
             # the low-rank gate sigmoid(up(down(x1))) is formed inside the VDA readout
             lin_gate = vv.OutputGateProjection(gate_down, k["lgate_up_w"], k["lgate_up_b"])
             alpha = frame_alpha(partial, frames, spatial, k["alpha_up_w"], k["dt_bias"],
@@ -377,10 +379,9 @@ class HybridDiTBlock(nn.Module):
             # The gate projection (x1 only) runs on the side stream beside the QK norm + RoPE
             # pass; the window attention waits for its softmax gate through an event.
             side.wait_stream(main)
+            gate_ready = torch.cuda.Event()
             with torch.cuda.stream(side):
-                soft_gate, beta, lin_gate, alpha = gates()
-                gate_ready = torch.cuda.Event()
-                gate_ready.record(side)
+                soft_gate, beta, lin_gate, alpha = gates(gate_ready)
         else:
             soft_gate, beta, lin_gate, alpha = gates()
         # The two branch outputs are the two halves of the [O | O_lin] operand. The kernels
