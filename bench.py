@@ -578,7 +578,7 @@ def visible_pairs(frames, spatial, radius):
 
 def host_threads():
     """Host cores this process may run on (its CPU affinity; os.cpu_count() counts the
-    whole machine, which a GPU box shares among its GPUs)."""
+    whole machine, which a host with several GPUs shares among them)."""
     try:
         return len(os.sched_getaffinity(0))
     except AttributeError:
@@ -771,14 +771,18 @@ def summarize_traffic(fetch_csv, write_csv, command=""):
                      "    python3 bench.py --summarize-traffic "
                      f"{fetch_csv} {write_csv}", ""]
     else:
+        # the profiler's output directory and file prefix of each pass, read back from the
+        # CSV paths (<dir>/<prefix>_counter_collection.csv)
+        def pass_args(csv_path):
+            prefix = os.path.basename(csv_path).split("_counter_collection")[0]
+            return f"-d {os.path.dirname(csv_path) or '.'} -o {prefix}"
         cmd_lines = [
             "Commands (from the repository root, on one MI355X; one block forward, no warmup):", "",
-            "    rocprofv3 --pmc FETCH_SIZE -d gpurun_out/pmc_fetch -o f --output-format csv -- "
+            f"    rocprofv3 --pmc FETCH_SIZE {pass_args(fetch_csv)} --output-format csv -- "
             "python3 bench.py --steps 1 --warmup 0 --isolated-steps 0 --no-cpu-baseline --calibrate-copy",
-            "    rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_write -o w --output-format csv -- "
+            f"    rocprofv3 --pmc WRITE_SIZE {pass_args(write_csv)} --output-format csv -- "
             "python3 bench.py --steps 1 --warmup 0 --isolated-steps 0 --no-cpu-baseline --calibrate-copy",
-            "    python3 bench.py --summarize-traffic gpurun_out/pmc_fetch/f_counter_collection.csv "
-            "gpurun_out/pmc_write/w_counter_collection.csv", ""]
+            f"    python3 bench.py --summarize-traffic {fetch_csv} {write_csv}", ""]
     out = ["# HBM traffic per MXFP8 GEMM launch, hybrid DiT block at 108,000 tokens", "",
            *cmd_lines,
            "Calibration: `torch.neg` over 2^29 bf16 values (1 GiB read, 1 GiB written) reads "
@@ -864,7 +868,7 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the block runs whole on a single MI355X "
-              "(no sharding in this build); run with --gpus 1", file=sys.stderr)
+              "(no sharding is implemented); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch
