@@ -62,9 +62,9 @@ gate_projection_kernel(const uint16_t* __restrict__ x, int64_t x_st, int k,
                        const uint16_t* __restrict__ gate_bias, uint16_t* __restrict__ soft_gate,
                        uint16_t* __restrict__ beta, uint16_t* __restrict__ gate_down,
                        float* __restrict__ partial) {
-  // Two rings of LDS stages: 8 of x1 (its HBM stream needs many bytes in flight) and 3 of W
-  // (read by every workgroup, mostly from L2). After the K loop the W ring stages the
-  // outputs: softmax gate [128][64], beta [128][64], down [128][128] bf16.
+  // Two rings of LDS stages: kARing (6) of x1 (its HBM stream needs many bytes in flight)
+  // and kWRing (4) of W (read by every workgroup, mostly from L2). After the K loop the W
+  // ring stages the outputs: softmax gate [128][64], beta [128][64], down [128][128] bf16.
   __shared__ __attribute__((aligned(1024))) uint16_t sA[kARing * kGRows * kGK];
   __shared__ __attribute__((aligned(1024))) uint16_t sW[kWRing * kGCols * kGK];
   __shared__ float s_alpha[2][kGRank];

@@ -655,7 +655,18 @@ __device__ __forceinline__ void cv_buffer_to_lds16(__amdgpu_buffer_rsrc_t r, uin
 }
 
 // Sum over the 64 lanes of a wave (every lane gets the same bits).
-__device__ __forceinline__ float wave_sum(float x) { return sum_quad_rows(sum16(x)); }
+// Total over the wave, the same bits in every lane: the 16-lane row sums r0..r3 (sum16),
+// then DPP row_bcast:15 (each row adds lane 15 of the row below it) and row_bcast:31 (rows 2
+// and 3 add lane 31). Lane 63 then holds (r3 + r2) + (r1 + r0): row 3 added lane 47 (r2)
+// and then lane 31 (r1 + r0, row 1 having added lane 15). v_readlane makes it wave-uniform;
+// the other lanes' partial sums are never read. The same sum as sum_quad_rows(sum16(x))
+// (addition commutes), without the register copies that the permlane swaps need.
+__device__ __forceinline__ float wave_sum(float x) {
+  x = sum16(x);
+  x += dpp_f32<0x142>(x);
+  x += dpp_f32<0x143>(x);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 vda_conv_prepare_kernel(const uint16_t* __restrict__ tokens, int64_t row_stride,
@@ -759,11 +770,7 @@ vda_conv_prepare_kernel(const uint16_t* __restrict__ tokens, int64_t row_stride,
     __syncthreads();   // frame t is in LDS; every wave is done with frame t - 1's buffer
     if (t + 1 < frames) dma_frame(t + 1, buf ^ 1);
     if (t < frames) {
-      float acc[4][4][2];
-#pragma unroll
-      for (int oy = 0; oy < 4; ++oy)
-#pragma unroll
-        for (int ox = 0; ox < 4; ++ox) acc[oy][ox][0] = acc[oy][ox][1] = 0.f;
+      float acc[4][4][2];   // set by each output's first tap row (i == 0)
       const uint8_t* src = &lds[buf][((by * 4) * kCvHalo + bx * 4) * 256 + lane * 4];
 #pragma unroll
       for (int ir = 0; ir < 8; ++ir) {
@@ -793,9 +800,17 @@ vda_conv_prepare_kernel(const uint16_t* __restrict__ tokens, int64_t row_stride,
           for (int c = 0; c < 2; ++c)
 #pragma unroll
             for (int ox = 0; ox < 4; ++ox) {
-              float a = dot2(xp[c][ox], wsp2[c][i][0], acc[oy][ox][c]);
-              a = dot2(xp[c][ox + 2], wsp2[c][i][1], a);
-              acc[oy][ox][c] = __builtin_fmaf(x4[c][ox], wsp4[c][i], a);
+              if (i == 0) {
+                // the first row starts the sum with its tap-4 product (exact in fp32: two
+                // bf16 factors), so no dot starts from a zeroed register
+                float a = x4[c][ox] * wsp4[c][i];
+                a = dot2(xp[c][ox], wsp2[c][i][0], a);
+                acc[oy][ox][c] = dot2(xp[c][ox + 2], wsp2[c][i][1], a);
+              } else {
+                float a = dot2(xp[c][ox], wsp2[c][i][0], acc[oy][ox][c]);
+                a = dot2(xp[c][ox + 2], wsp2[c][i][1], a);
+                acc[oy][ox][c] = __builtin_fmaf(x4[c][ox], wsp4[c][i], a);
+              }
             }
         }
       }
@@ -816,10 +831,11 @@ vda_conv_prepare_kernel(const uint16_t* __restrict__ tokens, int64_t row_stride,
     for (int p = 0; p < 16; ++p)
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        // frames o .. o + 4 in pairs (o, o + 1), (o + 2, o + 3), then o + 4
-        float a = dot2(pair(win[(P + 1) % 5][p], win[(P + 2) % 5][p], c), wtm2[c][0], 0.f);
+        // frame o + 4's product (exact in fp32), then frames o .. o + 3 in pairs (o, o + 1),
+        // (o + 2, o + 3)
+        float a = chan(win[P][p], c) * wtm4[c];
+        a = dot2(pair(win[(P + 1) % 5][p], win[(P + 2) % 5][p], c), wtm2[c][0], a);
         a = dot2(pair(win[(P + 3) % 5][p], win[(P + 4) % 5][p], c), wtm2[c][1], a);
-        a = __builtin_fmaf(chan(win[P][p], c), wtm4[c], a);
         y[p][c] = silu(a);
       }
     if (l2norm) {
