@@ -627,7 +627,11 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
   // bf16(a * that), quantizes and stores output chunk j. Bias is interleaved the same way.
   constexpr bool swiglu = kMode == 3;
   float* pass_slot = reinterpret_cast<float*>(lds + 2 * kPStep) + (wm * 64 + lane) * 32;
-  auto epilogue_direct = [&](int64_t m0, int64_t n0) __attribute__((always_inline)) {
+  // kGelu (compile time) applies GELU-tanh: with a runtime test of the activation inside the
+  // unrolled value loop, the compiler branched around every pair's GELU, so the exp2 and
+  // reciprocal latencies of neighbouring pairs could not overlap.
+  auto epilogue_direct = [&](int64_t m0, int64_t n0, auto gelu_tag) __attribute__((always_inline)) {
+    constexpr bool kGelu = decltype(gelu_tag)::value;
     const int64_t col0 = n0 + wn * 128 + c_lo * 4;       // + 16 nt (physical columns)
     const int64_t rows0 = m0 + wm * 128 + frag_row;      // + 16 mt
     // the output columns of the lane: physical for GELU / none, block j of a for SwiGLU
@@ -734,7 +738,7 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
           for (int v = 0; v < 4; v += 2) {
             float a = y[nt][v] + bias4[nt][v], b = y[nt][v + 1] + bias4[nt][v + 1];
             round_bf16_pair(a, b);
-            if (ep.act == 1) {
+            if constexpr (kGelu) {
               a = gelu_tanh(a);
               b = gelu_tanh(b);
               round_bf16_pair(a, b);
@@ -1007,10 +1011,17 @@ mxfp8_gemm_persistent_kernel(const uint8_t* __restrict__ A, const uint8_t* __res
     int tm, tn;
     tile_coords(static_cast<int>(blockIdx.x) + c_tile * grid, num_wg, tiles_m, tiles_n, group_m,
                 tm, tn);
-    if constexpr (kMode >= 2)
-      epilogue_direct(static_cast<int64_t>(tm) * kPTile, static_cast<int64_t>(tn) * kPTile);
-    else
-      epilogue_staged(static_cast<int64_t>(tm) * kPTile, static_cast<int64_t>(tn) * kPTile);
+    const int64_t m0 = static_cast<int64_t>(tm) * kPTile, n0 = static_cast<int64_t>(tn) * kPTile;
+    if constexpr (kMode == 2) {
+      if (ep.act == 1)
+        epilogue_direct(m0, n0, std::true_type{});
+      else
+        epilogue_direct(m0, n0, std::false_type{});
+    } else if constexpr (kMode == 3) {
+      epilogue_direct(m0, n0, std::false_type{});
+    } else {
+      epilogue_staged(m0, n0);
+    }
   }
   // the DMAs issued past the last step must land before the workgroup's LDS is released
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
