@@ -312,10 +312,15 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
     // tile t is resident and every wave is done with the other buffer
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (t + 1 < ntiles) {
-      const int na = a0 + (t + 1) * kBN;
-      issue_tile(na, min(na + kBN, b0), kBuf == 0 ? sK1 : sK0, kBuf == 0 ? sV1 : sV0);
-    }
+    const int na = a0 + (t + 1) * kBN, nb = min(na + kBN, b0);
+    uint16_t* ndk = kBuf == 0 ? sK1 : sK0;
+    uint16_t* ndv = kBuf == 0 ? sV1 : sV0;
+    // a full next tile of a live wave goes out one segment per channel step of Sᵀ, in the
+    // shadow of that step's MFMAs
+    const bool spread = kD == 128 && t + 1 < ntiles && wave_live && nb - na == kBN;
+    if (t + 1 < ntiles && !spread) issue_tile(na, nb, ndk, ndv);
+    const __amdgpu_buffer_rsrc_t nk_rsrc = tile_rsrc(k_head + static_cast<int64_t>(na) * in.k_st * 2);
+    const __amdgpu_buffer_rsrc_t nv_rsrc = tile_rsrc(v_head + static_cast<int64_t>(na) * in.v_st * 2);
     const int a = a0 + t * kBN, b = min(a + kBN, b0);
     if (!wave_live) return;
 
@@ -344,6 +349,16 @@ window_attn_kernel(Layout in, const int* __restrict__ blocks, const int* __restr
 #pragma unroll
       for (int kt = 0; kt < kKT; ++kt) s[kt] = E::mfma(kf[ks & 1][kt], qf[ks], s[kt]);
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (kD == 128 && kD / 16 == 2 * kSegs) {
+        if (spread) {
+          const int j = ks % kSegs, seg = j * kWaves + wave;
+          if (ks < kSegs)
+            load_to_lds16(nk_rsrc, koff[j], 0, ndk + seg * kSegRows * kD);
+          else
+            load_to_lds16(nv_rsrc, voff[j], 0, ndv + seg * kSegRows * kD);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     // ---- online softmax (exp2 domain; scores scaled inside the exponent's fma) ----
     if (b - a < kBN) {  // tail tile: keys past the interval end do not exist
