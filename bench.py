@@ -953,10 +953,25 @@ def main():
             timed_steps(step, iso_steps)
         block.overlap_vda = True
         iso = aggregate(iso_timer, plans)
+        attn_timer = iso_timer
         log(f"isolated branch kernels timed over {iso_steps} steps; the block without the "
             f"side stream: {serial_ms:.2f} ms")
     else:   # only the overlapped times exist
         iso, iso_steps = per, b_steps
+        attn_timer = timer
+    # the block's two attention launches apart: the +-radius frame window and the
+    # cross-attention to the context rows (told apart by their plans)
+    attn_launches = {}
+    for label, key in (("self", plan.device_plan.intervals.data_ptr()),
+                       ("cross", cplan.intervals.data_ptr())):
+        ts = [t for nm, a, t, _ in attn_timer.durations() if nm in ATTENTION and a[11] == key]
+        if ts:
+            avg = sum(ts) / len(ts)
+            flop = 4.0 * D * cfg.heads * plans[key]
+            attn_launches[label] = {"avg_launch_ms": round(avg, 4),
+                                    "tflops": round(flop / (avg * 1e-3) / 1e12, 1),
+                                    "bf16_frac": round(flop / (avg * 1e-3) / 1e12 /
+                                                       PEAK_BF16_TFLOPS, 4)}
     # The GEMM family from the steps without the side stream: there every projection launches
     # on the caller's stream and runs alone (in the overlapped block the two context
     # projections queue on the side stream behind the attention's workgroups).
@@ -1027,6 +1042,7 @@ def main():
                                  "ms": round(hb_t / iso_steps, 3)},
         "window_attention_tflops": round(w[2] / (w[1] * 1e-3) / 1e12, 1),
         "window_attention_bf16_frac": round(w[2] / (w[1] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "window_attention_launches": attn_launches,
         "configs": configs,
         "short_conv_prepare": conv,
         "production_geometry": production,
