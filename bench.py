@@ -959,6 +959,38 @@ def main():
     else:   # only the overlapped times exist
         iso, iso_steps = per, b_steps
         attn_timer = timer
+    # the block's projections apart, told apart by their shapes: QKV (N = 3 inner), [O | O_lin]
+    # (K = 2 inner), cross-Q and cross-O (K = N = hidden, without and with the residual), the
+    # context K / V rows, FFN-up (the producer entry point) and FFN-down (K = FFN width)
+    inner = cfg.heads * cfg.head_dim
+
+    def gemm_label(nm, a):
+        if nm == "vdn_mxfp8_gemm_act_quantize":
+            return "ffn_up"
+        kp, rows, n, res = a[6], a[14], a[15], a[10] is not None
+        if rows != tokens:
+            return "context_kv"
+        if kp == padded(2 * inner):
+            return "o_cat"
+        if kp == padded(cfg.ffn):
+            return "ffn_down"
+        if n == 3 * inner:
+            return "qkv"
+        return "cross_o" if res else "cross_q"
+
+    gemm_launches = {}
+    for nm, a, t, _ in attn_timer.durations():
+        if nm in GEMMS:
+            flop, _ = work(nm, a, plans)
+            e = gemm_launches.setdefault(gemm_label(nm, a), [0, 0.0, 0.0])
+            e[0] += 1
+            e[1] += t
+            e[2] += flop
+    gemm_launches = {k: {"launches_per_step": e[0] // max(iso_steps, 1),
+                         "avg_launch_ms": round(e[1] / e[0], 4),
+                         "tflops": round(e[2] / (e[1] * 1e-3) / 1e12, 1),
+                         "mxfp8_frac": round(e[2] / (e[1] * 1e-3) / 1e12 / PEAK_MXFP8_TFLOPS, 4)}
+                     for k, e in gemm_launches.items()}
     # the block's two attention launches apart: the +-radius frame window and the
     # cross-attention to the context rows (told apart by their plans)
     attn_launches = {}
@@ -1043,6 +1075,7 @@ def main():
         "window_attention_tflops": round(w[2] / (w[1] * 1e-3) / 1e12, 1),
         "window_attention_bf16_frac": round(w[2] / (w[1] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "window_attention_launches": attn_launches,
+        "gemm_launches": gemm_launches,
         "configs": configs,
         "short_conv_prepare": conv,
         "production_geometry": production,
