@@ -656,10 +656,10 @@ __device__ __forceinline__ void cv_buffer_to_lds16(__amdgpu_buffer_rsrc_t r, uin
 
 // Sum over the 64 lanes of a wave (every lane gets the same bits).
 // Total over the wave, the same bits in every lane: the 16-lane row sums r0..r3 (sum16),
-// then DPP row_bcast:15 (each row adds lane 15 of the row below it) and row_bcast:31 (rows 2
-// and 3 add lane 31). Lane 63 then holds (r3 + r2) + (r1 + r0): row 3 added lane 47 (r2)
-// and then lane 31 (r1 + r0, row 1 having added lane 15). v_readlane makes it wave-uniform;
-// the other lanes' partial sums are never read. The same sum as sum_quad_rows(sum16(x))
+// then DPP row_bcast:15 (rows 1-3 add lane 15 of the row before them; row 0 has no source
+// row) and row_bcast:31 (rows 2 and 3 add lane 31). Lane 63 then holds (r3 + r2) + (r1 + r0):
+// row 3 added lane 47 (r2) and then lane 31 (r1 + r0, row 1 having added lane 15).
+// v_readlane makes it wave-uniform; the other lanes' partial sums are never read. The same sum as sum_quad_rows(sum16(x))
 // (addition commutes), without the register copies that the permlane swaps need.
 __device__ __forceinline__ float wave_sum(float x) {
   x = sum16(x);
