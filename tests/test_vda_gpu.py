@@ -347,7 +347,7 @@ def _conv_weights(conv, proj):
 
 
 @pytest.mark.parametrize("frames,fh,fw", [(1, 1, 1), (3, 7, 5), (5, 9, 12), (2, 16, 8),
-                                          (6, 10, 17)])
+                                          (6, 10, 17), (4, 6, 9), (9, 8, 8)])
 @pytest.mark.parametrize("l2", [False, True])
 def test_conv_prepare_against_oracle(device, frames, fh, fw, l2):
     """Fused spatial + temporal short conv, SiLU / L2, frame-major store, against the float64
@@ -357,7 +357,9 @@ def test_conv_prepare_against_oracle(device, frames, fh, fw, l2):
     kernel's fp32 spatial sum and the float64 one round to neighbouring bf16 values the
     temporal sum moves by one such step times a tap weight: that is the absolute slack,
     2^-8 * max|spatial| * max|w_tm|, and it may be used by at most 1e-4 of the outputs.
-    Frame sizes cover partial 8 x 8 tiles and a frame smaller than the 5 x 5 stencil."""
+    Frame sizes cover partial 8 x 8 tiles and a frame smaller than the 5 x 5 stencil; the
+    frame counts give every remainder of the kernel's frame loop (frames + 2 steps, unrolled
+    five times: remainders 3, 4, 0, 2, 3, 1, 1)."""
     h = 2
     conv = _sep_conv(h, ("k",), frames * 31 + fw)
     g = torch.Generator().manual_seed(fh)
